@@ -1,0 +1,205 @@
+"""Benchmark of the MI355X hot path: weighted_laplace_sum + weighted_abs_sum_full forward at the headline shape.
+
+One step = one weighted_laplace_sum forward and one weighted_abs_sum_full forward (the two ops the add_laplace and
+add_riesz / add_bump layers call) over one batch of BASELINE.json configs[3]: B=1, H=12 (P=12), N=M=16384,
+D=Dv=64, fp32, q, k, v ~ N(0,1) drawn from numpy PCG64(seed 0) in the order q, k, v, resident in HBM before timing.
+
+Prints ONE JSON line (rank 0, N=1). `value` = query-feature sums per second over the whole step (2 * P*M*D units per
+step). `roofline` is for the dominant kernel, timed with hipEvents recorded by libqlka on the kernels' own stream
+inside the timed region. `cpu_baseline` times the reference's dense PyTorch path (restated in oracle/dense.py) on the
+host CPU on a bounded query sample of the same workload.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(REPO, "quasi-linear-kernel-attention_amd")
+sys.path.insert(0, PKG)
+sys.path.insert(0, REPO)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "query-feature sums/sec (B·H·N·D) at N=16384 D=64 fp32; achieved HBM GB/s %peak"
+HBM_PEAK_GBS = 8000.0
+P, D, N, M, C = 12, 64, 16384, 16384, 64
+
+# Algorithmic bytes per (p, d, m) query-feature unit of one op call at N = M (B_scan of the hot-path survey):
+# read the key and query segments once (4 N + 4 M per (p, d)), stream v once in sorted order (4 N C), emit one fp32
+# contribution per (query, channel) (4 M C) plus out_u (4 M); divided by the M units of a (p, d) segment.
+def bscan_bytes_per_unit(n, m, c, with_u=True):
+    return 4.0 * (n + m + n * c + m * c + (m if with_u else 0)) / m
+
+
+def make_inputs(dev, seed=0):
+    rng = np.random.default_rng(np.random.PCG64(seed))
+    q = rng.standard_normal((P, D, M), dtype=np.float32)
+    k = rng.standard_normal((P, D, N), dtype=np.float32)
+    v = rng.standard_normal((P, N, C), dtype=np.float32)
+    return [torch.from_numpy(a).to(dev) for a in (q, k, v)]
+
+
+def cpu_baseline(seed=0, mq=8, reps=3):
+    """The reference's dense PyTorch path (kernels.py:73,81 restated in oracle/dense.py), torch-CPU fp32 eager, on a
+    seeded sample of mq queries per p against all N keys of the headline workload. Cost is linear in the number of
+    queries, so query-feature sums/s = 2 * P * mq * D / t (both ops)."""
+    from oracle import dense
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    rng = np.random.default_rng(np.random.PCG64(seed))
+    q = torch.from_numpy(rng.standard_normal((P, D, M), dtype=np.float32)[:, :, :mq].copy())
+    k = torch.from_numpy(rng.standard_normal((P, D, N), dtype=np.float32))
+    v = torch.from_numpy(rng.standard_normal((P, N, C), dtype=np.float32))
+
+    def step():
+        dense.dense_laplace_sum(q, k, v)
+        dense.dense_abs_sum(q, k, v)
+
+    step()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        step()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    return {"value": 2 * P * mq * D / t, "unit": "query-feature sums/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"dense torch-CPU fp32 laplace + abs sums (oracle/dense.py), P={P} D={D} N={N} C={C}, "
+                      f"{mq} queries per p (of {M}), 1 warmup + median of {reps}; "
+                      f"cpu={_cpu_model()}"}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _traffic(kernel):
+    """HBM bytes per launch of `kernel` measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, copy-calibrated),
+    committed in profiles/traffic.json; None when not measured."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); this build has no multi-GPU path "
+              "(sharding over P or over d is described in DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    from qlka import _lib
+    from weighted_abs_sum import weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    q, k, v = make_inputs(dev)
+    lib = _lib.load()
+
+    def step():
+        weighted_laplace_sum(q, k, v)
+        weighted_abs_sum_full(q, k, v, backend="cuda")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    lib.qlka_timing_enable(1)
+    lib.qlka_timing_reset()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(stop)
+    stages = {}
+    for name in ("lds_radix_sort", "merge_runs", "fill_zero", "lap_range_sums", "lap_range_scan", "lap_range_walk",
+                 "abs_range_sums", "abs_range_scan", "abs_range_walk"):
+        ms, cnt = _lib.stage_time(name)
+        if cnt:
+            stages[name] = {"ms_total": ms, "launches": cnt, "ms_per_launch": ms / cnt}
+    lib.qlka_timing_enable(0)
+
+    ms_per_step = ms_total / args.steps
+    units = P * M * D
+    value = 2 * units / (ms_per_step / 1e3)
+
+    # dominant kernel and its roofline (per-unit algorithmic bytes x units per launch / launch duration)
+    dom = max(stages, key=lambda s: stages[s]["ms_total"])
+    per_unit = bscan_bytes_per_unit(N, M, C)
+    bytes_per_launch = per_unit * units
+    if dom in ("lds_radix_sort",):   # sort: read keys, write sorted keys + perm (12 B per key)
+        bytes_per_launch = 12.0 * P * D * N
+    achieved = bytes_per_launch / (stages[dom]["ms_per_launch"] / 1e3) / 1e9
+    roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(dom),
+            "algorithmic_bytes_per_launch": bytes_per_launch}
+
+    # per-op view against the north-star target (B_scan / op time)
+    sort_ms = stages.get("lds_radix_sort", {}).get("ms_total", 0.0) / max(1, 2 * args.steps)  # 2 sorts per op call
+    op_ms = {
+        "weighted_laplace_sum": sum(stages.get(s, {}).get("ms_total", 0.0)
+                                    for s in ("lap_range_sums", "lap_range_scan", "lap_range_walk")) / args.steps
+        + 2 * sort_ms,
+        "weighted_abs_sum_full": sum(stages.get(s, {}).get("ms_total", 0.0)
+                                     for s in ("abs_range_sums", "abs_range_scan", "abs_range_walk")) / args.steps
+        + 2 * sort_ms,
+    }
+    fill = stages.get("fill_zero", {}).get("ms_total", 0.0) / args.steps / 2
+    op_ms = {kk: vv + fill for kk, vv in op_ms.items()}
+    bscan = bytes_per_launch if dom != "lds_radix_sort" else per_unit * units
+    op_roof = {kk: round(bscan / (vv / 1e3) / 1e9 / HBM_PEAK_GBS, 4) for kk, vv in op_ms.items()}
+
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "query-feature sums/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: q, k, v ~ N(0,1) fp32 from numpy PCG64(0), resident in HBM",
+        "config": {"workload": "BASELINE configs[3] raw ops: weighted_laplace_sum + weighted_abs_sum_full forward, "
+                               "B=1 H=12 N=M=16384 D=Dv=64 fp32",
+                   "P": P, "D": D, "N": N, "M": M, "C": C, "units_per_step": 2 * units},
+        "roofline": roof,
+        "op_ms": {kk: round(vv, 4) for kk, vv in op_ms.items()},
+        "op_bscan_roofline_frac": op_roof,
+        "stages": {kk: round(vv["ms_per_launch"], 4) for kk, vv in stages.items()},
+        "device": torch.cuda.get_device_name(dev),
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

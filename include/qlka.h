@@ -1,0 +1,103 @@
+/*
+ * libqlka: MI355X (gfx950) weighted abs / Laplace sums, the hot path of quasi-linear kernel attention.
+ *
+ * A plain C ABI: device pointers, sizes and a hipStream_t passed as void*. Nothing here allocates device memory:
+ * the caller passes outputs and a workspace of at least the size the matching *_ws_bytes() returns. All launches are
+ * asynchronous on `stream`. Every function returns 0 on success or a QLKA_E* code; qlka_last_error() then holds a
+ * message for the calling thread.
+ *
+ * Layouts (the reference's own, Weighted_Abs_Sum/weighted_abs_sum/ops.py:107-110): q (P, D, M), k (P, D, N),
+ * v (P, N, C), row outputs (P, M, C), out_u (P, M), per-feature outputs (P, D, M) / (P, D, N); fp32, contiguous.
+ * Limits (Weighted_Abs_Sum/csrc/binding.cpp:69-84): P, D, N, M >= 1; 1 <= C <= 128; N, M <= 131072;
+ * P*D*max(N, M) <= INT32_MAX.
+ */
+#ifndef QLKA_H
+#define QLKA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QLKA_OK         0
+#define QLKA_EINVAL     1   /* argument validation failed (message says which) */
+#define QLKA_EWORKSPACE 2   /* workspace null or smaller than *_ws_bytes() */
+#define QLKA_EHIP       3   /* a HIP launch failed */
+
+/* Message of the last error on this thread ("" if none). */
+const char* qlka_last_error(void);
+/* ABI version of this library. */
+int qlka_version(void);
+
+/*
+ * weighted_laplace_sum forward.
+ *   out_w[p,m,c] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|) v[p,n,c],  out_u[p,m] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|)
+ * Replaces _ext.weighted_laplace_sum_forward (Weighted_Laplace_Sum/csrc/binding.cpp:63-100).
+ */
+size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C);
+int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                     int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * weighted_abs_sum forward; out_u == NULL gives the plain op, out_u != NULL the _full op.
+ *   out_w[p,m,c] = sum_{d,n} |k[p,d,n] - q[p,d,m]| v[p,n,c],  out_u[p,m] = sum_{d,n} |k[p,d,n] - q[p,d,m]|
+ * path: -1 auto, 0 global, 1 fused (the fused path exists for max(N, M) <= 4096 only, as in the reference).
+ * Replaces _ext.weighted_abs_sum_forward / weighted_abs_sum_full_forward (Weighted_Abs_Sum/csrc/binding.cpp:229-239).
+ */
+size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C);
+int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                 int P, int D, int N, int M, int C, int path, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * weighted_abs_sum backward; g_u == NULL gives the plain backward, g_u != NULL the _full backward.
+ *   grad_q[p,d,m] = sum_n s(q_m - k_n) (<v_n, g_w[m]> + g_u[m]),  grad_k[p,d,n] = sum_m s(k_n - q_m) (<g_w[m], v_n> + g_u[m]),
+ *   grad_v[p,n,c] = sum_{d,m} |k_n - q_m| g_w[p,m,c];  s(x) = +1 for x > 0, -1 otherwise (a tie counts -1).
+ * Replaces _ext.weighted_abs_sum_backward / weighted_abs_sum_full_backward (Weighted_Abs_Sum/csrc/binding.cpp:242-380).
+ */
+size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C);
+int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                 float* grad_q, float* grad_k, float* grad_v,
+                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * weighted_sgn_sum: out[p,d,m] = sum_n sgn(k[p,d,n] - q[p,d,m]) <v[p,n,:], g[p,m,:]>, with a tie counted +1
+ * (it is the negated grad_q walk). Replaces _ext.weighted_sgn_sum_forward (Weighted_Abs_Sum/csrc/binding.cpp:384-439).
+ */
+size_t qlka_sgn_fwd_ws_bytes(int P, int D, int N, int M, int C);
+int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g, float* out,
+                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Test entry: stable ascending sort of num_segs contiguous segments of seg_len fp32 keys; perm[i] is the in-segment
+ * index of the i-th smallest key (np.argsort(kind="stable"); -0.0 ties +0.0 and is written as +0.0).
+ * Replaces launch_iota + launch_cub_sort (Weighted_Abs_Sum/csrc/sort_utils.cu:85-117).
+ */
+size_t qlka_seg_sort_ws_bytes(int num_segs, int seg_len);
+int qlka_seg_sort(const float* keys, float* sorted, uint32_t* perm, int num_segs, int seg_len,
+                  void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Test entry: merge rank of every query, rank[s,m] = #{n : k[s,n] < q[s,m]} (np.searchsorted(side="left")), computed
+ * by the same sort + range split + merge walk the operators use. Replaces the walk start / emit rule of
+ * Weighted_Abs_Sum/csrc/walk_common.cuh:10-30 and abs_kernels.cu:324.
+ */
+size_t qlka_merge_rank_ws_bytes(int num_segs, int N, int M);
+int qlka_merge_rank(const float* q, const float* k, int32_t* rank, int num_segs, int N, int M,
+                    void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Optional per-stage timing (no reference counterpart; measurement aid for bench.py). When enabled, every kernel
+ * launch is bracketed by hipEvents on its own stream; qlka_timing_read() synchronises them and reports the
+ * accumulated milliseconds and launch count of one stage ("lap_range_walk", "abs_range_walk", "lds_radix_sort", ...).
+ */
+int qlka_timing_enable(int on);
+int qlka_timing_reset(void);
+int qlka_timing_read(const char* stage, double* total_ms, long long* count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLKA_H */

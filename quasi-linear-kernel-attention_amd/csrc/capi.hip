@@ -1,0 +1,250 @@
+// The C ABI of libqlka (include/qlka.h): validation, workspace layout and the launch sequence of each operator.
+// The reference's host bindings (Weighted_Abs_Sum/csrc/binding.cpp, Weighted_Laplace_Sum/csrc/binding.cpp) do the
+// same jobs with ATen tensors; here the caller owns every buffer and the library only carves the workspace.
+#include "qlka.h"
+#include "qlka_internal.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+using namespace qlka;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_status(int e, const char* where) {
+    if (e == 0) return QLKA_OK;
+    return fail(QLKA_EHIP, "%s: %s", where, hipGetErrorString((hipError_t)e));
+}
+
+inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Same limits and wording as check_qkv (Weighted_Abs_Sum/csrc/binding.cpp:79-83).
+int check_dims(int P, int D, int N, int M, int C) {
+    if (P <= 0) return fail(QLKA_EINVAL, "P must be > 0");
+    if (M <= 0 || N <= 0 || D <= 0) return fail(QLKA_EINVAL, "N, M and D must be > 0");
+    if (C < 1 || C > 128) return fail(QLKA_EINVAL, "C (v.size(2)) must be in [1, 128]");
+    if (N > 131072 || M > 131072) return fail(QLKA_EINVAL, "N and M must be <= 131072");
+    if ((int64_t)P * D * std::max(N, M) > (int64_t)INT32_MAX)
+        return fail(QLKA_EINVAL, "P*D*max(N,M) must fit int32 (cub sort offsets)");
+    return QLKA_OK;
+}
+
+// Sorted k and q of every segment, then the range arrays of the walks.
+struct SortedWs {
+    float* ks; uint32_t* kp; float* qs; uint32_t* qp;
+    void* sort_scratch; RangeArrays ra;
+};
+
+size_t sorted_ws_bytes(int S, int N, int M, int C, int range_stream_max) {
+    size_t b = 0;
+    b += 2 * align256((size_t)S * N * 4);
+    b += 2 * align256((size_t)S * M * 4);
+    b += align256(std::max(seg_sort_scratch_bytes(S, N), seg_sort_scratch_bytes(S, M)));
+    b += align256(range_arrays_bytes(S, range_stream_max, C));
+    return b;
+}
+
+SortedWs carve_sorted(void* ws, int S, int N, int M, int C, int range_stream_max) {
+    char* b = (char*)ws;
+    SortedWs w;
+    w.ks = (float*)b;    b += align256((size_t)S * N * 4);
+    w.kp = (uint32_t*)b; b += align256((size_t)S * N * 4);
+    w.qs = (float*)b;    b += align256((size_t)S * M * 4);
+    w.qp = (uint32_t*)b; b += align256((size_t)S * M * 4);
+    w.sort_scratch = b;  b += align256(std::max(seg_sort_scratch_bytes(S, N), seg_sort_scratch_bytes(S, M)));
+    w.ra = carve_range_arrays(b, S, range_stream_max, C);
+    return w;
+}
+
+int check_ws(void* ws, size_t have, size_t need) {
+    if (need > have || (need > 0 && ws == nullptr))
+        return fail(QLKA_EWORKSPACE, "workspace too small: %zu bytes given, %zu needed", have, need);
+    return QLKA_OK;
+}
+
+int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, hipStream_t st) {
+    int e = seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st);
+    if (e) return hip_status(e, "segmented sort of k");
+    e = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, st);
+    if (e) return hip_status(e, "segmented sort of q");
+    return QLKA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qlka_last_error(void) { return g_err.c_str(); }
+
+int qlka_version(void) { return 1; }
+
+// ------------------------------------------------------------------------------------------------ laplace forward
+size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C) {
+    if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    return sorted_ws_bytes(P * D, N, M, C, N);
+}
+
+int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                     int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !out_w || !out_u) return fail(QLKA_EINVAL, "q, k, v, out_w and out_u must be non-null");
+    if (int e = check_ws(ws, ws_bytes, qlka_laplace_fwd_ws_bytes(P, D, N, M, C))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    const int S = P * D;
+    SortedWs w = carve_sorted(ws, S, N, M, C, N);
+    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+    int e = fill_zero(out_w, (size_t)P * M * C, st);
+    if (!e) e = fill_zero(out_u, (size_t)P * M, st);
+    if (e) return hip_status(e, "zeroing outputs");
+    e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, out_w, out_u, P, D, N, M, C, w.ra, st);
+    return hip_status(e, "laplace walk");
+}
+
+// ---------------------------------------------------------------------------------------------------- abs forward
+size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {
+    if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    return sorted_ws_bytes(P * D, N, M, C, N);
+}
+
+int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                 int P, int D, int N, int M, int C, int path, void* ws, size_t ws_bytes, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (path < -1 || path > 1) return fail(QLKA_EINVAL, "path must be -1 (auto), 0 (global) or 1 (fused)");
+    if (!q || !k || !v || !out_w) return fail(QLKA_EINVAL, "q, k, v and out_w must be non-null");
+    // The reference's fused kernel only covers max(N, M) <= 4096 (Weighted_Abs_Sum/csrc/binding.cpp:177-188).
+    if (path == 1 && std::max(N, M) > 4096)
+        return fail(QLKA_EINVAL, "fused path pinned but unavailable: needs max(N,M) <= 4096 and the "
+                                 "bucket's shared memory to fit this device");
+    if (int e = check_ws(ws, ws_bytes, qlka_abs_fwd_ws_bytes(P, D, N, M, C))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    const int S = P * D;
+    SortedWs w = carve_sorted(ws, S, N, M, C, N);
+    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+    int e = fill_zero(out_w, (size_t)P * M * C, st);
+    if (!e && out_u) e = fill_zero(out_u, (size_t)P * M, st);
+    if (e) return hip_status(e, "zeroing outputs");
+    AbsWalkArgs a{};
+    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
+    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
+    a.out_row = out_w; a.out_u = out_u; a.out_dot = nullptr; a.out_rank = nullptr;
+    a.sign = 1.f; a.P = P; a.D = D; a.C = C;
+    e = abs_walk(a, out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW, w.ra, st);
+    return hip_status(e, "abs walk");
+}
+
+// --------------------------------------------------------------------------------------------------- abs backward
+size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
+    if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    return sorted_ws_bytes(P * D, N, M, C, std::max(N, M));
+}
+
+int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                 float* grad_q, float* grad_k, float* grad_v,
+                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
+        return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
+    if (int e = check_ws(ws, ws_bytes, qlka_abs_bwd_ws_bytes(P, D, N, M, C))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    const int S = P * D;
+    SortedWs w = carve_sorted(ws, S, N, M, C, std::max(N, M));
+    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+
+    // grad_q: stream = sorted k with rows v, queries = q, dotted with g_w (+ g_u * (2 rank - N))
+    AbsWalkArgs a{};
+    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
+    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g_w; a.uq = g_u;
+    a.out_dot = grad_q; a.sign = 1.f; a.P = P; a.D = D; a.C = C;
+    int e = abs_walk(a, g_u ? (ABS_DOT | ABS_DOTX1) : ABS_DOT, w.ra, st);
+    if (e) return hip_status(e, "grad_q walk");
+
+    // grad_k and grad_v: stream = sorted q with rows g_w (+ scalars g_u), queries = k
+    e = fill_zero(grad_v, (size_t)P * N * C, st);
+    if (e) return hip_status(e, "zeroing grad_v");
+    AbsWalkArgs b{};
+    b.ks = w.qs; b.kp = w.qp; b.Ns = M; b.w = g_w; b.u = g_u;
+    b.qs = w.ks; b.qp = w.kp; b.Mq = N; b.g = v; b.uq = nullptr;
+    b.out_row = grad_v; b.out_dot = grad_k; b.sign = 1.f; b.P = P; b.D = D; b.C = C;
+    e = abs_walk(b, g_u ? (ABS_ROW | ABS_DOT | ABS_DOTX2) : (ABS_ROW | ABS_DOT), w.ra, st);
+    return hip_status(e, "grad_k/grad_v walk");
+}
+
+// -------------------------------------------------------------------------------------------------------- sgn sum
+size_t qlka_sgn_fwd_ws_bytes(int P, int D, int N, int M, int C) {
+    if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    return sorted_ws_bytes(P * D, N, M, C, N);
+}
+
+int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g, float* out,
+                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !g || !out) return fail(QLKA_EINVAL, "q, k, v, g and out must be non-null");
+    if (int e = check_ws(ws, ws_bytes, qlka_sgn_fwd_ws_bytes(P, D, N, M, C))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    const int S = P * D;
+    SortedWs w = carve_sorted(ws, S, N, M, C, N);
+    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+    AbsWalkArgs a{};
+    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v;
+    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g;
+    a.out_dot = out; a.sign = -1.f; a.P = P; a.D = D; a.C = C;
+    int e = abs_walk(a, ABS_DOT, w.ra, st);
+    return hip_status(e, "sgn walk");
+}
+
+// ------------------------------------------------------------------------------------------------ test entries
+size_t qlka_seg_sort_ws_bytes(int num_segs, int seg_len) {
+    if (num_segs <= 0 || seg_len <= 0) return 0;
+    return seg_sort_scratch_bytes(num_segs, seg_len);
+}
+
+int qlka_seg_sort(const float* keys, float* sorted, uint32_t* perm, int num_segs, int seg_len,
+                  void* ws, size_t ws_bytes, void* stream) {
+    g_err.clear();
+    if (num_segs <= 0 || seg_len <= 0) return fail(QLKA_EINVAL, "num_segs and seg_len must be > 0");
+    if ((int64_t)num_segs * seg_len > (int64_t)INT32_MAX) return fail(QLKA_EINVAL, "num_segs*seg_len must fit int32");
+    if (!keys || !sorted || !perm) return fail(QLKA_EINVAL, "keys, sorted and perm must be non-null");
+    if (int e = check_ws(ws, ws_bytes, qlka_seg_sort_ws_bytes(num_segs, seg_len))) return e;
+    return hip_status(seg_sort(keys, sorted, perm, num_segs, seg_len, ws, (hipStream_t)stream), "segmented sort");
+}
+
+size_t qlka_merge_rank_ws_bytes(int num_segs, int N, int M) {
+    if (num_segs <= 0 || N <= 0 || M <= 0) return 0;
+    return sorted_ws_bytes(num_segs, N, M, 1, N);
+}
+
+int qlka_merge_rank(const float* q, const float* k, int32_t* rank, int num_segs, int N, int M,
+                    void* ws, size_t ws_bytes, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(num_segs, 1, N, M, 1)) return e;
+    if (!q || !k || !rank) return fail(QLKA_EINVAL, "q, k and rank must be non-null");
+    if (int e = check_ws(ws, ws_bytes, qlka_merge_rank_ws_bytes(num_segs, N, M))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    SortedWs w = carve_sorted(ws, num_segs, N, M, 1, N);
+    if (int e = sort_both(q, k, w, num_segs, N, M, st)) return e;
+    AbsWalkArgs a{};
+    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = nullptr;
+    a.qs = w.qs; a.qp = w.qp; a.Mq = M;
+    a.out_rank = rank; a.P = num_segs; a.D = 1; a.C = 1;
+    return hip_status(abs_walk(a, ABS_RANK, w.ra, st), "rank walk");
+}
+
+}  // extern "C"

@@ -1,0 +1,116 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) kernels of libqlka.
+//
+// Conventions used by every kernel in this library:
+//  * A "segment" is one (p, d) pair: s = p * D + d. q is (P, D, M) and k is (P, D, N), so the M queries / N keys of
+//    a segment are one contiguous run (layout of Weighted_Abs_Sum/weighted_abs_sum/ops.py:107-110 and
+//    Weighted_Laplace_Sum/weighted_laplace_sum/__init__.py:4-12).
+//  * Value rows (v, g) are (P, rows, C) row-major. In every walk a wave owns one key range and lane l owns channels
+//    l and l + 64 (NV = 1 or 2 channel slots per lane), so one row gather is one coalesced 4*C-byte load.
+//  * Sorted order is the stable ascending order of the fp32 values with -0.0 == +0.0 (the CUB contract at
+//    Weighted_Abs_Sum/csrc/sort_utils.cu:85-87); the merge rank of a query is #{keys < query}
+//    (np.searchsorted(side="left")), so a query is emitted before keys equal to it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace qlka {
+
+constexpr int WAVE = 64;
+
+// ---------------------------------------------------------------------------------------------------------------
+// fp32 <-> order-preserving uint32 (ascending uint order == ascending float order, -0.0 folded onto +0.0)
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t float_to_ordered(float f) {
+    uint32_t b = __float_as_uint(f);
+    if (b == 0x80000000u) b = 0u;                         // -0.0 sorts (and ties) as +0.0
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float ordered_to_float(uint32_t u) {
+    uint32_t b = (u & 0x80000000u) ? (u & 0x7fffffffu) : ~u;
+    return __uint_as_float(b);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// wave64 primitives
+// ---------------------------------------------------------------------------------------------------------------
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
+
+// value of x in lane `src` (src must be wave-uniform); lowers to v_readlane_b32
+__device__ __forceinline__ float bcast(float x, int src) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));
+}
+__device__ __forceinline__ int bcast(int x, int src) { return __builtin_amdgcn_readlane(x, src); }
+__device__ __forceinline__ uint32_t bcast(uint32_t x, int src) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, src);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, WAVE);
+    return x;
+}
+
+// Inclusive forward scan of the affine recurrence y_t = a_t * y_{t-1} + b_t across lanes (lane order). On return
+// (a, b) of lane t compose lanes 0..t: y_t = a * y_{-1} + b.
+__device__ __forceinline__ void wave_affine_scan_fwd(float& a, float& b) {
+    const int l = lane_id();
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        float ap = __shfl_up(a, off, WAVE);
+        float bp = __shfl_up(b, off, WAVE);
+        if (l >= off) { b = a * bp + b; a = a * ap; }
+    }
+}
+
+// Inclusive backward scan of y_t = a_t * y_{t+1} + b_t across lanes (reverse lane order). On return (a, b) of lane t
+// compose lanes t..63: y_t = a * y_{64} + b.
+__device__ __forceinline__ void wave_affine_scan_bwd(float& a, float& b) {
+    const int l = lane_id();
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        float an = __shfl_down(a, off, WAVE);
+        float bn = __shfl_down(b, off, WAVE);
+        if (l + off < WAVE) { b = a * bn + b; a = a * an; }
+    }
+}
+
+// Inclusive prefix sum across lanes.
+__device__ __forceinline__ float wave_prefix_sum(float x) {
+    const int l = lane_id();
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        float y = __shfl_up(x, off, WAVE);
+        if (l >= off) x += y;
+    }
+    return x;
+}
+
+// Number of elements of the ascending array a[0, n) that are <= x (std::upper_bound), found by the whole wave with a
+// 64-ary search: every round each lane probes one of 64 evenly spaced split points, so n = 2^17 needs 3 rounds of
+// dependent loads instead of 17. The predicate a[i] <= x is monotone, so the probes that pass form a lane prefix.
+// Must be called by all 64 lanes with the same (a, n, x).
+__device__ __forceinline__ int wave_upper_bound(const float* __restrict__ a, int n, float x) {
+    const int l = lane_id();
+    int lo = 0, hi = n;                                   // answer in [lo, hi]
+    while (lo < hi) {
+        const int span   = hi - lo;
+        const int stride = (span + WAVE - 1) / WAVE;      // >= 1
+        const int idx    = lo + (l + 1) * stride - 1;     // last element of lane l's block
+        const bool ok    = (idx < hi) && (a[idx] <= x);
+        const int c      = __popcll(__ballot(ok));        // blocks entirely <= x
+        const int nlo    = lo + c * stride;
+        const int nhi    = min(hi, nlo + stride - 1);
+        if (stride == 1) { lo = hi = nlo; break; }
+        lo = nlo; hi = nhi;
+    }
+    return lo;
+}
+
+// Relaxed agent-scope fp32 add with no return value (lowers to global_atomic_add_f32 without glc).
+__device__ __forceinline__ void atomic_add_f32(float* p, float v) {
+    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace qlka

@@ -1,0 +1,80 @@
+// Host-side launchers shared between the kernel files and the C ABI (capi.hip). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstddef>
+#include <cstdint>
+
+namespace qlka {
+
+// Brackets one kernel launch with hipEvents on its stream when qlka_timing_enable(1) is set (timing.hip).
+class StageTimer {
+public:
+    StageTimer(const char* name, hipStream_t st);
+    ~StageTimer();
+    StageTimer(const StageTimer&) = delete;
+    StageTimer& operator=(const StageTimer&) = delete;
+private:
+    const char* name_;
+    hipStream_t st_;
+    hipEvent_t a_ = nullptr, b_ = nullptr;
+};
+
+// Longest run the LDS radix sort handles in one workgroup (16384 keys * (4 B key + 4 B index) = 128 KB of LDS).
+constexpr int LDS_SORT_MAX = 16384;
+
+// ---- sort.hip ----
+size_t seg_sort_scratch_bytes(int S, int L);
+// Stable ascending sort of S contiguous segments of length L. Returns a hipError_t value (0 on success).
+int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch, hipStream_t st);
+
+// ---- walks.hip ----
+// Keys per key range (one wave per range) for a channel count C.
+__host__ __device__ inline int range_keys(int C) { return C <= 64 ? 64 : 32; }
+// Floats per range row in the range arrays (C channels + 2 scalar extras).
+__host__ __device__ inline int range_stride(int C) { return C + 2; }
+
+struct RangeArrays {
+    float* ta;   // [S][G+1][stride]
+    float* tb;   // [S][G+1][stride]
+    int*   qb;   // [S][G]
+};
+size_t range_arrays_bytes(int S, int Nstream, int C);
+RangeArrays carve_range_arrays(void* base, int S, int Nstream, int C);
+
+// Fill n floats with zero (a kernel, so it can sit inside a captured graph).
+int fill_zero(float* p, size_t n, hipStream_t st);
+
+// out_w[p,m,c] += sum_{d,n} exp(-|k - q|) v[p,n,c];  out_u[p,m] += sum_{d,n} exp(-|k - q|)
+int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
+                 float* out_w, float* out_u, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st);
+
+// Emission modes of the abs-family walk (bit set).
+enum AbsMode : int {
+    ABS_ROW   = 1,    // out_row[p, m, :] += sum_n |k_n - q_m| w_n            (atomics)
+    ABS_ONES  = 2,    // out_u[p, m]      += sum_n |k_n - q_m|                (atomics)
+    ABS_DOT   = 4,    // out_dot[s, m]     = sign * sum_n s(q_m - k_n) <w_n, g_m>, s(0) = -1   (store)
+    ABS_DOTX1 = 8,    //   ... + uq[p, m] * (2 rank - Ns)
+    ABS_DOTX2 = 16,   //   ... + sum_n s(q_m - k_n) u_n
+    ABS_RANK  = 32,   // out_rank[s, m]    = #{n : k_n < q_m}                 (store)
+};
+
+struct AbsWalkArgs {
+    // stream: sorted values + perm of the "keys" the prefix runs over, and their weight rows
+    const float* ks; const uint32_t* kp; int Ns;
+    const float* w;          // (P, Ns, C) weight rows, gathered by kp
+    const float* u;          // (P, Ns) scalar weights (ABS_DOTX2) or null
+    // queries
+    const float* qs; const uint32_t* qp; int Mq;
+    const float* g;          // (P, Mq, C) rows dotted at emission (ABS_DOT) or null
+    const float* uq;         // (P, Mq) (ABS_DOTX1) or null
+    float* out_row;          // (P, Mq, C)
+    float* out_u;            // (P, Mq)
+    float* out_dot;          // (P, D, Mq)
+    int32_t* out_rank;       // (P, D, Mq)
+    float sign;
+    int P, D, C;
+};
+int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
+
+}  // namespace qlka

@@ -1,0 +1,228 @@
+// Stage 1 of the hot path: per-segment stable ascending sort of fp32 keys with a uint32 permutation payload.
+//
+// Replaces the reference's CUB segmented radix sort + iota (Weighted_Abs_Sum/csrc/sort_utils.cu:17-117,
+// Weighted_Laplace_Sum/csrc/sort_utils.cu:14-126) with two gfx950 kernels of our own:
+//  * lds_radix_sort: one workgroup sorts one run of up to 16384 keys entirely in LDS (keys + indices = 128 KB of the
+//    160 KB LDS), 4 LSD passes of 8-bit digits. Stable ranking inside a wave uses 8 ballots to find the lanes that
+//    share a digit (no match instruction on CDNA), per-wave digit counters in LDS, and a digit-major exclusive scan.
+//  * merge_runs: for segments longer than one LDS run, stable merge-path merges of sorted runs (ties keep the left
+//    run first), ping-ponging between two scratch buffers; the last pass writes floats + perm.
+// Output contract: sorted[i] are the keys in stable ascending order (-0.0 written as +0.0), perm[i] the index within
+// the segment of the i-th smallest key (== np.argsort(kind="stable")).
+#include "qlka_common.h"
+#include "qlka_internal.h"
+
+#include <utility>
+
+namespace qlka {
+
+template <int WAVES, int ITEMS>
+__global__ __launch_bounds__(WAVES * WAVE)
+void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int run_len, const int runs_per_seg,
+                    float* __restrict__ out_keys, uint32_t* __restrict__ out_perm,        // direct output (1 run)
+                    uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_idx)       // run output (merging)
+{
+    constexpr int THREADS = WAVES * WAVE;
+    constexpr int CAP     = THREADS * ITEMS;
+    __shared__ uint32_t skey[CAP];
+    __shared__ uint32_t sidx[CAP];
+    __shared__ uint32_t hist[WAVES * 256];
+    __shared__ uint32_t dbase[256];
+
+    const int seg   = blockIdx.x / runs_per_seg;
+    const int run   = blockIdx.x - seg * runs_per_seg;
+    const int start = run * run_len;
+    const int len   = min(run_len, seg_len - start);
+    const size_t seg_off = (size_t)seg * seg_len;
+    const float* src = in + seg_off + start;
+
+    const int tid  = threadIdx.x;
+    const int wave = tid / WAVE;
+    const int lane = tid & (WAVE - 1);
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (WAVE - lane));
+
+    for (int i = tid; i < CAP; i += THREADS) {
+        uint32_t u = 0xffffffffu;                         // pads sort after every finite or infinite key
+        if (i < len) u = float_to_ordered(src[i]);
+        skey[i] = u;
+        sidx[i] = (uint32_t)i;                            // index inside the run (< 16384)
+    }
+
+#pragma unroll 1
+    for (int shift = 0; shift < 32; shift += 8) {
+        for (int i = tid; i < WAVES * 256; i += THREADS) hist[i] = 0u;
+        __syncthreads();                                  // previous scatter done, counters cleared
+
+        uint32_t key[ITEMS], pk[ITEMS];                   // pk = run index << 16 | offset within the wave's digit
+        const int wbase = wave * WAVE * ITEMS;
+#pragma unroll
+        for (int r = 0; r < ITEMS; ++r) {                 // item (wave, r, lane) sits at wbase + r*64 + lane
+            key[r] = skey[wbase + r * WAVE + lane];
+            pk[r]  = sidx[wbase + r * WAVE + lane] << 16;
+        }
+#pragma unroll
+        for (int r = 0; r < ITEMS; ++r) {
+            const uint32_t dig = (key[r] >> shift) & 255u;
+            uint64_t peers = ~0ull;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) {
+                const bool bit    = (dig >> b) & 1u;
+                const uint64_t m  = __ballot(bit);
+                peers &= bit ? m : ~m;
+            }
+            const uint32_t below = (uint32_t)__popcll(peers & lt_mask);
+            const uint32_t cnt   = (uint32_t)__popcll(peers);
+            const uint32_t old   = hist[wave * 256 + dig];   // every peer reads before the leader's write below
+            if (below == 0) hist[wave * 256 + dig] = old + cnt;
+            pk[r] |= old + below;
+        }
+        __syncthreads();                                  // all per-wave digit counts final; all items in regs
+
+        for (int d = tid; d < 256; d += THREADS) {        // exclusive over waves (digit-major order)
+            uint32_t run_sum = 0;
+            for (int w = 0; w < WAVES; ++w) {
+                const uint32_t c = hist[w * 256 + d];
+                hist[w * 256 + d] = run_sum;
+                run_sum += c;
+            }
+            dbase[d] = run_sum;
+        }
+        __syncthreads();
+        if (wave == 0) {                                  // exclusive scan of the 256 digit totals
+            uint32_t a0 = dbase[lane * 4 + 0], a1 = dbase[lane * 4 + 1];
+            uint32_t a2 = dbase[lane * 4 + 2], a3 = dbase[lane * 4 + 3];
+            uint32_t s = a0 + a1 + a2 + a3, incl = s;
+#pragma unroll
+            for (int o = 1; o < WAVE; o <<= 1) {
+                uint32_t y = (uint32_t)__shfl_up((int)incl, o, WAVE);
+                if (lane >= o) incl += y;
+            }
+            uint32_t e = incl - s;
+            dbase[lane * 4 + 0] = e; e += a0;
+            dbase[lane * 4 + 1] = e; e += a1;
+            dbase[lane * 4 + 2] = e; e += a2;
+            dbase[lane * 4 + 3] = e;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < ITEMS; ++r) {
+            const uint32_t dig  = (key[r] >> shift) & 255u;
+            const uint32_t dest = dbase[dig] + hist[wave * 256 + dig] + (pk[r] & 0xffffu);
+            skey[dest] = key[r];
+            sidx[dest] = pk[r] >> 16;
+        }
+    }
+    __syncthreads();
+
+    if (runs_per_seg == 1) {
+        for (int i = tid; i < len; i += THREADS) {
+            out_keys[seg_off + i] = ordered_to_float(skey[i]);
+            out_perm[seg_off + i] = (uint32_t)start + sidx[i];
+        }
+    } else {
+        for (int i = tid; i < len; i += THREADS) {
+            run_keys[seg_off + start + i] = skey[i];
+            run_idx[seg_off + start + i]  = (uint32_t)start + sidx[i];
+        }
+    }
+}
+
+// One stable merge pass: runs of `width` become runs of 2*width. Each thread emits ITEMS consecutive outputs of one
+// pair after a merge-path search for its first output (A = left run wins ties).
+constexpr int MERGE_ITEMS   = 8;
+constexpr int MERGE_THREADS = 256;
+
+__global__ __launch_bounds__(MERGE_THREADS)
+void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__ src_i,
+                uint32_t* __restrict__ dst_k, uint32_t* __restrict__ dst_i,
+                float* __restrict__ out_keys, uint32_t* __restrict__ out_perm,
+                const int seg_len, const int width, const int final_pass, const int blocks_per_seg)
+{
+    const int seg = blockIdx.x / blocks_per_seg;
+    const int blk = blockIdx.x - seg * blocks_per_seg;
+    const int o0  = (blk * MERGE_THREADS + threadIdx.x) * MERGE_ITEMS;          // position within the segment
+    if (o0 >= seg_len) return;
+    const size_t so = (size_t)seg * seg_len;
+
+    const int pair0 = (o0 / (2 * width)) * (2 * width);
+    const int a0    = pair0;
+    const int la    = min(width, seg_len - a0);
+    const int b0    = a0 + la;
+    const int lb    = max(0, min(width, seg_len - b0));
+    const uint32_t* A  = src_k + so + a0;
+    const uint32_t* B  = src_k + so + b0;
+    const uint32_t* Ai = src_i + so + a0;
+    const uint32_t* Bi = src_i + so + b0;
+
+    const int o = o0 - pair0;                              // output offset inside the pair
+    int lo = max(0, o - lb), hi = min(o, la);
+    while (lo < hi) {                                      // smallest i with A[i] > B[o - i - 1]
+        const int mid = (lo + hi) >> 1;
+        if (A[mid] <= B[o - mid - 1]) lo = mid + 1; else hi = mid;
+    }
+    int i = lo, j = o - lo;
+    const int n_out = min(MERGE_ITEMS, la + lb - o);
+    for (int t = 0; t < n_out; ++t) {
+        uint32_t key, idx;
+        if (i < la && (j >= lb || A[i] <= B[j])) { key = A[i]; idx = Ai[i]; ++i; }
+        else                                       { key = B[j]; idx = Bi[j]; ++j; }
+        const size_t dpos = so + o0 + t;
+        if (final_pass) { out_keys[dpos] = ordered_to_float(key); out_perm[dpos] = idx; }
+        else            { dst_k[dpos] = key; dst_i[dpos] = idx; }
+    }
+}
+
+template <int WAVES, int ITEMS>
+static void launch_lds(const float* in, int S, int L, int run_len, int runs, float* ok, uint32_t* op,
+                       uint32_t* rk, uint32_t* ri, hipStream_t st) {
+    StageTimer t("lds_radix_sort", st);
+    hipLaunchKernelGGL((lds_radix_sort<WAVES, ITEMS>), dim3(S * runs), dim3(WAVES * WAVE), 0, st,
+                       in, L, run_len, runs, ok, op, rk, ri);
+}
+
+size_t seg_sort_scratch_bytes(int S, int L) {
+    if (L <= LDS_SORT_MAX) return 0;
+    return 4 * (size_t)S * (size_t)L * sizeof(uint32_t);   // two (key, idx) ping-pong buffers
+}
+
+int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch, hipStream_t st) {
+    if (S <= 0 || L <= 0) return 0;
+    if (L <= LDS_SORT_MAX) {
+        // smallest (waves, items) whose capacity covers L; more waves for long runs keep 16 items per thread max
+        if      (L <= 64)    launch_lds<1, 1>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 128)   launch_lds<1, 2>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 256)   launch_lds<1, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 512)   launch_lds<2, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 1024)  launch_lds<4, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 2048)  launch_lds<8, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 4096)  launch_lds<16, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 8192)  launch_lds<16, 8>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else                 launch_lds<16, 16>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        return (int)hipGetLastError();
+    }
+    const size_t n = (size_t)S * (size_t)L;
+    uint32_t* k0 = (uint32_t*)scratch;
+    uint32_t* i0 = k0 + n;
+    uint32_t* k1 = i0 + n;
+    uint32_t* i1 = k1 + n;
+    const int runs = (L + LDS_SORT_MAX - 1) / LDS_SORT_MAX;
+    launch_lds<16, 16>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
+    int err = (int)hipGetLastError();
+    if (err) return err;
+    const int per_block = MERGE_THREADS * MERGE_ITEMS;
+    const int bps = (L + per_block - 1) / per_block;
+    dim3 grid((unsigned)((long)bps * S));
+    for (int width = LDS_SORT_MAX; width < L; width *= 2) {
+        const int fin = (2 * width >= L);
+        StageTimer t("merge_runs", st);
+        hipLaunchKernelGGL(merge_runs, grid, dim3(MERGE_THREADS), 0, st, k0, i0, k1, i1, out_keys, out_perm,
+                           L, width, fin, bps);
+        err = (int)hipGetLastError();
+        if (err) return err;
+        std::swap(k0, k1);
+        std::swap(i0, i1);
+    }
+    return 0;
+}
+
+}  // namespace qlka

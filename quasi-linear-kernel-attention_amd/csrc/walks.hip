@@ -1,0 +1,711 @@
+// Stages 2-4 of the hot path: merge rank, prefix/suffix scans and emission, for both operators.
+//
+// Per segment s = (p, d) the keys are sorted (sort.hip) and cut into key ranges of RK keys; one wave owns one range
+// and the queries whose merge rank r = #{keys < q} falls in it (the last range also owns r = N). Three kernels:
+//
+//   *_range_sums   one wave per range: the range's summary, computed directly (every term has its own weight,
+//                  no recurrence), and the range's query boundary by a 64-ary search in the sorted queries.
+//   *_range_scan   one wave per segment: turns the summaries into each range's entry state (exclusive prefix over
+//                  the ranges to the left) and, for the Laplace sum, exit state (exclusive suffix to the right).
+//   *_range_walk   one wave per range: gathers the range's RK value rows into registers (lane = channel), runs the
+//                  recurrences key by key and emits every owned query once.
+//
+// Laplace (Weighted_Laplace_Sum/csrc/laplace_kernels.cu:5-29 states the same math): with sorted keys k_0..k_{N-1}
+//   L_j = e^{-(k_j - k_{j-1})} L_{j-1} + v_j,   R_j = v_j + e^{-(k_{j+1} - k_j)} R_{j+1},
+//   query q of rank r gets  e^{-(q - k_{r-1})} L_{r-1} + e^{-(k_r - q)} R_r.
+// Every exponent argument is <= 0 and every decay factor is <= 1, so nothing overflows and nothing cancels. The walk
+// keeps R for all RK keys of its range in registers (computed backwards from the range's exit state), so v is
+// gathered twice per key and feature (sums + walk) instead of the reference's three times.
+//
+// Abs family (Weighted_Abs_Sum/csrc/abs_kernels.cu:9-19 and sgn_kernels.cu:8-15 state the same identities): the
+// stream state after the keys below q is PW = sum w_n and B = sum (k_prev - k_n) w_n, all distances measured from
+// the last absorbed key k_prev, so
+//   sum_{k_n < q} (q - k_n) w_n = (q - k_prev) PW + B,
+//   sum_n |k_n - q| w_n        = 2 [(q - k_prev) PW + B] - Btot - (q - k_max) Wtot,
+//   sum_n s(q - k_n) <w_n, g>  = <g, 2 PW - Wtot>          (s(0) = -1: a tie counts as a key above q).
+// Distances from k_prev and k_max (instead of raw k*v sums) keep the walk translation invariant. Only a prefix is
+// needed, so the abs walks gather each row once in the walk plus once in the sums.
+//
+// Outputs of the row emissions are summed over the D features of a p with relaxed fp32 atomics (one coalesced
+// 4*C-byte atomic per query and feature); the scalar emissions of the sgn walks have exactly one writer and store.
+#include "qlka_common.h"
+#include "qlka_internal.h"
+
+namespace qlka {
+
+constexpr int WPB = 4;             // waves per workgroup for the range kernels
+
+
+static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t range_arrays_bytes(int S, int Ns, int C) {
+    const int RK = range_keys(C);
+    const size_t G = (size_t)((Ns + RK - 1) / RK);
+    const size_t rows = (size_t)S * (G + 1);
+    return 2 * align256(rows * range_stride(C) * sizeof(float)) + align256((size_t)S * G * sizeof(int));
+}
+
+RangeArrays carve_range_arrays(void* base, int S, int Ns, int C) {
+    const int RK = range_keys(C);
+    const size_t G = (size_t)((Ns + RK - 1) / RK);
+    const size_t rows = (size_t)S * (G + 1);
+    char* b = (char*)base;
+    RangeArrays r;
+    r.ta = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
+    r.tb = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
+    r.qb = (int*)b;
+    return r;
+}
+
+__global__ __launch_bounds__(256)
+void fill_zero_kernel(float4* __restrict__ p4, float* __restrict__ p, const size_t n4, const size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t j = i; j < n4; j += stride) p4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (size_t j = n4 * 4 + i; j < n; j += stride) p[j] = 0.f;
+}
+
+int fill_zero(float* p, size_t n, hipStream_t st) {
+    if (n == 0) return 0;
+    const bool al = (((uintptr_t)p) & 15) == 0;
+    const size_t n4 = al ? n / 4 : 0;
+    const size_t work = n4 ? n4 : n;
+    const unsigned blocks = (unsigned)std::min<size_t>((work + 255) / 256, 8192);
+    StageTimer t("fill_zero", st);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, st, (float4*)p, p, n4, n);
+    return (int)hipGetLastError();
+}
+
+// =================================================================================================================
+// Laplace
+// =================================================================================================================
+
+// Range summary: Lt = sum_t e^{-(k_last - k_t)} v_t (the L state at the range's last key, starting from zero),
+// Rt = sum_t e^{-(k_t - k_first)} v_t (the R state at its first key, zero beyond the range). Slot C: the v == 1 sums.
+template <int NV, int RK>
+__global__ __launch_bounds__(WPB * WAVE)
+void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
+                    const float* __restrict__ v, float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
+                    const int S, const int D, const int N, const int M, const int C, const int G)
+{
+    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    if (wv >= (long)S * G) return;
+    const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
+    const int p = s / D, l = lane_id();
+    const int base = g * RK, nk = min(RK, N - base);
+    const float* kseg = ks + (size_t)s * N;
+
+    const int li = base + min(l, nk - 1);
+    const float kl = kseg[li];
+    const uint32_t pl = kp[(size_t)s * N + li];
+    const float kfirst = kseg[base], klast = kseg[base + nk - 1];
+    const bool real = l < nk;
+    const float wl = real ? __expf(-(klast - kl)) : 0.f;
+    const float wr = real ? __expf(-(kl - kfirst)) : 0.f;
+
+    const float* vp = v + (size_t)p * N * C;
+    float sl[NV], sr[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) { sl[j] = 0.f; sr[j] = 0.f; }
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+        const uint32_t row = bcast(pl, t);
+        const float a = bcast(wl, t), b = bcast(wr, t);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = l + WAVE * j;
+            const float x = (c < C) ? vp[(size_t)row * C + c] : 0.f;
+            sl[j] += a * x;
+            sr[j] += b * x;
+        }
+    }
+    const float l1 = wave_sum(wl), r1 = wave_sum(wr);
+
+    const int CS = range_stride(C);
+    float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
+    float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = l + WAVE * j;
+        if (c < C) { ra[c] = sl[j]; rb[c] = sr[j]; }
+    }
+    if (l == 0) { ra[C] = l1; rb[C] = r1; }
+
+    const int ub = wave_upper_bound(qs + (size_t)s * M, M, klast);
+    if (l == 0) qb[(size_t)s * G + g] = ub;
+}
+
+// Entry L state of every range (relative to the key before the range) and exit R state (relative to the key after
+// it), in place. One wave per segment walks its G ranges; rows are prefetched in batches of 8.
+template <int NV, int RK>
+__global__ __launch_bounds__(WPB * WAVE)
+void lap_range_scan(const float* __restrict__ ks, float* __restrict__ ta, float* __restrict__ tb,
+                    const int S, const int N, const int C, const int G)
+{
+    const int s = blockIdx.x * WPB + threadIdx.x / WAVE;
+    if (s >= S) return;
+    const int l = lane_id();
+    const int CS = range_stride(C);
+    const float* kseg = ks + (size_t)s * N;
+    float* A = ta + (size_t)s * (G + 1) * CS;
+    float* B = tb + (size_t)s * (G + 1) * CS;
+    constexpr int BATCH = 8;
+
+    // forward (L): entry(g) = sum over ranges < g, relative to k_last(g-1)
+    float cur[NV + 1];
+#pragma unroll
+    for (int j = 0; j <= NV; ++j) cur[j] = 0.f;
+    float kprev = 0.f;
+    for (int g0 = 0; g0 < G; g0 += BATCH) {
+        float a[BATCH][NV + 1], kk[BATCH];
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int g = min(g0 + b, G - 1);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                a[b][j] = (c < C) ? A[(size_t)g * CS + c] : 0.f;
+            }
+            a[b][NV] = A[(size_t)g * CS + C];
+            kk[b] = kseg[min(N, (g + 1) * RK) - 1];
+        }
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int g = g0 + b;
+            if (g >= G) break;
+            const float dec = (g == 0) ? 0.f : __expf(-(kk[b] - kprev));
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                if (c < C) A[(size_t)g * CS + c] = cur[j];
+            }
+            if (l == 0) A[(size_t)g * CS + C] = cur[NV];
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) cur[j] = a[b][j] + dec * cur[j];
+            kprev = kk[b];
+        }
+    }
+    // backward (R): exit(g) = sum over ranges > g, relative to k_first(g+1)
+#pragma unroll
+    for (int j = 0; j <= NV; ++j) cur[j] = 0.f;
+    float knext = 0.f;
+    for (int g0 = G - 1; g0 >= 0; g0 -= BATCH) {
+        float b_[BATCH][NV + 1], kk[BATCH];
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int g = max(g0 - b, 0);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                b_[b][j] = (c < C) ? B[(size_t)g * CS + c] : 0.f;
+            }
+            b_[b][NV] = B[(size_t)g * CS + C];
+            kk[b] = kseg[g * RK];
+        }
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int g = g0 - b;
+            if (g < 0) break;
+            const float dec = (g == G - 1) ? 0.f : __expf(-(knext - kk[b]));
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                if (c < C) B[(size_t)g * CS + c] = cur[j];
+            }
+            if (l == 0) B[(size_t)g * CS + C] = cur[NV];
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) cur[j] = b_[b][j] + dec * cur[j];
+            knext = kk[b];
+        }
+    }
+}
+
+template <int NV, int RK>
+__global__ __launch_bounds__(WPB * WAVE)
+void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
+                    const uint32_t* __restrict__ qp, const float* __restrict__ v,
+                    const float* __restrict__ ta, const float* __restrict__ tb, const int* __restrict__ qb,
+                    float* __restrict__ out_w, float* __restrict__ out_u,
+                    const int S, const int D, const int N, const int M, const int C, const int G)
+{
+    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    if (wv >= (long)S * G) return;
+    const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
+    const int p = s / D, l = lane_id();
+    const int base = g * RK, nk = min(RK, N - base);
+    const float* kseg = ks + (size_t)s * N;
+    const float* qseg = qs + (size_t)s * M;
+    const uint32_t* qpseg = qp + (size_t)s * M;
+
+    const int li = base + min(l, nk - 1);
+    const float kl = kseg[li];
+    const uint32_t pl = kp[(size_t)s * N + li];
+    const bool real = l < nk;
+    const bool has_prev = g > 0, has_next = g < G - 1;
+    const float kbefore = has_prev ? kseg[base - 1] : 0.f;
+    const float kafter  = has_next ? kseg[base + RK] : 0.f;
+
+    // value rows of the range (pads: zero rows, keys equal to the last real key)
+    const float* vp = v + (size_t)p * N * C;
+    float x[RK][NV];
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+        const uint32_t row = bcast(pl, t);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = l + WAVE * j;
+            x[t][j] = (c < C) ? vp[(size_t)row * C + c] : 0.f;
+        }
+    }
+
+    const int CS = range_stride(C);
+    const float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
+    const float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
+    float L[NV], Rx[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = l + WAVE * j;
+        L[j]  = (c < C) ? ra[c] : 0.f;
+        Rx[j] = (c < C) ? rb[c] : 0.f;
+    }
+    const float L1in = ra[C], R1out = rb[C];
+
+    // lane t: decay into key t from the key before it, and from key t to the key after it
+    float kbef = __shfl_up(kl, 1, WAVE);
+    if (l == 0) kbef = kbefore;
+    const float dprev = (l == 0 && !has_prev) ? 0.f : __expf(-(kl - kbef));
+    float kaft = __shfl_down(kl, 1, WAVE);
+    if (l == RK - 1) kaft = kafter;
+    const float dnext = (l == RK - 1 && !has_next) ? 0.f : __expf(-(kaft - kl));
+
+    // v == 1 channel: L1 after key t and R1 at key t, as lane-t values of two affine scans
+    float a1 = (l < RK) ? dprev : 1.f, b1 = real ? 1.f : 0.f;
+    wave_affine_scan_fwd(a1, b1);
+    const float l1 = a1 * L1in + b1;
+    float a2 = (l < RK) ? dnext : 1.f, b2 = real ? 1.f : 0.f;
+    wave_affine_scan_bwd(a2, b2);
+    const float r1 = a2 * R1out + b2;
+
+    // R_t for all keys of the range, backwards from the exit state; overwrites nothing, x is still needed for L
+    float R[RK][NV];
+#pragma unroll
+    for (int t = RK - 1; t >= 0; --t) {
+        const float dn = bcast(dnext, t);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) R[t][j] = x[t][j] + dn * (t == RK - 1 ? Rx[j] : R[t + 1][j]);
+    }
+
+    // owned queries [q0, q1) of the sorted queries
+    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+    const int q1 = has_next ? qb[(size_t)s * G + g] : M;
+    int qi = q0, qbase = q0;
+    float qbuf = (q0 + l < q1) ? qseg[q0 + l] : 0.f;
+    uint32_t pbuf = (q0 + l < q1) ? qpseg[q0 + l] : 0u;
+
+    float* ow = out_w + (size_t)p * M * C;
+    float* ou = out_u + (size_t)p * M;
+    float kprev = kbefore, l1cur = L1in;
+    bool left = has_prev;
+
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+        const float kt = bcast(kl, t);
+        const float r1t = bcast(r1, t);
+        while (qi < q1) {
+            if (qi - qbase == WAVE) {
+                qbase = qi;
+                qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
+                pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
+            }
+            const float qv = bcast(qbuf, qi - qbase);
+            if (!(qv <= kt)) break;
+            const uint32_t m = bcast(pbuf, qi - qbase);
+            const float eL = left ? __expf(-(qv - kprev)) : 0.f;
+            const float eR = __expf(-(kt - qv));
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                if (c < C) atomic_add_f32(ow + (size_t)m * C + c, eL * L[j] + eR * R[t][j]);
+            }
+            if (l == 0) atomic_add_f32(ou + m, eL * l1cur + eR * r1t);
+            ++qi;
+        }
+        const float dp = bcast(dprev, t);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) L[j] = dp * L[j] + x[t][j];
+        l1cur = bcast(l1, t);
+        kprev = kt;
+        left = true;
+    }
+    // queries above every key (rank N): only the last range owns them, and they have no right side
+    while (qi < q1) {
+        if (qi - qbase == WAVE) {
+            qbase = qi;
+            qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
+            pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
+        }
+        const float qv = bcast(qbuf, qi - qbase);
+        const uint32_t m = bcast(pbuf, qi - qbase);
+        const float eL = __expf(-(qv - kprev));
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = l + WAVE * j;
+            if (c < C) atomic_add_f32(ow + (size_t)m * C + c, eL * L[j]);
+        }
+        if (l == 0) atomic_add_f32(ou + m, eL * l1cur);
+        ++qi;
+    }
+}
+
+template <int NV, int RK>
+static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
+                          float* out_w, float* out_u, int P, int D, int N, int M, int C, RangeArrays ra,
+                          hipStream_t st) {
+    const int S = P * D;
+    const int G = (N + RK - 1) / RK;
+    const long waves = (long)S * G;
+    const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
+    {
+        StageTimer t("lap_range_sums", st);
+        hipLaunchKernelGGL((lap_range_sums<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
+                           ks, kp, qs, v, ra.ta, ra.tb, ra.qb, S, D, N, M, C, G);
+    }
+    {
+        StageTimer t("lap_range_scan", st);
+        hipLaunchKernelGGL((lap_range_scan<NV, RK>), dim3((S + WPB - 1) / WPB), dim3(WPB * WAVE), 0, st,
+                           ks, ra.ta, ra.tb, S, N, C, G);
+    }
+    {
+        StageTimer t("lap_range_walk", st);
+        hipLaunchKernelGGL((lap_range_walk<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
+                           ks, kp, qs, qp, v, ra.ta, ra.tb, ra.qb, out_w, out_u, S, D, N, M, C, G);
+    }
+    return (int)hipGetLastError();
+}
+
+int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
+                 float* out_w, float* out_u, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st) {
+    if (C <= WAVE) return laplace_walk_t<1, 64>(ks, kp, qs, qp, v, out_w, out_u, P, D, N, M, C, ra, st);
+    return laplace_walk_t<2, 32>(ks, kp, qs, qp, v, out_w, out_u, P, D, N, M, C, ra, st);
+}
+
+// =================================================================================================================
+// Abs family
+// =================================================================================================================
+
+// Range summary: Wt = sum_t w_t, Bt = sum_t (k_last - k_t) w_t; slot C: Ut = sum_t u_t (ta), B1t = sum_t
+// (k_last - k_t) (tb).
+template <int NV, int RK, bool WANT_W, bool WANT_U>
+__global__ __launch_bounds__(WPB * WAVE)
+void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
+                    const float* __restrict__ w, const float* __restrict__ u,
+                    float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
+                    const int S, const int D, const int Ns, const int Mq, const int C, const int G)
+{
+    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    if (wv >= (long)S * G) return;
+    const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
+    const int p = s / D, l = lane_id();
+    const int base = g * RK, nk = min(RK, Ns - base);
+    const float* kseg = ks + (size_t)s * Ns;
+
+    const int li = base + min(l, nk - 1);
+    const float kl = kseg[li];
+    const uint32_t pl = kp[(size_t)s * Ns + li];
+    const float klast = kseg[base + nk - 1];
+    const bool real = l < nk;
+    const float dl = real ? (klast - kl) : 0.f;
+
+    const float* wp = w + (size_t)p * Ns * C;
+    float sw[NV], sb[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) { sw[j] = 0.f; sb[j] = 0.f; }
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+        const uint32_t row = bcast(pl, t);
+        const float dt = bcast(dl, t);
+        const float keep = (t < nk) ? 1.f : 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = l + WAVE * j;
+            const float xv = (WANT_W && c < C) ? wp[(size_t)row * C + c] * keep : 0.f;
+            sw[j] += xv;
+            sb[j] += dt * xv;
+        }
+    }
+    const float b1 = wave_sum(dl);
+    float u1 = 0.f;
+    if constexpr (WANT_U) u1 = wave_sum(real ? u[(size_t)p * Ns + pl] : 0.f);
+
+    const int CS = range_stride(C);
+    float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
+    float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = l + WAVE * j;
+        if (c < C) { ra[c] = sw[j]; rb[c] = sb[j]; }
+    }
+    if (l == 0) { ra[C] = u1; rb[C] = b1; }
+
+    const int ub = wave_upper_bound(qs + (size_t)s * Mq, Mq, klast);
+    if (l == 0) qb[(size_t)s * G + g] = ub;
+}
+
+// Entry state (PW, B relative to the key before the range; slot C: PU, B1) of every range in place, and the totals
+// (Wtot, Btot relative to k_max; Utot, B1tot) in row G.
+template <int NV, int RK>
+__global__ __launch_bounds__(WPB * WAVE)
+void abs_range_scan(const float* __restrict__ ks, float* __restrict__ ta, float* __restrict__ tb,
+                    const int S, const int Ns, const int C, const int G)
+{
+    const int s = blockIdx.x * WPB + threadIdx.x / WAVE;
+    if (s >= S) return;
+    const int l = lane_id();
+    const int CS = range_stride(C);
+    const float* kseg = ks + (size_t)s * Ns;
+    float* A = ta + (size_t)s * (G + 1) * CS;
+    float* B = tb + (size_t)s * (G + 1) * CS;
+    constexpr int BATCH = 8;
+
+    float pw[NV + 1], bb[NV + 1];   // slot NV: PU / B1
+#pragma unroll
+    for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
+    float cnt = 0.f, kprev = 0.f;
+    for (int g0 = 0; g0 < G; g0 += BATCH) {
+        float a[BATCH][NV + 1], b_[BATCH][NV + 1], kk[BATCH];
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int g = min(g0 + b, G - 1);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                a[b][j]  = (c < C) ? A[(size_t)g * CS + c] : 0.f;
+                b_[b][j] = (c < C) ? B[(size_t)g * CS + c] : 0.f;
+            }
+            a[b][NV]  = A[(size_t)g * CS + C];
+            b_[b][NV] = B[(size_t)g * CS + C];
+            kk[b] = kseg[min(Ns, (g + 1) * RK) - 1];
+        }
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int g = g0 + b;
+            if (g >= G) break;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                if (c < C) { A[(size_t)g * CS + c] = pw[j]; B[(size_t)g * CS + c] = bb[j]; }
+            }
+            if (l == 0) { A[(size_t)g * CS + C] = pw[NV]; B[(size_t)g * CS + C] = bb[NV]; }
+            const float gap = (g == 0) ? 0.f : (kk[b] - kprev);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) { bb[j] = b_[b][j] + bb[j] + gap * pw[j]; pw[j] += a[b][j]; }
+            bb[NV] = b_[b][NV] + bb[NV] + gap * cnt;
+            pw[NV] += a[b][NV];
+            cnt += (float)min(RK, Ns - g * RK);
+            kprev = kk[b];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = l + WAVE * j;
+        if (c < C) { A[(size_t)G * CS + c] = pw[j]; B[(size_t)G * CS + c] = bb[j]; }
+    }
+    if (l == 0) { A[(size_t)G * CS + C] = pw[NV]; B[(size_t)G * CS + C] = bb[NV]; }
+}
+
+template <int NV, int RK, int MODE>
+__global__ __launch_bounds__(WPB * WAVE)
+void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __restrict__ tb,
+                    const int* __restrict__ qb, const int G)
+{
+    constexpr bool ROW = MODE & ABS_ROW, ONES = MODE & ABS_ONES, DOT = MODE & ABS_DOT;
+    constexpr bool X1 = MODE & ABS_DOTX1, X2 = MODE & ABS_DOTX2, RANK = MODE & ABS_RANK;
+    constexpr bool NEED_B = ROW || ONES;
+    constexpr bool NEED_W = ROW || DOT;
+    const int S = a.P * a.D, C = a.C, Ns = a.Ns, Mq = a.Mq;
+    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    if (wv >= (long)S * G) return;
+    const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
+    const int p = s / a.D, l = lane_id();
+    const int base = g * RK, nk = min(RK, Ns - base);
+    const float* kseg = a.ks + (size_t)s * Ns;
+    const float* qseg = a.qs + (size_t)s * Mq;
+    const uint32_t* qpseg = a.qp + (size_t)s * Mq;
+
+    const int li = base + min(l, nk - 1);
+    const float kl = kseg[li];
+    const uint32_t pl = a.kp[(size_t)s * Ns + li];
+    const bool real = l < nk;
+    const bool has_prev = g > 0, has_next = g < G - 1;
+    const float kbefore = has_prev ? kseg[base - 1] : 0.f;
+    const float kmax = kseg[Ns - 1];
+
+    const float* wp = a.w + (size_t)p * Ns * C;
+    float x[RK][NV];
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+        const uint32_t row = bcast(pl, t);
+        const float keep = (t < nk) ? 1.f : 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = l + WAVE * j;
+            x[t][j] = (NEED_W && c < C) ? wp[(size_t)row * C + c] * keep : 0.f;
+        }
+    }
+    float ul = 0.f;
+    if constexpr (X2) ul = real ? a.u[(size_t)p * Ns + pl] : 0.f;
+
+    float kbef = __shfl_up(kl, 1, WAVE);
+    if (l == 0) kbef = kbefore;
+    const float gap = (real && (l > 0 || has_prev)) ? (kl - kbef) : 0.f;
+
+    const int CS = range_stride(C);
+    const float* rowA = ta + ((size_t)s * (G + 1) + g) * CS;
+    const float* rowB = tb + ((size_t)s * (G + 1) + g) * CS;
+    const float* totA = ta + ((size_t)s * (G + 1) + G) * CS;
+    const float* totB = tb + ((size_t)s * (G + 1) + G) * CS;
+    float PW[NV], Bv[NV], Wt[NV], Bt[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = l + WAVE * j;
+        const bool ok = c < C;
+        PW[j] = ok ? rowA[c] : 0.f;
+        Wt[j] = ok ? totA[c] : 0.f;
+        Bv[j] = (NEED_B && ok) ? rowB[c] : 0.f;
+        Bt[j] = (NEED_B && ok) ? totB[c] : 0.f;
+    }
+    float PU = 0.f, Ut = 0.f, B1 = 0.f, B1t = 0.f;
+    if constexpr (X2) { PU = rowA[C]; Ut = totA[C]; }
+    if constexpr (ONES) { B1 = rowB[C]; B1t = totB[C]; }
+    float cnt = (float)base;
+    const float Nf = (float)Ns;
+
+    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+    const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
+    int qi = q0, qbase = q0;
+    float qbuf = (q0 + l < q1) ? qseg[q0 + l] : 0.f;
+    uint32_t pbuf = (q0 + l < q1) ? qpseg[q0 + l] : 0u;
+    float kprev = kbefore;
+
+    auto emit = [&](const float qv, const uint32_t m) {
+        const float lq = qv - kprev;
+        const bool any = cnt > 0.f;
+        if constexpr (ROW) {
+            float* orow = a.out_row + ((size_t)p * Mq + m) * C;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                const float la = any ? (lq * PW[j] + Bv[j]) : 0.f;
+                if (c < C) atomic_add_f32(orow + c, 2.f * la - Bt[j] - (qv - kmax) * Wt[j]);
+            }
+        }
+        if constexpr (ONES) {
+            const float la = any ? (lq * cnt + B1) : 0.f;
+            if (l == 0) atomic_add_f32(a.out_u + (size_t)p * Mq + m, 2.f * la - B1t - (qv - kmax) * Nf);
+        }
+        if constexpr (DOT) {
+            const float* grow = a.g + ((size_t)p * Mq + m) * C;
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                if (c < C) acc += grow[c] * (2.f * PW[j] - Wt[j]);
+            }
+            acc = wave_sum(acc);
+            if constexpr (X1) acc += a.uq[(size_t)p * Mq + m] * (2.f * cnt - Nf);
+            if constexpr (X2) acc += 2.f * PU - Ut;
+            if (l == 0) a.out_dot[(size_t)s * Mq + m] = a.sign * acc;
+        }
+        if constexpr (RANK) {
+            if (l == 0) a.out_rank[(size_t)s * Mq + m] = (int32_t)cnt;
+        }
+    };
+
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+        const float kt = bcast(kl, t);
+        while (qi < q1) {
+            if (qi - qbase == WAVE) {
+                qbase = qi;
+                qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
+                pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
+            }
+            const float qv = bcast(qbuf, qi - qbase);
+            if (!(qv <= kt)) break;
+            emit(qv, bcast(pbuf, qi - qbase));
+            ++qi;
+        }
+        const float gt = bcast(gap, t);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            if constexpr (NEED_B) Bv[j] += gt * PW[j];
+            PW[j] += x[t][j];
+        }
+        if constexpr (ONES) B1 += gt * cnt;
+        if constexpr (X2) PU += bcast(ul, t);
+        cnt += (t < nk) ? 1.f : 0.f;
+        kprev = kt;
+    }
+    while (qi < q1) {
+        if (qi - qbase == WAVE) {
+            qbase = qi;
+            qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
+            pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
+        }
+        emit(bcast(qbuf, qi - qbase), bcast(pbuf, qi - qbase));
+        ++qi;
+    }
+}
+
+template <int NV, int RK, int MODE>
+static void launch_abs_walk(const AbsWalkArgs& a, RangeArrays ra, int G, hipStream_t st) {
+    const long waves = (long)a.P * a.D * G;
+    const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
+    StageTimer t("abs_range_walk", st);
+    hipLaunchKernelGGL((abs_range_walk<NV, RK, MODE>), dim3(blocks), dim3(WPB * WAVE), 0, st, a, ra.ta, ra.tb,
+                       ra.qb, G);
+}
+
+template <int NV, int RK>
+static int abs_walk_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
+    const int S = a.P * a.D;
+    const int G = (a.Ns + RK - 1) / RK;
+    const long waves = (long)S * G;
+    const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
+    {
+        StageTimer t("abs_range_sums", st);
+        if (mode & ABS_DOTX2)
+            hipLaunchKernelGGL((abs_range_sums<NV, RK, true, true>), dim3(blocks), dim3(WPB * WAVE), 0, st,
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.ta, ra.tb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+        else if (mode == ABS_RANK)
+            hipLaunchKernelGGL((abs_range_sums<NV, RK, false, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.ta, ra.tb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+        else
+            hipLaunchKernelGGL((abs_range_sums<NV, RK, true, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.ta, ra.tb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+    }
+    {
+        StageTimer t("abs_range_scan", st);
+        hipLaunchKernelGGL((abs_range_scan<NV, RK>), dim3((S + WPB - 1) / WPB), dim3(WPB * WAVE), 0, st,
+                           a.ks, ra.ta, ra.tb, S, a.Ns, a.C, G);
+    }
+    switch (mode) {
+        case ABS_ROW:                         launch_abs_walk<NV, RK, ABS_ROW>(a, ra, G, st); break;
+        case ABS_ROW | ABS_ONES:              launch_abs_walk<NV, RK, ABS_ROW | ABS_ONES>(a, ra, G, st); break;
+        case ABS_DOT:                         launch_abs_walk<NV, RK, ABS_DOT>(a, ra, G, st); break;
+        case ABS_DOT | ABS_DOTX1:             launch_abs_walk<NV, RK, ABS_DOT | ABS_DOTX1>(a, ra, G, st); break;
+        case ABS_ROW | ABS_DOT:               launch_abs_walk<NV, RK, ABS_ROW | ABS_DOT>(a, ra, G, st); break;
+        case ABS_ROW | ABS_DOT | ABS_DOTX2:   launch_abs_walk<NV, RK, ABS_ROW | ABS_DOT | ABS_DOTX2>(a, ra, G, st);
+                                              break;
+        case ABS_RANK:                        launch_abs_walk<NV, RK, ABS_RANK>(a, ra, G, st); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+    return (int)hipGetLastError();
+}
+
+int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
+    if (a.C <= WAVE) return abs_walk_t<1, 64>(a, mode, ra, st);
+    return abs_walk_t<2, 32>(a, mode, ra, st);
+}
+
+}  // namespace qlka

@@ -1,0 +1,103 @@
+"""Public ops and backend dispatch of weighted_abs_sum, mirroring Weighted_Abs_Sum/weighted_abs_sum/ops.py:1-139.
+
+Backends "auto", "keops", "cuda", "cuda-fused", "cuda-global" are all accepted (ops.py:12-13). On MI355X every backend
+runs the native gfx950 kernels of libqlka.so:
+
+* "cuda" / "cuda-global" -> path -1 / 0, "cuda-fused" -> path 1 (which, as in the reference, raises for
+  max(N, M) > 4096).
+* "keops" (passed by Experiments/kernel_attention/attention.py:63 for S < 256) has no pykeops behind it on ROCm; it runs
+  the same native walk. The only semantic difference from pykeops is the sign of an exact tie in weighted_sgn_sum
+  (pykeops: sign(0) = 0, keops_backend.py:40-41; the walk: a tie counts as +1 there, as the reference's CUDA path).
+* "auto" behaves as in the reference: "keops" strictly below KEOPS_CUTOFF, else "cuda".
+"""
+
+import torch
+
+from weighted_abs_sum import _ext as _C
+
+_BACKENDS = ("auto", "keops", "cuda", "cuda-fused", "cuda-global")
+_PATH = {"cuda": -1, "cuda-fused": 1, "cuda-global": 0, "keops": -1}
+
+# "auto" uses the keops route strictly below this max(N,M)
+KEOPS_CUTOFF = 512
+
+
+def set_keops_cutoff(n):
+    """Set the max(N,M) below which backend='auto' uses the keops route (0 disables)."""
+    global KEOPS_CUTOFF
+    KEOPS_CUTOFF = int(n)
+    return KEOPS_CUTOFF
+
+
+def _resolve(backend, q, k, v):
+    if backend not in _BACKENDS:
+        raise ValueError(f"backend must be one of {_BACKENDS}, got {backend!r}")
+    if backend != "auto":
+        return backend
+    if not (q.is_cuda and q.dtype == torch.float32):
+        return "cuda"   # let the extension raise its precise error message
+    if max(q.shape[-1], k.shape[-1]) < KEOPS_CUTOFF:
+        return "keops"
+    return "cuda"
+
+
+class _WeightedAbsSum(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, path):
+        ctx.save_for_backward(q, k, v)
+        ctx.set_materialize_grads(False)
+        return _C.weighted_abs_sum_forward(q, k, v, path)
+
+    @staticmethod
+    def backward(ctx, g_w):
+        q, k, v = ctx.saved_tensors
+        grad_q, grad_k, grad_v = _C.weighted_abs_sum_backward(q, k, v, g_w.contiguous())
+        return grad_q, grad_k, grad_v, None
+
+
+class _WeightedAbsSumFull(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, path):
+        ctx.save_for_backward(q, k, v)
+        ctx.set_materialize_grads(False)
+        return _C.weighted_abs_sum_full_forward(q, k, v, path)
+
+    @staticmethod
+    def backward(ctx, g_w, g_u):
+        q, k, v = ctx.saved_tensors
+        if g_u is None:     # out_u unused -> the cheaper plain backward
+            grad_q, grad_k, grad_v = _C.weighted_abs_sum_backward(q, k, v, g_w.contiguous())
+        else:
+            if g_w is None:
+                g_w = torch.zeros(q.shape[0], q.shape[2], v.shape[2], device=q.device, dtype=q.dtype)
+            grad_q, grad_k, grad_v = _C.weighted_abs_sum_full_backward(
+                q, k, v, g_w.contiguous(), g_u.contiguous())
+        return grad_q, grad_k, grad_v, None
+
+
+def weighted_abs_sum(q, k, v, backend="auto"):
+    """out[p,m,c] = sum_{n,d} |k[p,d,n] - q[p,d,m]| * v[p,n,c]
+
+    q: (P, D, M), k: (P, D, N), v: (P, N, C) -> (P, M, C). Differentiable.
+    """
+    b = _resolve(backend, q, k, v)
+    return _WeightedAbsSum.apply(q, k, v, _PATH[b])
+
+
+def weighted_abs_sum_full(q, k, v, backend="auto"):
+    """Returns (out_w, out_u): the weighted abs sum (P, M, C) and the unweighted abs sum
+    out_u[p,m] = sum_{n,d} |k[p,d,n] - q[p,d,m]| (P, M), from one pass. Differentiable in both outputs.
+    """
+    b = _resolve(backend, q, k, v)
+    return _WeightedAbsSumFull.apply(q, k, v, _PATH[b])
+
+
+def weighted_sgn_sum(q, k, v, g, backend="auto"):
+    """out[p,d,m] = sum_n sgn(k[p,d,n] - q[p,d,m]) * dot(v[p,n,:], g[p,m,:])
+
+    (P, D, M). Not differentiable (it IS a gradient).
+    """
+    b = _resolve(backend, q, k, v)
+    if b == "cuda-fused":
+        raise ValueError("weighted_sgn_sum has no fused path; use 'cuda' or 'cuda-global'")
+    return _C.weighted_sgn_sum_forward(q, k, v, g.contiguous())

@@ -1,0 +1,80 @@
+"""CPU checks of the C ABI: libqlka.so builds for gfx950, loads, exports every function include/qlka.h declares, and
+its host-side validation answers without touching a GPU (no compute call is made here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from qlka import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "qlka.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(qlka_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from qlka import build
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_boundary():
+    names = _declared()
+    for fn in ("qlka_laplace_fwd", "qlka_abs_fwd", "qlka_abs_bwd", "qlka_sgn_fwd", "qlka_seg_sort",
+               "qlka_merge_rank", "qlka_last_error"):
+        assert fn in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in _declared() if not hasattr(raw, n)]
+    assert not missing, f"not exported: {missing}"
+    assert set(_declared()) == set(_lib.EXPORTED), "ctypes signature table out of sync with include/qlka.h"
+
+
+def test_version_and_workspace_sizes(lib):
+    assert lib.qlka_version() == 1
+    small = lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4)
+    big = lib.qlka_laplace_fwd_ws_bytes(12, 64, 16384, 16384, 64)
+    assert 0 < small < big
+    assert lib.qlka_abs_bwd_ws_bytes(12, 64, 16384, 16384, 64) >= lib.qlka_abs_fwd_ws_bytes(12, 64, 16384, 16384, 64)
+    # the global (multi-run) sort needs scratch, the LDS sort none
+    assert lib.qlka_seg_sort_ws_bytes(4, 16384) == 0
+    assert lib.qlka_seg_sort_ws_bytes(4, 16385) > 0
+    assert lib.qlka_laplace_fwd_ws_bytes(0, 1, 1, 1, 1) == 0
+
+
+@pytest.mark.parametrize("dims,msg", [
+    ((1, 1, 8, 8, 129), "C (v.size(2)) must be in [1, 128]"),
+    ((1, 1, 8, 8, 0), "C (v.size(2)) must be in [1, 128]"),
+    ((1, 1, 131073, 8, 4), "N and M must be <= 131072"),
+    ((1, 0, 8, 8, 4), "N, M and D must be > 0"),
+    ((40000, 64, 1000, 1000, 4), "P*D*max(N,M) must fit int32"),
+])
+def test_validation_before_any_gpu_call(lib, dims, msg):
+    P, D, N, M, C = dims
+    dummy = ctypes.c_void_p(16)     # never dereferenced: validation fails first
+    rc = lib.qlka_laplace_fwd(dummy, dummy, dummy, dummy, dummy, P, D, N, M, C, dummy, 1 << 40, None)
+    assert rc == 1
+    assert msg in lib.qlka_last_error().decode()
+    rc = lib.qlka_abs_fwd(dummy, dummy, dummy, dummy, dummy, P, D, N, M, C, -1, dummy, 1 << 40, None)
+    assert rc == 1
+
+
+def test_path_and_workspace_errors(lib):
+    dummy = ctypes.c_void_p(16)
+    rc = lib.qlka_abs_fwd(dummy, dummy, dummy, dummy, dummy, 1, 1, 5000, 8, 4, 1, dummy, 1 << 40, None)
+    assert rc == 1 and "fused path pinned but unavailable" in lib.qlka_last_error().decode()
+    rc = lib.qlka_abs_fwd(dummy, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, 2, dummy, 1 << 40, None)
+    assert rc == 1 and "path must be -1 (auto), 0 (global) or 1 (fused)" in lib.qlka_last_error().decode()
+    rc = lib.qlka_laplace_fwd(dummy, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, dummy, 16, None)
+    assert rc == 2 and "workspace too small" in lib.qlka_last_error().decode()
+    rc = lib.qlka_laplace_fwd(None, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
+    assert rc == 1 and "non-null" in lib.qlka_last_error().decode()

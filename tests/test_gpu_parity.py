@@ -1,0 +1,259 @@
+"""GPU parity of the HIP path (through the drop-in packages and the C ABI) against the fp64 oracle.
+
+Bars: sort permutations and merge ranks bit-exact; every float output within REL = 1e-5 of the fp64 oracle per element,
+normalised by the sum of |term|.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _data(P, D, N, M, C, seed=0, kind="normal"):
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        q = rng.standard_normal((P, D, M)).astype(np.float32)
+        k = rng.standard_normal((P, D, N)).astype(np.float32)
+    elif kind == "ties":                           # few distinct levels: exact q == k ties and repeated keys
+        q = (rng.integers(-4, 5, size=(P, D, M)) / 4).astype(np.float32)
+        k = (rng.integers(-4, 5, size=(P, D, N)) / 4).astype(np.float32)
+    elif kind == "zeros":                          # +-0.0 mixed with a few other tied levels
+        lv = np.array([-0.0, 0.0, 1.0, -1.0, 0.5], dtype=np.float32)
+        q = rng.choice(lv, size=(P, D, M))
+        k = rng.choice(lv, size=(P, D, N))
+    elif kind == "wide":                           # wide spread: exp underflow in the Laplace sums
+        q = (rng.standard_normal((P, D, M)) * 40).astype(np.float32)
+        k = (rng.standard_normal((P, D, N)) * 40).astype(np.float32)
+    else:
+        raise ValueError(kind)
+    v = rng.standard_normal((P, N, C)).astype(np.float32)
+    return q, k, v
+
+
+def _assert_rel(got, want, norm, what):
+    err = brute.rel_err(got, want, norm)
+    worst = float(err.max()) if err.size else 0.0
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert worst <= REL, f"{what}: max rel err {worst:.3e} > {REL}"
+
+
+SHAPES = [
+    (1, 1, 1, 1, 1),
+    (2, 3, 7, 5, 4),
+    (2, 2, 64, 64, 64),
+    (2, 2, 65, 63, 33),
+    (3, 4, 129, 200, 64),
+    (2, 3, 1000, 700, 65),
+    (1, 2, 300, 257, 128),
+    (1, 3, 100, 90, 1),
+    (2, 2, 5000, 4097, 32),
+]
+
+
+# ------------------------------------------------------------------------------------------------ sort / rank
+@pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 100, 257, 1000, 2049, 5000, 8192, 16384, 16385, 40000])
+@pytest.mark.parametrize("kind", ["normal", "ties", "zeros"])
+def test_seg_sort_bit_exact(dev, L, kind):
+    from qlka import ops
+    S = 3
+    q, _, _ = _data(S, 1, 1, L, 1, seed=L, kind=kind)
+    keys = q.reshape(S, L)
+    srt, perm = ops.seg_sort(_t(keys, dev))
+    want_s, want_p = brute.stable_sort(keys)
+    np.testing.assert_array_equal(_np(perm), want_p)
+    np.testing.assert_array_equal(_np(srt), want_s)
+    assert not np.any((_np(srt) == 0) & np.signbit(_np(srt))), "-0.0 must be written as +0.0"
+
+
+@pytest.mark.parametrize("N,M", [(1, 1), (1, 5), (7, 1), (64, 64), (65, 200), (1000, 999), (3000, 70), (70000, 300)])
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_merge_rank_bit_exact(dev, N, M, kind):
+    from qlka import ops
+    S = 2
+    q, k, _ = _data(S, 1, N, M, 1, seed=N + M, kind=kind)
+    q, k = q.reshape(S, M), k.reshape(S, N)
+    if kind == "ties":   # some queries equal to keys exactly, some outside the key range
+        q[:, ::3] = k[:, (np.arange(0, M, 3) % N)]
+        q[:, 1] = k.min() - 1
+        q[:, -1] = k.max() + 1
+    r = ops.merge_rank(_t(q, dev), _t(k, dev))
+    np.testing.assert_array_equal(_np(r), brute.merge_rank(q, k))
+
+
+# --------------------------------------------------------------------------------------------------- forward ops
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_laplace_forward(dev, shape, kind):
+    from weighted_laplace_sum import weighted_laplace_sum
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape), kind=kind)
+    w, u = weighted_laplace_sum(_t(q, dev), _t(k, dev), _t(v, dev))
+    ow, ou, nw = brute.laplace_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, "laplace out_w")
+    _assert_rel(_np(u), ou, ou, "laplace out_u")
+
+
+def test_laplace_wide_spread_underflow(dev):
+    from weighted_laplace_sum import weighted_laplace_sum
+    q, k, v = _data(2, 3, 500, 400, 16, seed=5, kind="wide")
+    w, u = weighted_laplace_sum(_t(q, dev), _t(k, dev), _t(v, dev))
+    ow, ou, nw = brute.laplace_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, "laplace out_w (wide)")
+    _assert_rel(_np(u), ou, ou, "laplace out_u (wide)")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_abs_forward_full(dev, shape, kind):
+    from weighted_abs_sum import weighted_abs_sum, weighted_abs_sum_full
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 1, kind=kind)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+    w0 = weighted_abs_sum(tq, tk, tv, backend="cuda-global")
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, "abs out_w")
+    _assert_rel(_np(u), ou, ou, "abs out_u")
+    _assert_rel(_np(w0), ow, nw, "abs (plain) out")
+
+
+def test_abs_translation_far_from_zero(dev):
+    # keys and queries centred at 1000: the distance-relative walk must not cancel catastrophically
+    from weighted_abs_sum import weighted_abs_sum_full
+    q, k, v = _data(2, 3, 800, 600, 8, seed=7)
+    q = q + np.float32(1000.0)
+    k = k + np.float32(1000.0)
+    w, u = weighted_abs_sum_full(_t(q, dev), _t(k, dev), _t(v, dev))
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, "abs out_w (offset 1000)")
+    _assert_rel(_np(u), ou, ou, "abs out_u (offset 1000)")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_sgn_sum(dev, shape, kind):
+    from weighted_abs_sum import weighted_sgn_sum
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 2, kind=kind)
+    g = np.random.default_rng(3).standard_normal((P, M, C)).astype(np.float32)
+    out = weighted_sgn_sum(_t(q, dev), _t(k, dev), _t(v, dev), _t(g, dev), backend="cuda")
+    want, norm = brute.sgn_sum(q, k, v, g, tie=1.0)
+    _assert_rel(_np(out), want, norm, "sgn")
+
+
+# ---------------------------------------------------------------------------------------------------- backward
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("full", [False, True])
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_abs_backward(dev, shape, full, kind):
+    from weighted_abs_sum import _ext
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 3, kind=kind)
+    rng = np.random.default_rng(4)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32) if full else None
+    args = [_t(q, dev), _t(k, dev), _t(v, dev), _t(g_w, dev)]
+    if full:
+        gq, gk, gv = _ext.weighted_abs_sum_full_backward(*args, _t(g_u, dev))
+    else:
+        gq, gk, gv = _ext.weighted_abs_sum_backward(*args)
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u)
+    _assert_rel(_np(gq), wq, nq, "grad_q")
+    _assert_rel(_np(gk), wk, nk, "grad_k")
+    _assert_rel(_np(gv), wv, nv, "grad_v")
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_autograd_through_ops(dev, full):
+    from weighted_abs_sum import weighted_abs_sum, weighted_abs_sum_full
+    P, D, N, M, C = 2, 4, 300, 250, 16
+    q, k, v = _data(P, D, N, M, C, seed=21)
+    rng = np.random.default_rng(5)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+    if full:
+        w, u = weighted_abs_sum_full(tq, tk, tv)
+        loss = (w * _t(g_w, dev)).sum() + (u * _t(g_u, dev)).sum()
+    else:
+        w = weighted_abs_sum(tq, tk, tv)
+        loss = (w * _t(g_w, dev)).sum()
+    loss.backward()
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u if full else None)
+    _assert_rel(_np(tq.grad), wq, nq, "autograd grad_q")
+    _assert_rel(_np(tk.grad), wk, nk, "autograd grad_k")
+    _assert_rel(_np(tv.grad), wv, nv, "autograd grad_v")
+
+
+def test_full_backward_only_u(dev):
+    # out_w unused: g_w is None inside the autograd Function and becomes zeros (ops.py:99-101)
+    from weighted_abs_sum import weighted_abs_sum_full
+    P, D, N, M, C = 1, 3, 120, 100, 8
+    q, k, v = _data(P, D, N, M, C, seed=22)
+    g_u = np.random.default_rng(6).standard_normal((P, M)).astype(np.float32)
+    tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+    _, u = weighted_abs_sum_full(tq, tk, tv)
+    (u * _t(g_u, dev)).sum().backward()
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, np.zeros((P, M, C), np.float32), g_u)
+    _assert_rel(_np(tq.grad), wq, nq, "grad_q (u only)")
+    _assert_rel(_np(tk.grad), wk, nk, "grad_k (u only)")
+    np.testing.assert_array_equal(_np(tv.grad), np.zeros_like(v))
+
+
+# ------------------------------------------------------------------------------------------------ boundary on GPU
+def test_gpu_validation_errors(dev):
+    from weighted_abs_sum import _ext, weighted_abs_sum_full, weighted_sgn_sum
+    from weighted_laplace_sum import weighted_laplace_sum
+    q = torch.randn(1, 2, 8, device=dev)
+    k = torch.randn(1, 2, 8, device=dev)
+    with pytest.raises(RuntimeError, match=r"C \(v.size\(2\)\) must be in \[1, 128\]"):
+        _ext.weighted_abs_sum_forward(q, k, torch.randn(1, 8, 129, device=dev))
+    with pytest.raises(RuntimeError, match=r"C \(v.size\(2\)\) must be in \[1, 128\]"):
+        weighted_laplace_sum(q, k, torch.randn(1, 8, 129, device=dev))
+    with pytest.raises(RuntimeError, match="N and M must be <= 131072"):
+        _ext.weighted_abs_sum_forward(torch.randn(1, 1, 4, device=dev), torch.randn(1, 1, 131073, device=dev),
+                                      torch.randn(1, 131073, 1, device=dev))
+    with pytest.raises(RuntimeError, match="must be contiguous"):
+        _ext.weighted_abs_sum_forward(q.transpose(1, 2).contiguous().transpose(1, 2), k, torch.randn(1, 8, 4, device=dev))
+    with pytest.raises(RuntimeError, match="must be float32"):
+        weighted_laplace_sum(q.double(), k, torch.randn(1, 8, 4, device=dev))
+    with pytest.raises(RuntimeError, match="fused path pinned but unavailable"):
+        big = torch.randn(1, 1, 5000, device=dev)
+        weighted_abs_sum_full(big, big, torch.randn(1, 5000, 2, device=dev), backend="cuda-fused")
+    with pytest.raises(ValueError, match="no fused path"):
+        weighted_sgn_sum(q, k, torch.randn(1, 8, 4, device=dev), torch.randn(1, 8, 4, device=dev), backend="cuda-fused")
+    with pytest.raises(RuntimeError, match=r"g_w must have shape \(P, M, C\)"):
+        _ext.weighted_abs_sum_backward(q, k, torch.randn(1, 8, 4, device=dev), torch.randn(1, 8, 5, device=dev))
+    # the fused path within its range runs
+    w, u = weighted_abs_sum_full(q, k, torch.randn(1, 8, 4, device=dev), backend="cuda-fused")
+    assert w.shape == (1, 8, 4) and u.shape == (1, 8)
+
+
+def test_non_default_stream_and_repeat(dev):
+    # every launch is on the current stream; repeated calls give identical results up to atomic ordering
+    from weighted_laplace_sum import weighted_laplace_sum
+    q, k, v = _data(2, 4, 700, 600, 64, seed=30)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        w1, u1 = weighted_laplace_sum(tq, tk, tv)
+    s.synchronize()
+    w2, u2 = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v)
+    _assert_rel(_np(w1), ow, nw, "stream out_w")
+    _assert_rel(_np(w2), ow, nw, "default stream out_w")
+    _assert_rel(_np(u1), ou, ou, "stream out_u")

@@ -1,0 +1,247 @@
+"""Pins the CPU oracle (oracle/brute.py) before it is trusted as the parity checker.
+
+The reference ships no tests, fixtures or golden vectors for this path, so every oracle function is pinned by an
+independent formulation, closed forms, invariants and brute force on tiny inputs, each chosen so a plausible mistake
+(a dropped term, a wrong sign or index, a transposed operand, the wrong tie rule) fails at least one check.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute, dense, inputs
+
+
+def _rand(P=2, D=3, N=7, M=5, C=4, seed=0, ties=False):
+    rng = np.random.default_rng(seed)
+    if ties:
+        q = rng.integers(-3, 4, size=(P, D, M)).astype(np.float32) / 2
+        k = rng.integers(-3, 4, size=(P, D, N)).astype(np.float32) / 2
+    else:
+        q = rng.standard_normal((P, D, M)).astype(np.float32)
+        k = rng.standard_normal((P, D, N)).astype(np.float32)
+    v = rng.standard_normal((P, N, C)).astype(np.float32)
+    return q, k, v
+
+
+# ------------------------------------------------------------------------------------------------------- abs sum
+@pytest.mark.parametrize("ties", [False, True])
+@pytest.mark.parametrize("shape", [(2, 3, 7, 5, 4), (1, 1, 1, 1, 1), (3, 2, 9, 13, 3)])
+def test_abs_brute_matches_sorted_prefix_form(shape, ties):
+    P, D, N, M, C = shape
+    q, k, v = _rand(P, D, N, M, C, ties=ties)
+    w, u, _ = brute.abs_sum(q, k, v)
+    w2, u2 = brute.abs_sum_sorted(q, k, v)
+    np.testing.assert_allclose(w, w2, rtol=1e-12, atol=1e-10)
+    np.testing.assert_allclose(u, u2, rtol=1e-12, atol=1e-10)
+
+
+def test_abs_hand_computed():
+    # P=1, D=2, keys (0,2) and (1,-1), queries (1, 0): sum_d |k_d - q_d| per key, times v
+    q = np.array([[[1.0], [0.0]]], dtype=np.float32)               # (1, 2, 1)
+    k = np.array([[[0.0, 2.0], [1.0, -1.0]]], dtype=np.float32)    # (1, 2, 2)
+    v = np.array([[[1.0, 10.0], [2.0, 20.0]]], dtype=np.float32)   # (1, 2, 2)
+    # key 0: |0-1| + |1-0| = 2 ; key 1: |2-1| + |-1-0| = 2
+    w, u, _ = brute.abs_sum(q, k, v)
+    np.testing.assert_allclose(w[0, 0], [2 * 1 + 2 * 2, 2 * 10 + 2 * 20])
+    np.testing.assert_allclose(u[0, 0], 4.0)
+
+
+def test_abs_invariants():
+    q, k, v = _rand(2, 4, 11, 6, 3, seed=3)
+    w, u, _ = brute.abs_sum(q, k, v)
+    # v == 1 -> every channel equals out_u
+    w1, u1, _ = brute.abs_sum(q, k, np.ones_like(v))
+    np.testing.assert_allclose(w1, np.repeat(u1[:, :, None], 3, axis=2), rtol=1e-12)
+    # translation invariance
+    wt, ut, _ = brute.abs_sum(q + 5.0, k + 5.0, v)
+    np.testing.assert_allclose(wt, w, rtol=1e-5, atol=1e-5)
+    # linearity in v
+    w2, _, _ = brute.abs_sum(q, k, 2 * v.astype(np.float64) + 1)
+    np.testing.assert_allclose(w2, 2 * w + w1, rtol=1e-10, atol=1e-9)
+    # symmetry: swapping the roles of q and k transposes the distance matrix
+    A = np.zeros((2, 6, 11))
+    for d in range(4):
+        A += np.abs(q[:, d, :, None].astype(np.float64) - k[:, d, None, :])
+    np.testing.assert_allclose(u, A.sum(axis=2), rtol=1e-12)
+
+
+def test_abs_subsample_matches_full():
+    q, k, v = _rand(2, 3, 20, 17, 5, seed=4)
+    idx = inputs.query_subsample(2, 17, per_p=6, seed=9)
+    w, u, n = brute.abs_sum(q, k, v)
+    ws, us, ns = brute.abs_sum(q, k, v, qidx=idx)
+    for p in range(2):
+        np.testing.assert_allclose(ws[p], w[p][idx[p]])
+        np.testing.assert_allclose(us[p], u[p][idx[p]])
+        np.testing.assert_allclose(ns[p], n[p][idx[p]])
+
+
+# ---------------------------------------------------------------------------------------------------- laplace sum
+@pytest.mark.parametrize("ties", [False, True])
+def test_laplace_brute_matches_recurrence(ties):
+    q, k, v = _rand(2, 3, 9, 7, 3, seed=5, ties=ties)
+    w, u, _ = brute.laplace_sum(q, k, v)
+    w2, u2 = brute.laplace_sum_recurrence(q, k, v)
+    np.testing.assert_allclose(w, w2, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(u, u2, rtol=1e-12, atol=1e-12)
+
+
+def test_laplace_special_cases():
+    # single key: out_u = sum_d exp(-|k_d - q_d|)
+    q = np.array([[[0.5, -1.0], [2.0, 0.0]]], dtype=np.float32)     # (1, 2, 2)
+    k = np.array([[[0.0], [1.0]]], dtype=np.float32)                # (1, 2, 1)
+    v = np.array([[[3.0]]], dtype=np.float32)
+    w, u, _ = brute.laplace_sum(q, k, v)
+    want = np.exp(-np.abs(k[0, :, 0][:, None].astype(np.float64) - q[0])).sum(axis=0)
+    np.testing.assert_allclose(u[0], want, rtol=1e-12)
+    np.testing.assert_allclose(w[0, :, 0], 3.0 * want, rtol=1e-12)
+    # exact ties give exp(0) = 1 per feature
+    qt = np.zeros((1, 3, 1), np.float32)
+    kt = np.zeros((1, 3, 4), np.float32)
+    _, ut, _ = brute.laplace_sum(qt, kt, np.ones((1, 4, 1), np.float32))
+    np.testing.assert_allclose(ut, [[12.0]])
+    # a huge spread underflows to 0, never NaN
+    qf = np.full((1, 1, 1), 1e4, np.float32)
+    kf = np.zeros((1, 1, 2), np.float32)
+    wf, uf, _ = brute.laplace_sum(qf, kf, np.ones((1, 2, 2), np.float32))
+    assert np.all(wf == 0) and np.all(uf == 0) and not np.isnan(wf).any()
+    # v == 1 -> out_w channels == out_u
+    q2, k2, v2 = _rand(2, 3, 6, 5, 2, seed=8)
+    w1, u1, _ = brute.laplace_sum(q2, k2, np.ones_like(v2))
+    np.testing.assert_allclose(w1, np.repeat(u1[:, :, None], 2, axis=2), rtol=1e-12)
+
+
+def test_laplace_padded_key_identity():
+    # a padded key (k = 0, v = 0) adds exp(-|q_d|) per feature to out_u only (__init__.py:12, attention.py:69-71)
+    q, k, v = _rand(1, 3, 5, 4, 2, seed=11)
+    kp = np.concatenate([k, np.zeros((1, 3, 2), np.float32)], axis=2)
+    vp = np.concatenate([v, np.zeros((1, 2, 2), np.float32)], axis=1)
+    w, u, _ = brute.laplace_sum(q, k, v)
+    wp, up, _ = brute.laplace_sum(q, kp, vp)
+    np.testing.assert_allclose(wp, w, rtol=1e-12)
+    np.testing.assert_allclose(up - 2 * np.exp(-np.abs(q[0].astype(np.float64))).sum(axis=0), u, rtol=1e-12)
+
+
+# ------------------------------------------------------------------------------------------------- sgn / backward
+def test_sgn_tie_conventions_by_hand():
+    # one feature, keys (0, 1, 1, 2), query 1 -> keys below: 0; equal: two 1s; above: 2
+    q = np.array([[[1.0]]], np.float32)
+    k = np.array([[[0.0, 1.0, 1.0, 2.0]]], np.float32)
+    v = np.array([[[1.0], [10.0], [100.0], [1000.0]]], np.float32)
+    g = np.ones((1, 1, 1), np.float32)
+    plus, _ = brute.sgn_sum(q, k, v, g, tie=1.0)       # CUDA walk: tie +1
+    zero, _ = brute.sgn_sum(q, k, v, g, tie=0.0)       # keops: tie 0
+    assert plus[0, 0, 0] == -1 + 10 + 100 + 1000
+    assert zero[0, 0, 0] == -1 + 1000
+    (gq, gk, _), _ = brute.abs_backward(q, k, v, g)
+    assert gq[0, 0, 0] == -plus[0, 0, 0]                # sgn op == -grad_q (binding.cpp:383,438)
+    # grad_k[n] = sum_m s(k_n - q_m) <g_m, v_n>, tie -1
+    np.testing.assert_array_equal(gk[0, 0], [-1.0, -10.0, -100.0, 1000.0])
+
+
+def test_sgn_is_negated_grad_q_random():
+    q, k, v = _rand(2, 3, 8, 6, 4, seed=12, ties=True)
+    g = np.random.default_rng(1).standard_normal((2, 6, 4)).astype(np.float32)
+    s, _ = brute.sgn_sum(q, k, v, g, tie=1.0)
+    (gq, _, _), _ = brute.abs_backward(q, k, v, g)
+    np.testing.assert_allclose(s, -gq, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_backward_matches_autograd(full):
+    P, D, N, M, C = 2, 3, 6, 5, 2
+    q, k, v = _rand(P, D, N, M, C, seed=13)
+    rng = np.random.default_rng(2)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32) if full else None
+    tq = torch.tensor(q, dtype=torch.float64, requires_grad=True)
+    tk = torch.tensor(k, dtype=torch.float64, requires_grad=True)
+    tv = torch.tensor(v, dtype=torch.float64, requires_grad=True)
+    d1 = (tq.unsqueeze(3) - tk.unsqueeze(2)).abs().sum(dim=1)      # (P, M, N)
+    loss = ((d1 @ tv) * torch.tensor(g_w, dtype=torch.float64)).sum()
+    if full:
+        loss = loss + (d1.sum(-1) * torch.tensor(g_u, dtype=torch.float64)).sum()
+    loss.backward()
+    (gq, gk, gv), _ = brute.abs_backward(q, k, v, g_w, g_u)
+    np.testing.assert_allclose(gq, tq.grad.numpy(), rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(gk, tk.grad.numpy(), rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(gv, tv.grad.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_dense_forward_gradcheck():
+    # the dense fp64 forward the backward oracle is checked against is itself differentiable-correct (tie-free)
+    P, D, N, M, C = 1, 2, 4, 3, 2
+    q, k, v = _rand(P, D, N, M, C, seed=14)
+    args = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (q, k, v)]
+
+    def f(tq, tk, tv):
+        return dense.dense_abs_sum(tq, tk, tv)
+    assert torch.autograd.gradcheck(f, args)
+
+
+# ------------------------------------------------------------------------------------------------ sort / rank
+def test_stable_sort_matches_python_sort():
+    x = np.array([[1.0, -0.0, 0.0, -1.0, 1.0, 0.0, -0.0, 2.0, -1.0]], np.float32)
+    srt, perm = brute.stable_sort(x)
+    py = sorted(range(x.shape[1]), key=lambda i: (float(x[0, i]), i))   # Python's sort is stable; -0.0 == 0.0
+    np.testing.assert_array_equal(perm[0], py)
+    assert not np.signbit(srt).any() or np.all(srt[np.signbit(srt)] < 0)   # no -0.0 in the output
+
+
+def test_merge_rank_brute_force():
+    rng = np.random.default_rng(3)
+    k = rng.integers(-5, 6, size=(3, 40)).astype(np.float32)
+    q = rng.integers(-6, 7, size=(3, 25)).astype(np.float32)
+    r = brute.merge_rank(q, k)
+    want = (k[:, None, :] < q[:, :, None]).sum(axis=2)
+    np.testing.assert_array_equal(r, want)
+
+
+# ------------------------------------------------------------------------------------------ dense (reference) path
+def test_dense_ops_match_brute():
+    q, k, v = _rand(2, 3, 9, 7, 4, seed=15)
+    tq, tk, tv = (torch.tensor(a, dtype=torch.float64) for a in (q, k, v))
+    w, u = dense.dense_abs_sum(tq, tk, tv)
+    bw, bu, _ = brute.abs_sum(q, k, v)
+    np.testing.assert_allclose(w.numpy(), bw, rtol=1e-12)
+    np.testing.assert_allclose(u.numpy(), bu, rtol=1e-12)
+    w, u = dense.dense_laplace_sum(tq, tk, tv)
+    bw, bu, _ = brute.laplace_sum(q, k, v)
+    np.testing.assert_allclose(w.numpy(), bw, rtol=1e-12)
+    np.testing.assert_allclose(u.numpy(), bu, rtol=1e-12)
+
+
+@pytest.mark.parametrize("kernel", ["add_laplace", "add_riesz", "add_bump"])
+def test_layer_epilogues_match_kernel_matrix(kernel):
+    # attention() over the fast ops (here: the dense ops) equals the normalised naive kernel matrix (attention.py:29)
+    B, H, S, D = 1, 2, 6, 3
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, H, S, D, generator=g, dtype=torch.float64)
+    k = torch.randn(B, H, S, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, H, S, D, generator=g, dtype=torch.float64)
+    tau = dense.TAU[kernel]
+    out = dense.attention(q, k, v, kernel, tau, dense.dense_abs_sum, dense.dense_laplace_sum)
+    P = B * H
+    qq = q.transpose(2, 3).reshape(P, D, S)
+    kk = k.transpose(2, 3).reshape(P, D, S)
+    vv = v.reshape(P, S, D)
+    A = dense.dense_kernel_matrix(kernel, qq, kk, tau)
+    ref = (A @ vv) / A.sum(dim=2, keepdim=True).clamp_min(dense.CLAMP)
+    np.testing.assert_allclose(out.reshape(P, S, D).numpy(), ref.numpy(), rtol=1e-9, atol=1e-9)
+
+
+def test_bump_identity():
+    x = np.linspace(-3, 3, 61)
+    np.testing.assert_allclose(np.maximum(0, 1 - np.abs(x)), np.abs(x + 1) / 2 + np.abs(x - 1) / 2 - np.abs(x),
+                               atol=1e-15)
+
+
+def test_inputs_are_seeded():
+    a = inputs.make(2, 3, 5, 4, 2, seed=0, grads=True)
+    b = inputs.make(2, 3, 5, 4, 2, seed=0, grads=True)
+    for key in a:
+        np.testing.assert_array_equal(a[key], b[key])
+    m = inputs.make(1, 2, 5000, 10, 2, kind="mixture")
+    lv = m["k"][np.abs(m["k"] * 16 - np.round(m["k"] * 16)) == 0]
+    assert lv.size > 0.4 * m["k"].size                   # about half the keys sit on the 256 exact levels
