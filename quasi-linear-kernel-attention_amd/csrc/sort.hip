@@ -50,8 +50,10 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
 
 #pragma unroll 1
     for (int shift = 0; shift < 32; shift += 8) {
-        for (int i = tid; i < WAVES * 256; i += THREADS) hist[i] = 0u;
-        __syncthreads();                                  // previous scatter done, counters cleared
+        // Each wave clears only its own counter row: the previous pass's scatter of this wave (which reads that row)
+        // has already completed in program order, while other waves may still be scattering with their rows.
+        for (int i = lane; i < 256; i += WAVE) hist[wave * 256 + i] = 0u;
+        __syncthreads();                                  // every scatter done, every row cleared
 
         uint32_t key[ITEMS], pk[ITEMS];                   // pk = run index << 16 | offset within the wave's digit
         const int wbase = wave * WAVE * ITEMS;

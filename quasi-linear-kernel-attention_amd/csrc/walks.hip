@@ -251,10 +251,11 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 #pragma unroll
     for (int t = 0; t < RK; ++t) {
         const uint32_t row = bcast(pl, t);
+        const float keep = (t < nk) ? 1.f : 0.f;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = l + WAVE * j;
-            x[t][j] = (c < C) ? vp[(size_t)row * C + c] : 0.f;
+            x[t][j] = (c < C) ? vp[(size_t)row * C + c] * keep : 0.f;
         }
     }
 
