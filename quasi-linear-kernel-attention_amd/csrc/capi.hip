@@ -43,31 +43,52 @@ int check_dims(int P, int D, int N, int M, int C) {
     return QLKA_OK;
 }
 
-// Sorted k and q of every segment, then the range arrays of the walks.
+// Workspace of one call: sorted k and q of every segment, the sort scratch, the range arrays of the walks and, for
+// the row-emitting walks, the per-feature contribution slab (+ the sorted-order v == 1 contributions and the LDS
+// scatter partials when out_u is wanted).
 struct SortedWs {
     float* ks; uint32_t* kp; float* qs; uint32_t* qp;
     void* sort_scratch; RangeArrays ra;
+    float* slab; float* uslab; void* red_scratch;
 };
 
-size_t sorted_ws_bytes(int S, int N, int M, int C, int range_stream_max) {
+struct WsSpec {
+    int P, D, N, M, C;
+    int range_stream_max;   // longest stream a walk runs over (N, or max(N, M) for the backward)
+    int slab_rows;          // queries per feature of the row slab (0: no row emission)
+    bool want_u;            // v == 1 contributions (out_u)
+};
+
+size_t ws_part(const WsSpec& w, int i) {
+    const size_t S = (size_t)w.P * w.D;
+    switch (i) {
+        case 0: case 1: return align256(S * w.N * 4);
+        case 2: case 3: return align256(S * w.M * 4);
+        case 4: return align256(std::max(seg_sort_scratch_bytes((int)S, w.N), seg_sort_scratch_bytes((int)S, w.M)));
+        case 5: return align256(range_arrays_bytes((int)S, w.range_stream_max, w.C));
+        case 6: return w.slab_rows ? align256(S * w.slab_rows * (size_t)slab_stride(w.C) * 4) : 0;
+        case 7: return (w.slab_rows && w.want_u) ? align256(S * w.slab_rows * 4) : 0;
+        case 8: return (w.slab_rows && w.want_u) ? align256(reduce_scratch_bytes(w.P, w.D, w.slab_rows)) : 0;
+    }
+    return 0;
+}
+
+size_t ws_bytes(const WsSpec& w) {
     size_t b = 0;
-    b += 2 * align256((size_t)S * N * 4);
-    b += 2 * align256((size_t)S * M * 4);
-    b += align256(std::max(seg_sort_scratch_bytes(S, N), seg_sort_scratch_bytes(S, M)));
-    b += align256(range_arrays_bytes(S, range_stream_max, C));
+    for (int i = 0; i < 9; ++i) b += ws_part(w, i);
     return b;
 }
 
-SortedWs carve_sorted(void* ws, int S, int N, int M, int C, int range_stream_max) {
+SortedWs carve(void* ws, const WsSpec& w) {
     char* b = (char*)ws;
-    SortedWs w;
-    w.ks = (float*)b;    b += align256((size_t)S * N * 4);
-    w.kp = (uint32_t*)b; b += align256((size_t)S * N * 4);
-    w.qs = (float*)b;    b += align256((size_t)S * M * 4);
-    w.qp = (uint32_t*)b; b += align256((size_t)S * M * 4);
-    w.sort_scratch = b;  b += align256(std::max(seg_sort_scratch_bytes(S, N), seg_sort_scratch_bytes(S, M)));
-    w.ra = carve_range_arrays(b, S, range_stream_max, C);
-    return w;
+    char* part[9];
+    for (int i = 0; i < 9; ++i) { part[i] = b; b += ws_part(w, i); }
+    SortedWs r;
+    r.ks = (float*)part[0]; r.kp = (uint32_t*)part[1]; r.qs = (float*)part[2]; r.qp = (uint32_t*)part[3];
+    r.sort_scratch = part[4];
+    r.ra = carve_range_arrays(part[5], w.P * w.D, w.range_stream_max, w.C);
+    r.slab = (float*)part[6]; r.uslab = (float*)part[7]; r.red_scratch = part[8];
+    return r;
 }
 
 int check_ws(void* ws, size_t have, size_t need) {
@@ -93,36 +114,40 @@ const char* qlka_last_error(void) { return g_err.c_str(); }
 int qlka_version(void) { return 1; }
 
 // ------------------------------------------------------------------------------------------------ laplace forward
+static WsSpec laplace_spec(int P, int D, int N, int M, int C) { return WsSpec{P, D, N, M, C, N, M, true}; }
+
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return sorted_ws_bytes(P * D, N, M, C, N);
+    return ws_bytes(laplace_spec(P, D, N, M, C));
 }
 
 int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
-                     int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream) {
+                     int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !out_w || !out_u) return fail(QLKA_EINVAL, "q, k, v, out_w and out_u must be non-null");
-    if (int e = check_ws(ws, ws_bytes, qlka_laplace_fwd_ws_bytes(P, D, N, M, C))) return e;
+    const WsSpec spec = laplace_spec(P, D, N, M, C);
+    if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
     const int S = P * D;
-    SortedWs w = carve_sorted(ws, S, N, M, C, N);
+    SortedWs w = carve(ws, spec);
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
-    int e = fill_zero(out_w, (size_t)P * M * C, st);
-    if (!e) e = fill_zero(out_u, (size_t)P * M, st);
-    if (e) return hip_status(e, "zeroing outputs");
-    e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, out_w, out_u, P, D, N, M, C, w.ra, st);
-    return hip_status(e, "laplace walk");
+    int e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+    if (e) return hip_status(e, "laplace walk");
+    e = reduce_slabs(w.slab, w.uslab, w.qp, out_w, out_u, P, D, M, C, w.red_scratch, st);
+    return hip_status(e, "laplace reduce");
 }
 
 // ---------------------------------------------------------------------------------------------------- abs forward
+static WsSpec abs_fwd_spec(int P, int D, int N, int M, int C, bool full) { return WsSpec{P, D, N, M, C, N, M, full}; }
+
 size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return sorted_ws_bytes(P * D, N, M, C, N);
+    return ws_bytes(abs_fwd_spec(P, D, N, M, C, true));
 }
 
 int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
-                 int P, int D, int N, int M, int C, int path, void* ws, size_t ws_bytes, void* stream) {
+                 int P, int D, int N, int M, int C, int path, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (path < -1 || path > 1) return fail(QLKA_EINVAL, "path must be -1 (auto), 0 (global) or 1 (fused)");
@@ -131,40 +156,47 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
     if (path == 1 && std::max(N, M) > 4096)
         return fail(QLKA_EINVAL, "fused path pinned but unavailable: needs max(N,M) <= 4096 and the "
                                  "bucket's shared memory to fit this device");
-    if (int e = check_ws(ws, ws_bytes, qlka_abs_fwd_ws_bytes(P, D, N, M, C))) return e;
+    // the workspace is sized for the _full op (an upper bound of the plain one), so one size serves both
+    const WsSpec spec = abs_fwd_spec(P, D, N, M, C, true);
+    if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
     const int S = P * D;
-    SortedWs w = carve_sorted(ws, S, N, M, C, N);
+    SortedWs w = carve(ws, spec);
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
-    int e = fill_zero(out_w, (size_t)P * M * C, st);
-    if (!e && out_u) e = fill_zero(out_u, (size_t)P * M, st);
-    if (e) return hip_status(e, "zeroing outputs");
     AbsWalkArgs a{};
     a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
     a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
-    a.out_row = out_w; a.out_u = out_u; a.out_dot = nullptr; a.out_rank = nullptr;
+    a.slab = w.slab; a.uslab = out_u ? w.uslab : nullptr; a.CR = slab_stride(C);
+    a.out_dot = nullptr; a.out_rank = nullptr;
     a.sign = 1.f; a.P = P; a.D = D; a.C = C;
-    e = abs_walk(a, out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW, w.ra, st);
-    return hip_status(e, "abs walk");
+    int e = abs_walk(a, out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW, w.ra, st);
+    if (e) return hip_status(e, "abs walk");
+    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, out_w, out_u, P, D, M, C, w.red_scratch, st);
+    return hip_status(e, "abs reduce");
 }
 
 // --------------------------------------------------------------------------------------------------- abs backward
+static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
+    return WsSpec{P, D, N, M, C, std::max(N, M), N, false};   // the grad_v slab has one row per key
+}
+
 size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return sorted_ws_bytes(P * D, N, M, C, std::max(N, M));
+    return ws_bytes(abs_bwd_spec(P, D, N, M, C));
 }
 
 int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
                  float* grad_q, float* grad_k, float* grad_v,
-                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream) {
+                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
         return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
-    if (int e = check_ws(ws, ws_bytes, qlka_abs_bwd_ws_bytes(P, D, N, M, C))) return e;
+    const WsSpec spec = abs_bwd_spec(P, D, N, M, C);
+    if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
     const int S = P * D;
-    SortedWs w = carve_sorted(ws, S, N, M, C, std::max(N, M));
+    SortedWs w = carve(ws, spec);
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
 
     // grad_q: stream = sorted k with rows v, queries = q, dotted with g_w (+ g_u * (2 rank - N))
@@ -176,31 +208,32 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
     if (e) return hip_status(e, "grad_q walk");
 
     // grad_k and grad_v: stream = sorted q with rows g_w (+ scalars g_u), queries = k
-    e = fill_zero(grad_v, (size_t)P * N * C, st);
-    if (e) return hip_status(e, "zeroing grad_v");
     AbsWalkArgs b{};
     b.ks = w.qs; b.kp = w.qp; b.Ns = M; b.w = g_w; b.u = g_u;
     b.qs = w.ks; b.qp = w.kp; b.Mq = N; b.g = v; b.uq = nullptr;
-    b.out_row = grad_v; b.out_dot = grad_k; b.sign = 1.f; b.P = P; b.D = D; b.C = C;
+    b.slab = w.slab; b.uslab = nullptr; b.CR = slab_stride(C);
+    b.out_dot = grad_k; b.sign = 1.f; b.P = P; b.D = D; b.C = C;
     e = abs_walk(b, g_u ? (ABS_ROW | ABS_DOT | ABS_DOTX2) : (ABS_ROW | ABS_DOT), w.ra, st);
-    return hip_status(e, "grad_k/grad_v walk");
+    if (e) return hip_status(e, "grad_k/grad_v walk");
+    e = reduce_slabs(w.slab, nullptr, w.kp, grad_v, nullptr, P, D, N, C, w.red_scratch, st);
+    return hip_status(e, "grad_v reduce");
 }
 
 // -------------------------------------------------------------------------------------------------------- sgn sum
 size_t qlka_sgn_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return sorted_ws_bytes(P * D, N, M, C, N);
+    return ws_bytes(WsSpec{P, D, N, M, C, N, 0, false});
 }
 
 int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g, float* out,
-                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream) {
+                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g || !out) return fail(QLKA_EINVAL, "q, k, v, g and out must be non-null");
-    if (int e = check_ws(ws, ws_bytes, qlka_sgn_fwd_ws_bytes(P, D, N, M, C))) return e;
+    if (int e = check_ws(ws, ws_bytes_given, qlka_sgn_fwd_ws_bytes(P, D, N, M, C))) return e;
     hipStream_t st = (hipStream_t)stream;
     const int S = P * D;
-    SortedWs w = carve_sorted(ws, S, N, M, C, N);
+    SortedWs w = carve(ws, WsSpec{P, D, N, M, C, N, 0, false});
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
     AbsWalkArgs a{};
     a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v;
@@ -228,17 +261,17 @@ int qlka_seg_sort(const float* keys, float* sorted, uint32_t* perm, int num_segs
 
 size_t qlka_merge_rank_ws_bytes(int num_segs, int N, int M) {
     if (num_segs <= 0 || N <= 0 || M <= 0) return 0;
-    return sorted_ws_bytes(num_segs, N, M, 1, N);
+    return ws_bytes(WsSpec{num_segs, 1, N, M, 1, N, 0, false});
 }
 
 int qlka_merge_rank(const float* q, const float* k, int32_t* rank, int num_segs, int N, int M,
-                    void* ws, size_t ws_bytes, void* stream) {
+                    void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(num_segs, 1, N, M, 1)) return e;
     if (!q || !k || !rank) return fail(QLKA_EINVAL, "q, k and rank must be non-null");
-    if (int e = check_ws(ws, ws_bytes, qlka_merge_rank_ws_bytes(num_segs, N, M))) return e;
+    if (int e = check_ws(ws, ws_bytes_given, qlka_merge_rank_ws_bytes(num_segs, N, M))) return e;
     hipStream_t st = (hipStream_t)stream;
-    SortedWs w = carve_sorted(ws, num_segs, N, M, 1, N);
+    SortedWs w = carve(ws, WsSpec{num_segs, 1, N, M, 1, N, 0, false});
     if (int e = sort_both(q, k, w, num_segs, N, M, st)) return e;
     AbsWalkArgs a{};
     a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = nullptr;

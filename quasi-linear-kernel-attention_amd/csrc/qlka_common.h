@@ -37,6 +37,10 @@ __device__ __forceinline__ float ordered_to_float(uint32_t u) {
 // ---------------------------------------------------------------------------------------------------------------
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (WAVE - 1)); }
 
+// Index of this wave inside its workgroup, as a value the compiler knows is wave-uniform (so everything derived from
+// it lives in SGPRs and buffer descriptors need no waterfall loop).
+__device__ __forceinline__ int wave_in_block() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE)); }
+
 // value of x in lane `src` (src must be wave-uniform); lowers to v_readlane_b32
 __device__ __forceinline__ float bcast(float x, int src) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));
@@ -106,6 +110,22 @@ __device__ __forceinline__ int wave_upper_bound(const float* __restrict__ a, int
         lo = nlo; hi = nhi;
     }
     return lo;
+}
+
+// Raw buffer access with a uniform base (descriptor) + SGPR offset + per-lane VGPR offset: the per-row part of an
+// address stays in SGPRs, so a row gather/store costs no per-lane address arithmetic and rewrites no address VGPRs.
+// `bytes` bounds the descriptor (out-of-range lanes read 0 / drop their store); every caller's region is < 4 GB.
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000;     // raw 32-bit dword access, gfx9-family descriptor format
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, RSRC_WORD3);
+}
+__device__ __forceinline__ float buf_load(rsrc_t r, int voff, int soff) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ void buf_store(float x, rsrc_t r, int voff, int soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 0);
 }
 
 // Relaxed agent-scope fp32 add with no return value (lowers to global_atomic_add_f32 without glc).

@@ -34,8 +34,13 @@ __host__ __device__ inline int range_keys(int C) { return C <= 64 ? 64 : 32; }
 // Floats per range row in the range arrays (C channels + 2 scalar extras).
 __host__ __device__ inline int range_stride(int C) { return C + 2; }
 
+// Per-range arrays of the walks. The sums kernel writes the summaries (sa, sb); the scan reads them and writes the
+// entry/exit states (ta, tb) to separate arrays: a kernel never reads memory it also writes (a uniform-address read
+// may become a scalar load that the compiler treats as invariant and moves past the kernel's own vector stores).
 struct RangeArrays {
-    float* ta;   // [S][G+1][stride]
+    float* sa;   // [S][G+1][stride] range summaries
+    float* sb;   // [S][G+1][stride]
+    float* ta;   // [S][G+1][stride] range states (written by the scan)
     float* tb;   // [S][G+1][stride]
     int*   qb;   // [S][G]
 };
@@ -45,14 +50,24 @@ RangeArrays carve_range_arrays(void* base, int S, int Nstream, int C);
 // Fill n floats with zero (a kernel, so it can sit inside a captured graph).
 int fill_zero(float* p, size_t n, hipStream_t st);
 
-// out_w[p,m,c] += sum_{d,n} exp(-|k - q|) v[p,n,c];  out_u[p,m] += sum_{d,n} exp(-|k - q|)
+// Row stride (floats) of the per-feature contribution slab: C rounded up to whole 128-byte lines.
+__host__ __device__ inline int slab_stride(int C) { return (C + 31) / 32 * 32; }
+
+// Per feature d of p: slab[(p*D + d)*M + m][c] = sum_n exp(-|k_n - q_m|) v[p,n,c] (row stride slab_stride(C)),
+// uslab[(p*D + d)*M + i] = sum_n exp(-|k_n - q_(i)|) for the i-th smallest query of the feature.
 int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 float* out_w, float* out_u, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st);
+                 float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st);
+
+// D-reduction of the slabs: out[p,m,c] = sum_d slab[(p*D+d)*M + m][c]; out_u[p,m] = sum_d uslab contribution of m
+// (scattered through LDS windows by the sorted-order permutation qp). out_u / uslab may be null.
+size_t reduce_scratch_bytes(int P, int D, int M);
+int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qp, float* out, float* out_u,
+                 int P, int D, int M, int C, void* scratch, hipStream_t st);
 
 // Emission modes of the abs-family walk (bit set).
 enum AbsMode : int {
-    ABS_ROW   = 1,    // out_row[p, m, :] += sum_n |k_n - q_m| w_n            (atomics)
-    ABS_ONES  = 2,    // out_u[p, m]      += sum_n |k_n - q_m|                (atomics)
+    ABS_ROW   = 1,    // slab[(p,d), m, :] = sum_n |k_n - q_m| w_n            (row store)
+    ABS_ONES  = 2,    // uslab[(p,d), i]   = sum_n |k_n - q_(i)|, sorted order (store)
     ABS_DOT   = 4,    // out_dot[s, m]     = sign * sum_n s(q_m - k_n) <w_n, g_m>, s(0) = -1   (store)
     ABS_DOTX1 = 8,    //   ... + uq[p, m] * (2 rank - Ns)
     ABS_DOTX2 = 16,   //   ... + sum_n s(q_m - k_n) u_n
@@ -68,8 +83,9 @@ struct AbsWalkArgs {
     const float* qs; const uint32_t* qp; int Mq;
     const float* g;          // (P, Mq, C) rows dotted at emission (ABS_DOT) or null
     const float* uq;         // (P, Mq) (ABS_DOTX1) or null
-    float* out_row;          // (P, Mq, C)
-    float* out_u;            // (P, Mq)
+    float* slab;             // (P*D, Mq, CR) per-feature contribution rows (ABS_ROW)
+    float* uslab;            // (P*D, Mq) per-feature v == 1 contributions in sorted order (ABS_ONES)
+    int CR;                  // slab row stride
     float* out_dot;          // (P, D, Mq)
     int32_t* out_rank;       // (P, D, Mq)
     float sign;

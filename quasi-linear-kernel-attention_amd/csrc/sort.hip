@@ -41,10 +41,11 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
     const int lane = tid & (WAVE - 1);
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (WAVE - lane));
 
-    for (int i = tid; i < CAP; i += THREADS) {
-        uint32_t u = 0xffffffffu;                         // pads sort after every finite or infinite key
-        if (i < len) u = float_to_ordered(src[i]);
-        skey[i] = u;
+#pragma unroll
+    for (int r = 0; r < ITEMS; ++r) {
+        const int i = tid + r * THREADS;
+        const float f = src[min(i, len - 1)];             // unconditional (clamped) load: all ITEMS stay in flight
+        skey[i] = (i < len) ? float_to_ordered(f) : 0xffffffffu;   // pads sort after every finite or infinite key
         sidx[i] = (uint32_t)i;                            // index inside the run (< 16384)
     }
 

@@ -42,7 +42,7 @@ size_t range_arrays_bytes(int S, int Ns, int C) {
     const int RK = range_keys(C);
     const size_t G = (size_t)((Ns + RK - 1) / RK);
     const size_t rows = (size_t)S * (G + 1);
-    return 2 * align256(rows * range_stride(C) * sizeof(float)) + align256((size_t)S * G * sizeof(int));
+    return 4 * align256(rows * range_stride(C) * sizeof(float)) + align256((size_t)S * G * sizeof(int));
 }
 
 RangeArrays carve_range_arrays(void* base, int S, int Ns, int C) {
@@ -51,6 +51,8 @@ RangeArrays carve_range_arrays(void* base, int S, int Ns, int C) {
     const size_t rows = (size_t)S * (G + 1);
     char* b = (char*)base;
     RangeArrays r;
+    r.sa = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
+    r.sb = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
     r.ta = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
     r.tb = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
     r.qb = (int*)b;
@@ -76,6 +78,21 @@ int fill_zero(float* p, size_t n, hipStream_t st) {
     return (int)hipGetLastError();
 }
 
+// Rank of query value q among the first nk (<= RK) keys of the range held one per lane in kl (ascending):
+// #{t < nk : k_t < q}, in [0, nk]. Branch-free binary search over lane shuffles, valid for any per-lane q.
+template <int RK>
+__device__ __forceinline__ int range_rank(const float kl, const int nk, const float q) {
+    int pos = 0;
+#pragma unroll
+    for (int step = RK / 2; step >= 1; step >>= 1) {
+        const float kv = __shfl(kl, pos + step - 1, WAVE);
+        if (pos + step <= nk && kv < q) pos += step;
+    }
+    const float kv = __shfl(kl, min(pos, RK - 1), WAVE);
+    if (pos < nk && kv < q) ++pos;
+    return pos;
+}
+
 // =================================================================================================================
 // Laplace
 // =================================================================================================================
@@ -86,9 +103,9 @@ template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
 void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
                     const float* __restrict__ v, float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
-                    const int S, const int D, const int N, const int M, const int C, const int G)
+                    const int S, const int D, const int N, const int M, const int C, const int G)  // ta/tb: summaries
 {
-    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    const long wv = (long)blockIdx.x * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / D, l = lane_id();
@@ -103,7 +120,7 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
     const float wl = real ? __expf(-(klast - kl)) : 0.f;
     const float wr = real ? __expf(-(kl - kfirst)) : 0.f;
 
-    const float* vp = v + (size_t)p * N * C;
+    const rsrc_t vr = make_rsrc(v + (size_t)p * N * C, (uint32_t)((size_t)N * C * 4));
     float sl[NV], sr[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) { sl[j] = 0.f; sr[j] = 0.f; }
@@ -114,7 +131,8 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = l + WAVE * j;
-            const float x = (c < C) ? vp[(size_t)row * C + c] : 0.f;
+            const float xr = buf_load(vr, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
+            const float x = (c < C) ? xr : 0.f;
             sl[j] += a * x;
             sr[j] += b * x;
         }
@@ -139,14 +157,16 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 // it), in place. One wave per segment walks its G ranges; rows are prefetched in batches of 8.
 template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
-void lap_range_scan(const float* __restrict__ ks, float* __restrict__ ta, float* __restrict__ tb,
-                    const int S, const int N, const int C, const int G)
+void lap_range_scan(const float* __restrict__ ks, const float* __restrict__ sa, const float* __restrict__ sb,
+                    float* __restrict__ ta, float* __restrict__ tb, const int S, const int N, const int C, const int G)
 {
-    const int s = blockIdx.x * WPB + threadIdx.x / WAVE;
+    const int s = blockIdx.x * WPB + wave_in_block();
     if (s >= S) return;
     const int l = lane_id();
     const int CS = range_stride(C);
     const float* kseg = ks + (size_t)s * N;
+    const float* SA = sa + (size_t)s * (G + 1) * CS;
+    const float* SB = sb + (size_t)s * (G + 1) * CS;
     float* A = ta + (size_t)s * (G + 1) * CS;
     float* B = tb + (size_t)s * (G + 1) * CS;
     constexpr int BATCH = 8;
@@ -164,9 +184,9 @@ void lap_range_scan(const float* __restrict__ ks, float* __restrict__ ta, float*
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int c = l + WAVE * j;
-                a[b][j] = (c < C) ? A[(size_t)g * CS + c] : 0.f;
+                a[b][j] = SA[(size_t)g * CS + min(c, C - 1)];
             }
-            a[b][NV] = A[(size_t)g * CS + C];
+            a[b][NV] = SA[(size_t)g * CS + C];
             kk[b] = kseg[min(N, (g + 1) * RK) - 1];
         }
 #pragma unroll
@@ -197,9 +217,9 @@ void lap_range_scan(const float* __restrict__ ks, float* __restrict__ ta, float*
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int c = l + WAVE * j;
-                b_[b][j] = (c < C) ? B[(size_t)g * CS + c] : 0.f;
+                b_[b][j] = SB[(size_t)g * CS + min(c, C - 1)];
             }
-            b_[b][NV] = B[(size_t)g * CS + C];
+            b_[b][NV] = SB[(size_t)g * CS + C];
             kk[b] = kseg[g * RK];
         }
 #pragma unroll
@@ -225,10 +245,10 @@ __global__ __launch_bounds__(WPB * WAVE)
 void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
                     const uint32_t* __restrict__ qp, const float* __restrict__ v,
                     const float* __restrict__ ta, const float* __restrict__ tb, const int* __restrict__ qb,
-                    float* __restrict__ out_w, float* __restrict__ out_u,
-                    const int S, const int D, const int N, const int M, const int C, const int G)
+                    float* __restrict__ slab, float* __restrict__ uslab,
+                    const int S, const int D, const int N, const int M, const int C, const int CR, const int G)
 {
-    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    const long wv = (long)blockIdx.x * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / D, l = lane_id();
@@ -246,7 +266,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
     const float kafter  = has_next ? kseg[base + RK] : 0.f;
 
     // value rows of the range (pads: zero rows, keys equal to the last real key)
-    const float* vp = v + (size_t)p * N * C;
+    const rsrc_t vr = make_rsrc(v + (size_t)p * N * C, (uint32_t)((size_t)N * C * 4));
     float x[RK][NV];
 #pragma unroll
     for (int t = 0; t < RK; ++t) {
@@ -255,7 +275,8 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = l + WAVE * j;
-            x[t][j] = (c < C) ? vp[(size_t)row * C + c] * keep : 0.f;
+            const float xr = buf_load(vr, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
+            x[t][j] = (c < C) ? xr * keep : 0.f;
         }
     }
 
@@ -266,8 +287,8 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = l + WAVE * j;
-        L[j]  = (c < C) ? ra[c] : 0.f;
-        Rx[j] = (c < C) ? rb[c] : 0.f;
+        L[j]  = (c < C) ? ra[min(c, C - 1)] : 0.f;
+        Rx[j] = (c < C) ? rb[min(c, C - 1)] : 0.f;
     }
     const float L1in = ra[C], R1out = rb[C];
 
@@ -287,7 +308,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
     wave_affine_scan_bwd(a2, b2);
     const float r1 = a2 * R1out + b2;
 
-    // R_t for all keys of the range, backwards from the exit state; overwrites nothing, x is still needed for L
+    // R_t for all keys of the range, backwards from the exit state; x is still needed for L
     float R[RK][NV];
 #pragma unroll
     for (int t = RK - 1; t >= 0; --t) {
@@ -296,71 +317,69 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
         for (int j = 0; j < NV; ++j) R[t][j] = x[t][j] + dn * (t == RK - 1 ? Rx[j] : R[t + 1][j]);
     }
 
-    // owned queries [q0, q1) of the sorted queries
+    // Owned queries [q0, q1) of the sorted queries, in blocks of 64. Per block, lane i first takes query i and
+    // computes its rank t inside the range and its two decay factors (one v_exp each for all 64 queries); then the
+    // wave walks the keys with lane = channel and writes each query's contribution row.
     const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
     const int q1 = has_next ? qb[(size_t)s * G + g] : M;
-    int qi = q0, qbase = q0;
-    float qbuf = (q0 + l < q1) ? qseg[q0 + l] : 0.f;
-    uint32_t pbuf = (q0 + l < q1) ? qpseg[q0 + l] : 0u;
+    // this segment's contribution rows (indexed by query) and v == 1 contributions (sorted order)
+    const rsrc_t sr_ = make_rsrc(slab + (size_t)s * M * CR, (uint32_t)((size_t)M * CR * 4));
+    float* useg = uslab + (size_t)s * M;
 
-    float* ow = out_w + (size_t)p * M * C;
-    float* ou = out_u + (size_t)p * M;
-    float kprev = kbefore, l1cur = L1in;
-    bool left = has_prev;
+    for (int qb0 = q0; qb0 < q1; qb0 += WAVE) {
+        const int nq = min(WAVE, q1 - qb0);
+        const bool act = l < nq;
+        const int qi = min(qb0 + l, q1 - 1);              // clamped: unconditional loads
+        const float qv = qseg[qi];
+        const uint32_t mq = qpseg[qi];
+        const int t = range_rank<RK>(kl, nk, qv);
+        const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
+        const float knv = __shfl(kl, min(t, RK - 1), WAVE);
+        const float l1p = __shfl(l1, max(t - 1, 0), WAVE);
+        const float r1n = __shfl(r1, min(t, RK - 1), WAVE);
+        const bool lft = t > 0 || has_prev;
+        const float eL = lft ? __expf(-(qv - (t > 0 ? kpv : kbefore))) : 0.f;
+        const float eR = (t < nk) ? __expf(-(knv - qv)) : 0.f;
+        if (act) useg[qb0 + l] = eL * (t > 0 ? l1p : L1in) + eR * r1n;
+        // byte offset of each query's slab row, computed here so no load result is first used inside the store loop
+        // (vmcnt also counts stores: a late first use of a load would wait for every store issued before it)
+        const int rowoff = (int)(mq * CR * 4);
 
+        float Lc[NV];
 #pragma unroll
-    for (int t = 0; t < RK; ++t) {
-        const float kt = bcast(kl, t);
-        const float r1t = bcast(r1, t);
-        while (qi < q1) {
-            if (qi - qbase == WAVE) {
-                qbase = qi;
-                qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
-                pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
+        for (int jj = 0; jj < NV; ++jj) Lc[jj] = L[jj];
+        int j = 0;
+#pragma unroll
+        for (int tt = 0; tt < RK; ++tt) {
+            const int cnt = __popcll(__ballot(act && t == tt));
+            for (int r = 0; r < cnt; ++r, ++j) {
+                const float el = bcast(eL, j), er = bcast(eR, j);
+                const int so = bcast(rowoff, j);
+#pragma unroll
+                for (int jj = 0; jj < NV; ++jj) {
+                    const int c = l + WAVE * jj;
+                    if (c < C) buf_store(el * Lc[jj] + er * R[tt][jj], sr_, c * 4, so);
+                }
             }
-            const float qv = bcast(qbuf, qi - qbase);
-            if (!(qv <= kt)) break;
-            const uint32_t m = bcast(pbuf, qi - qbase);
-            const float eL = left ? __expf(-(qv - kprev)) : 0.f;
-            const float eR = __expf(-(kt - qv));
+            const float dp = bcast(dprev, tt);
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                if (c < C) atomic_add_f32(ow + (size_t)m * C + c, eL * L[j] + eR * R[t][j]);
+            for (int jj = 0; jj < NV; ++jj) Lc[jj] = dp * Lc[jj] + x[tt][jj];
+        }
+        for (; j < nq; ++j) {                         // rank RK: above every key of a full last range
+            const float el = bcast(eL, j);
+            const int so = bcast(rowoff, j);
+#pragma unroll
+            for (int jj = 0; jj < NV; ++jj) {
+                const int c = l + WAVE * jj;
+                if (c < C) buf_store(el * Lc[jj], sr_, c * 4, so);
             }
-            if (l == 0) atomic_add_f32(ou + m, eL * l1cur + eR * r1t);
-            ++qi;
         }
-        const float dp = bcast(dprev, t);
-#pragma unroll
-        for (int j = 0; j < NV; ++j) L[j] = dp * L[j] + x[t][j];
-        l1cur = bcast(l1, t);
-        kprev = kt;
-        left = true;
-    }
-    // queries above every key (rank N): only the last range owns them, and they have no right side
-    while (qi < q1) {
-        if (qi - qbase == WAVE) {
-            qbase = qi;
-            qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
-            pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
-        }
-        const float qv = bcast(qbuf, qi - qbase);
-        const uint32_t m = bcast(pbuf, qi - qbase);
-        const float eL = __expf(-(qv - kprev));
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int c = l + WAVE * j;
-            if (c < C) atomic_add_f32(ow + (size_t)m * C + c, eL * L[j]);
-        }
-        if (l == 0) atomic_add_f32(ou + m, eL * l1cur);
-        ++qi;
     }
 }
 
 template <int NV, int RK>
 static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                          float* out_w, float* out_u, int P, int D, int N, int M, int C, RangeArrays ra,
+                          float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
                           hipStream_t st) {
     const int S = P * D;
     const int G = (N + RK - 1) / RK;
@@ -369,25 +388,25 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
     {
         StageTimer t("lap_range_sums", st);
         hipLaunchKernelGGL((lap_range_sums<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                           ks, kp, qs, v, ra.ta, ra.tb, ra.qb, S, D, N, M, C, G);
+                           ks, kp, qs, v, ra.sa, ra.sb, ra.qb, S, D, N, M, C, G);
     }
     {
         StageTimer t("lap_range_scan", st);
         hipLaunchKernelGGL((lap_range_scan<NV, RK>), dim3((S + WPB - 1) / WPB), dim3(WPB * WAVE), 0, st,
-                           ks, ra.ta, ra.tb, S, N, C, G);
+                           ks, ra.sa, ra.sb, ra.ta, ra.tb, S, N, C, G);
     }
     {
         StageTimer t("lap_range_walk", st);
         hipLaunchKernelGGL((lap_range_walk<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                           ks, kp, qs, qp, v, ra.ta, ra.tb, ra.qb, out_w, out_u, S, D, N, M, C, G);
+                           ks, kp, qs, qp, v, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C), G);
     }
     return (int)hipGetLastError();
 }
 
 int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 float* out_w, float* out_u, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st) {
-    if (C <= WAVE) return laplace_walk_t<1, 64>(ks, kp, qs, qp, v, out_w, out_u, P, D, N, M, C, ra, st);
-    return laplace_walk_t<2, 32>(ks, kp, qs, qp, v, out_w, out_u, P, D, N, M, C, ra, st);
+                 float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st) {
+    if (C <= WAVE) return laplace_walk_t<1, 64>(ks, kp, qs, qp, v, slab, uslab, P, D, N, M, C, ra, st);
+    return laplace_walk_t<2, 32>(ks, kp, qs, qp, v, slab, uslab, P, D, N, M, C, ra, st);
 }
 
 // =================================================================================================================
@@ -403,7 +422,7 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
                     const int S, const int D, const int Ns, const int Mq, const int C, const int G)
 {
-    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    const long wv = (long)blockIdx.x * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / D, l = lane_id();
@@ -417,7 +436,7 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
     const bool real = l < nk;
     const float dl = real ? (klast - kl) : 0.f;
 
-    const float* wp = w + (size_t)p * Ns * C;
+    const rsrc_t wr_ = make_rsrc(w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
     float sw[NV], sb[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) { sw[j] = 0.f; sb[j] = 0.f; }
@@ -429,14 +448,21 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = l + WAVE * j;
-            const float xv = (WANT_W && c < C) ? wp[(size_t)row * C + c] * keep : 0.f;
+            float xv = 0.f;
+            if constexpr (WANT_W) {
+                const float xr = buf_load(wr_, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
+                xv = (c < C) ? xr * keep : 0.f;
+            }
             sw[j] += xv;
             sb[j] += dt * xv;
         }
     }
     const float b1 = wave_sum(dl);
     float u1 = 0.f;
-    if constexpr (WANT_U) u1 = wave_sum(real ? u[(size_t)p * Ns + pl] : 0.f);
+    if constexpr (WANT_U) {
+        const float ur = u[(size_t)p * Ns + pl];
+        u1 = wave_sum(real ? ur : 0.f);
+    }
 
     const int CS = range_stride(C);
     float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
@@ -456,14 +482,16 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 // (Wtot, Btot relative to k_max; Utot, B1tot) in row G.
 template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
-void abs_range_scan(const float* __restrict__ ks, float* __restrict__ ta, float* __restrict__ tb,
-                    const int S, const int Ns, const int C, const int G)
+void abs_range_scan(const float* __restrict__ ks, const float* __restrict__ sa, const float* __restrict__ sb,
+                    float* __restrict__ ta, float* __restrict__ tb, const int S, const int Ns, const int C, const int G)
 {
-    const int s = blockIdx.x * WPB + threadIdx.x / WAVE;
+    const int s = blockIdx.x * WPB + wave_in_block();
     if (s >= S) return;
     const int l = lane_id();
     const int CS = range_stride(C);
     const float* kseg = ks + (size_t)s * Ns;
+    const float* SA = sa + (size_t)s * (G + 1) * CS;
+    const float* SB = sb + (size_t)s * (G + 1) * CS;
     float* A = ta + (size_t)s * (G + 1) * CS;
     float* B = tb + (size_t)s * (G + 1) * CS;
     constexpr int BATCH = 8;
@@ -480,11 +508,11 @@ void abs_range_scan(const float* __restrict__ ks, float* __restrict__ ta, float*
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
                 const int c = l + WAVE * j;
-                a[b][j]  = (c < C) ? A[(size_t)g * CS + c] : 0.f;
-                b_[b][j] = (c < C) ? B[(size_t)g * CS + c] : 0.f;
+                a[b][j]  = SA[(size_t)g * CS + min(c, C - 1)];   // unconditional; lanes >= C never stored
+                b_[b][j] = SB[(size_t)g * CS + min(c, C - 1)];
             }
-            a[b][NV]  = A[(size_t)g * CS + C];
-            b_[b][NV] = B[(size_t)g * CS + C];
+            a[b][NV]  = SA[(size_t)g * CS + C];
+            b_[b][NV] = SB[(size_t)g * CS + C];
             kk[b] = kseg[min(Ns, (g + 1) * RK) - 1];
         }
 #pragma unroll
@@ -524,7 +552,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     constexpr bool NEED_B = ROW || ONES;
     constexpr bool NEED_W = ROW || DOT;
     const int S = a.P * a.D, C = a.C, Ns = a.Ns, Mq = a.Mq;
-    const long wv = (long)blockIdx.x * WPB + threadIdx.x / WAVE;
+    const long wv = (long)blockIdx.x * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / a.D, l = lane_id();
@@ -541,7 +569,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     const float kbefore = has_prev ? kseg[base - 1] : 0.f;
     const float kmax = kseg[Ns - 1];
 
-    const float* wp = a.w + (size_t)p * Ns * C;
+    const rsrc_t wr_ = make_rsrc(a.w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
     float x[RK][NV];
 #pragma unroll
     for (int t = 0; t < RK; ++t) {
@@ -550,11 +578,18 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = l + WAVE * j;
-            x[t][j] = (NEED_W && c < C) ? wp[(size_t)row * C + c] * keep : 0.f;
+            x[t][j] = 0.f;
+            if constexpr (NEED_W) {
+                const float xr = buf_load(wr_, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
+                x[t][j] = (c < C) ? xr * keep : 0.f;
+            }
         }
     }
     float ul = 0.f;
-    if constexpr (X2) ul = real ? a.u[(size_t)p * Ns + pl] : 0.f;
+    if constexpr (X2) {
+        const float ur = a.u[(size_t)p * Ns + pl];
+        ul = real ? ur : 0.f;
+    }
 
     float kbef = __shfl_up(kl, 1, WAVE);
     if (l == 0) kbef = kbefore;
@@ -570,91 +605,102 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     for (int j = 0; j < NV; ++j) {
         const int c = l + WAVE * j;
         const bool ok = c < C;
-        PW[j] = ok ? rowA[c] : 0.f;
-        Wt[j] = ok ? totA[c] : 0.f;
-        Bv[j] = (NEED_B && ok) ? rowB[c] : 0.f;
-        Bt[j] = (NEED_B && ok) ? totB[c] : 0.f;
+        const int cc = min(c, C - 1);
+        PW[j] = ok ? rowA[cc] : 0.f;
+        Wt[j] = ok ? totA[cc] : 0.f;
+        Bv[j] = (NEED_B && ok) ? rowB[cc] : 0.f;
+        Bt[j] = (NEED_B && ok) ? totB[cc] : 0.f;
     }
     float PU = 0.f, Ut = 0.f, B1 = 0.f, B1t = 0.f;
     if constexpr (X2) { PU = rowA[C]; Ut = totA[C]; }
     if constexpr (ONES) { B1 = rowB[C]; B1t = totB[C]; }
-    float cnt = (float)base;
     const float Nf = (float)Ns;
 
     const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
     const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
-    int qi = q0, qbase = q0;
-    float qbuf = (q0 + l < q1) ? qseg[q0 + l] : 0.f;
-    uint32_t pbuf = (q0 + l < q1) ? qpseg[q0 + l] : 0u;
-    float kprev = kbefore;
+    // contribution rows of this segment (ROW) and rows dotted at emission (DOT)
+    const rsrc_t sr_ = ROW ? make_rsrc(a.slab + (size_t)s * Mq * a.CR, (uint32_t)((size_t)Mq * a.CR * 4))
+                           : make_rsrc(nullptr, 0);
+    const rsrc_t gr_ = DOT ? make_rsrc(a.g + (size_t)p * Mq * C, (uint32_t)((size_t)Mq * C * 4))
+                           : make_rsrc(nullptr, 0);
+    float* useg = ONES ? a.uslab + (size_t)s * Mq : nullptr;        // v == 1 contributions, sorted order
 
-    auto emit = [&](const float qv, const uint32_t m) {
-        const float lq = qv - kprev;
-        const bool any = cnt > 0.f;
-        if constexpr (ROW) {
-            float* orow = a.out_row + ((size_t)p * Mq + m) * C;
+    // Owned queries in blocks of 64: lane i takes query i for its rank inside the range and its distances, then the
+    // wave walks the keys (lane = channel) carrying the prefix state and emits each query at its rank.
+    for (int qb0 = q0; qb0 < q1; qb0 += WAVE) {
+        const int nq = min(WAVE, q1 - qb0);
+        const bool act = l < nq;
+        const int qi = min(qb0 + l, q1 - 1);              // clamped: unconditional loads
+        const float qv = qseg[qi];
+        const uint32_t mq = qpseg[qi];
+        const int t = range_rank<RK>(kl, nk, qv);
+        const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
+        const float lq = qv - (t > 0 ? kpv : kbefore);   // distance to the last key below q (unused when none)
+        const float qm = qv - kmax;
+        // per-query byte offsets of the slab row / dotted row, computed before any store is issued (see above)
+        const int rowoff = (int)(mq * (ROW ? a.CR : 0) * 4);
+        const int goff = (int)(mq * C * 4);
+        float uqv = 0.f;
+        if constexpr (X1) uqv = a.uq[(size_t)p * Mq + mq];
+        if constexpr (RANK) {
+            if (act) a.out_rank[(size_t)s * Mq + mq] = base + t;
+        }
+
+        float pw[NV], bv[NV];
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                const float la = any ? (lq * PW[j] + Bv[j]) : 0.f;
-                if (c < C) atomic_add_f32(orow + c, 2.f * la - Bt[j] - (qv - kmax) * Wt[j]);
+        for (int jj = 0; jj < NV; ++jj) { pw[jj] = PW[jj]; bv[jj] = Bv[jj]; }
+        float cnt = (float)base, b1 = B1, pu = PU, ubuf = 0.f;
+
+        auto emit = [&](const int j) {
+            const float lqj = bcast(lq, j), qmj = bcast(qm, j);
+            const uint32_t m = bcast(mq, j);
+            if constexpr (ROW) {
+                const int so = bcast(rowoff, j);
+#pragma unroll
+                for (int jj = 0; jj < NV; ++jj) {
+                    const int c = l + WAVE * jj;
+                    if (c < C) buf_store(2.f * (lqj * pw[jj] + bv[jj]) - Bt[jj] - qmj * Wt[jj], sr_, c * 4, so);
+                }
             }
+            if constexpr (ONES) {
+                if (l == j) ubuf = 2.f * (lqj * cnt + b1) - B1t - qmj * Nf;
+            }
+            if constexpr (DOT) {
+                float acc = 0.f;
+#pragma unroll
+                for (int jj = 0; jj < NV; ++jj) {
+                    const int c = l + WAVE * jj;
+                    const float gv = buf_load(gr_, min(c, C - 1) * 4, bcast(goff, j));
+                    if (c < C) acc += gv * (2.f * pw[jj] - Wt[jj]);
+                }
+                acc = wave_sum(acc);
+                if constexpr (X1) acc += bcast(uqv, j) * (2.f * cnt - Nf);
+                if constexpr (X2) acc += 2.f * pu - Ut;
+                if (l == 0) a.out_dot[(size_t)s * Mq + m] = a.sign * acc;
+            }
+        };
+
+        int j = 0;
+        if constexpr (ROW || ONES || DOT) {
+#pragma unroll
+            for (int tt = 0; tt < RK; ++tt) {
+                const int n_at = __popcll(__ballot(act && t == tt));
+                for (int r = 0; r < n_at; ++r, ++j) emit(j);
+                const float gt = bcast(gap, tt);
+#pragma unroll
+                for (int jj = 0; jj < NV; ++jj) {
+                    if constexpr (NEED_B) bv[jj] += gt * pw[jj];
+                    pw[jj] += x[tt][jj];
+                }
+                if constexpr (ONES) b1 += gt * cnt;
+                if constexpr (X2) pu += bcast(ul, tt);
+                cnt += (tt < nk) ? 1.f : 0.f;
+            }
+            for (; j < nq; ++j) emit(j);                // rank RK: above every key of a full last range
         }
         if constexpr (ONES) {
-            const float la = any ? (lq * cnt + B1) : 0.f;
-            if (l == 0) atomic_add_f32(a.out_u + (size_t)p * Mq + m, 2.f * la - B1t - (qv - kmax) * Nf);
+            if (act) useg[qb0 + l] = ubuf;
         }
-        if constexpr (DOT) {
-            const float* grow = a.g + ((size_t)p * Mq + m) * C;
-            float acc = 0.f;
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                if (c < C) acc += grow[c] * (2.f * PW[j] - Wt[j]);
-            }
-            acc = wave_sum(acc);
-            if constexpr (X1) acc += a.uq[(size_t)p * Mq + m] * (2.f * cnt - Nf);
-            if constexpr (X2) acc += 2.f * PU - Ut;
-            if (l == 0) a.out_dot[(size_t)s * Mq + m] = a.sign * acc;
-        }
-        if constexpr (RANK) {
-            if (l == 0) a.out_rank[(size_t)s * Mq + m] = (int32_t)cnt;
-        }
-    };
-
-#pragma unroll
-    for (int t = 0; t < RK; ++t) {
-        const float kt = bcast(kl, t);
-        while (qi < q1) {
-            if (qi - qbase == WAVE) {
-                qbase = qi;
-                qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
-                pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
-            }
-            const float qv = bcast(qbuf, qi - qbase);
-            if (!(qv <= kt)) break;
-            emit(qv, bcast(pbuf, qi - qbase));
-            ++qi;
-        }
-        const float gt = bcast(gap, t);
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            if constexpr (NEED_B) Bv[j] += gt * PW[j];
-            PW[j] += x[t][j];
-        }
-        if constexpr (ONES) B1 += gt * cnt;
-        if constexpr (X2) PU += bcast(ul, t);
-        cnt += (t < nk) ? 1.f : 0.f;
-        kprev = kt;
-    }
-    while (qi < q1) {
-        if (qi - qbase == WAVE) {
-            qbase = qi;
-            qbuf = (qi + l < q1) ? qseg[qi + l] : 0.f;
-            pbuf = (qi + l < q1) ? qpseg[qi + l] : 0u;
-        }
-        emit(bcast(qbuf, qi - qbase), bcast(pbuf, qi - qbase));
-        ++qi;
     }
 }
 
@@ -677,18 +723,18 @@ static int abs_walk_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_
         StageTimer t("abs_range_sums", st);
         if (mode & ABS_DOTX2)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, true>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.ta, ra.tb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
         else if (mode == ABS_RANK)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, false, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.ta, ra.tb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
         else
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.ta, ra.tb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
     }
     {
         StageTimer t("abs_range_scan", st);
         hipLaunchKernelGGL((abs_range_scan<NV, RK>), dim3((S + WPB - 1) / WPB), dim3(WPB * WAVE), 0, st,
-                           a.ks, ra.ta, ra.tb, S, a.Ns, a.C, G);
+                           a.ks, ra.sa, ra.sb, ra.ta, ra.tb, S, a.Ns, a.C, G);
     }
     switch (mode) {
         case ABS_ROW:                         launch_abs_walk<NV, RK, ABS_ROW>(a, ra, G, st); break;

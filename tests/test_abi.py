@@ -44,7 +44,10 @@ def test_version_and_workspace_sizes(lib):
     small = lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4)
     big = lib.qlka_laplace_fwd_ws_bytes(12, 64, 16384, 16384, 64)
     assert 0 < small < big
-    assert lib.qlka_abs_bwd_ws_bytes(12, 64, 16384, 16384, 64) >= lib.qlka_abs_fwd_ws_bytes(12, 64, 16384, 16384, 64)
+    # the row-emitting ops carry one contribution row per (p, d, query): the D-fold slab
+    assert big >= 12 * 64 * 16384 * 64 * 4
+    assert lib.qlka_abs_bwd_ws_bytes(12, 64, 16384, 16384, 64) >= 12 * 64 * 16384 * 64 * 4
+    assert lib.qlka_sgn_fwd_ws_bytes(12, 64, 16384, 16384, 64) < 12 * 64 * 16384 * 64 * 4
     # the global (multi-run) sort needs scratch, the LDS sort none
     assert lib.qlka_seg_sort_ws_bytes(4, 16384) == 0
     assert lib.qlka_seg_sort_ws_bytes(4, 16385) > 0

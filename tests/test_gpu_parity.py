@@ -258,3 +258,45 @@ def test_non_default_stream_and_repeat(dev):
     _assert_rel(_np(w1), ow, nw, "stream out_w")
     _assert_rel(_np(w2), ow, nw, "default stream out_w")
     _assert_rel(_np(u1), ou, ou, "stream out_u")
+
+
+@pytest.mark.parametrize("fill", [0x00, 0xFF, 0x7F])
+@pytest.mark.parametrize("shape", [(3, 4, 129, 200, 64), (2, 2, 5000, 4097, 32), (2, 3, 1000, 700, 65)])
+def test_workspace_contents_do_not_matter(dev, shape, fill):
+    # every op through the C ABI with the workspace pre-filled (NaN, zero, large): no stage may read workspace
+    # memory before writing it, and no kernel may read memory it also writes
+    from qlka import _lib
+    lib = _lib.load()
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape), kind="normal")
+    g_w = np.random.default_rng(8).standard_normal((P, M, C)).astype(np.float32)
+    tq, tk, tv, tg = _t(q, dev), _t(k, dev), _t(v, dev), _t(g_w, dev)
+    st = _lib.stream_of(dev)
+
+    def ws(nb):
+        return torch.full((max(nb, 1),), fill, dtype=torch.uint8, device=dev)
+
+    out, out_u = torch.empty((P, M, C), device=dev), torch.empty((P, M), device=dev)
+    w = ws(lib.qlka_laplace_fwd_ws_bytes(P, D, N, M, C))
+    _lib.check(lib.qlka_laplace_fwd(_lib.ptr(tq), _lib.ptr(tk), _lib.ptr(tv), _lib.ptr(out), _lib.ptr(out_u),
+                                    P, D, N, M, C, _lib.ptr(w), w.numel(), st))
+    ow, ou, nw = brute.laplace_sum(q, k, v)
+    _assert_rel(_np(out), ow, nw, "laplace out_w (poisoned ws)")
+    _assert_rel(_np(out_u), ou, ou, "laplace out_u (poisoned ws)")
+
+    w = ws(lib.qlka_abs_fwd_ws_bytes(P, D, N, M, C))
+    _lib.check(lib.qlka_abs_fwd(_lib.ptr(tq), _lib.ptr(tk), _lib.ptr(tv), _lib.ptr(out), _lib.ptr(out_u),
+                                P, D, N, M, C, -1, _lib.ptr(w), w.numel(), st))
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _assert_rel(_np(out), ow, nw, "abs out_w (poisoned ws)")
+    _assert_rel(_np(out_u), ou, ou, "abs out_u (poisoned ws)")
+
+    gq, gk, gv = (torch.empty((P, D, M), device=dev), torch.empty((P, D, N), device=dev),
+                  torch.empty((P, N, C), device=dev))
+    w = ws(lib.qlka_abs_bwd_ws_bytes(P, D, N, M, C))
+    _lib.check(lib.qlka_abs_bwd(_lib.ptr(tq), _lib.ptr(tk), _lib.ptr(tv), _lib.ptr(tg), _lib.ptr(None),
+                                _lib.ptr(gq), _lib.ptr(gk), _lib.ptr(gv), P, D, N, M, C, _lib.ptr(w), w.numel(), st))
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w)
+    _assert_rel(_np(gq), wq, nq, "grad_q (poisoned ws)")
+    _assert_rel(_np(gk), wk, nk, "grad_k (poisoned ws)")
+    _assert_rel(_np(gv), wv, nv, "grad_v (poisoned ws)")
