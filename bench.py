@@ -138,7 +138,7 @@ def main():
     ms_total = start.elapsed_time(stop)
     stages = {}
     for name in ("lds_radix_sort", "merge_runs", "fill_zero", "lap_range_sums", "lap_range_scan", "lap_range_walk",
-                 "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_scatter", "slab_reduce"):
+                 "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_gather", "slab_reduce"):
         ms, cnt = _lib.stage_time(name)
         if cnt:
             stages[name] = {"ms_total": ms, "launches": cnt, "ms_per_launch": ms / cnt}
@@ -159,19 +159,24 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(dom),
             "algorithmic_bytes_per_launch": bytes_per_launch}
 
-    # per-op view against the north-star target (B_scan / op time)
-    sort_ms = stages.get("lds_radix_sort", {}).get("ms_total", 0.0) / max(1, 2 * args.steps)  # 2 sorts per op call
+    # per-op time, each op timed alone over the same number of calls (north-star target: B_scan / op time)
+    def op_time(fn):
+        for _ in range(2):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
     op_ms = {
-        "weighted_laplace_sum": sum(stages.get(s, {}).get("ms_total", 0.0)
-                                    for s in ("lap_range_sums", "lap_range_scan", "lap_range_walk")) / args.steps
-        + 2 * sort_ms,
-        "weighted_abs_sum_full": sum(stages.get(s, {}).get("ms_total", 0.0)
-                                     for s in ("abs_range_sums", "abs_range_scan", "abs_range_walk")) / args.steps
-        + 2 * sort_ms,
+        "weighted_laplace_sum": op_time(lambda: weighted_laplace_sum(q, k, v)),
+        "weighted_abs_sum_full": op_time(lambda: weighted_abs_sum_full(q, k, v, backend="cuda")),
     }
-    fill = stages.get("fill_zero", {}).get("ms_total", 0.0) / args.steps / 2
-    op_ms = {kk: vv + fill for kk, vv in op_ms.items()}
-    bscan = bytes_per_launch if dom != "lds_radix_sort" else per_unit * units
+    bscan = per_unit * units
     op_roof = {kk: round(bscan / (vv / 1e3) / 1e9 / HBM_PEAK_GBS, 4) for kk, vv in op_ms.items()}
 
     out = {

@@ -49,7 +49,7 @@ int check_dims(int P, int D, int N, int M, int C) {
 struct SortedWs {
     float* ks; uint32_t* kp; float* qs; uint32_t* qp;
     void* sort_scratch; RangeArrays ra;
-    float* slab; float* uslab; void* red_scratch;
+    float* slab; float* uslab; uint32_t* qinv;
 };
 
 struct WsSpec {
@@ -68,7 +68,7 @@ size_t ws_part(const WsSpec& w, int i) {
         case 5: return align256(range_arrays_bytes((int)S, w.range_stream_max, w.C));
         case 6: return w.slab_rows ? align256(S * w.slab_rows * (size_t)slab_stride(w.C) * 4) : 0;
         case 7: return (w.slab_rows && w.want_u) ? align256(S * w.slab_rows * 4) : 0;
-        case 8: return (w.slab_rows && w.want_u) ? align256(reduce_scratch_bytes(w.P, w.D, w.slab_rows)) : 0;
+        case 8: return (w.slab_rows && w.want_u) ? align256(S * w.M * 4) : 0;   // inverse perm of the q sort
     }
     return 0;
 }
@@ -87,7 +87,8 @@ SortedWs carve(void* ws, const WsSpec& w) {
     r.ks = (float*)part[0]; r.kp = (uint32_t*)part[1]; r.qs = (float*)part[2]; r.qp = (uint32_t*)part[3];
     r.sort_scratch = part[4];
     r.ra = carve_range_arrays(part[5], w.P * w.D, w.range_stream_max, w.C);
-    r.slab = (float*)part[6]; r.uslab = (float*)part[7]; r.red_scratch = part[8];
+    r.slab = (float*)part[6]; r.uslab = (float*)part[7];
+    r.qinv = ws_part(w, 8) ? (uint32_t*)part[8] : nullptr;
     return r;
 }
 
@@ -98,9 +99,9 @@ int check_ws(void* ws, size_t have, size_t need) {
 }
 
 int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, hipStream_t st) {
-    int e = seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st);
+    int e = seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st);
     if (e) return hip_status(e, "segmented sort of k");
-    e = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, st);
+    e = seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, st);
     if (e) return hip_status(e, "segmented sort of q");
     return QLKA_OK;
 }
@@ -134,7 +135,7 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
     int e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
     if (e) return hip_status(e, "laplace walk");
-    e = reduce_slabs(w.slab, w.uslab, w.qp, out_w, out_u, P, D, M, C, w.red_scratch, st);
+    e = reduce_slabs(w.slab, w.uslab, w.qinv, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "laplace reduce");
 }
 
@@ -171,7 +172,7 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
     a.sign = 1.f; a.P = P; a.D = D; a.C = C;
     int e = abs_walk(a, out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW, w.ra, st);
     if (e) return hip_status(e, "abs walk");
-    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, out_w, out_u, P, D, M, C, w.red_scratch, st);
+    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qinv, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "abs reduce");
 }
 
@@ -215,7 +216,7 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
     b.out_dot = grad_k; b.sign = 1.f; b.P = P; b.D = D; b.C = C;
     e = abs_walk(b, g_u ? (ABS_ROW | ABS_DOT | ABS_DOTX2) : (ABS_ROW | ABS_DOT), w.ra, st);
     if (e) return hip_status(e, "grad_k/grad_v walk");
-    e = reduce_slabs(w.slab, nullptr, w.kp, grad_v, nullptr, P, D, N, C, w.red_scratch, st);
+    e = reduce_slabs(w.slab, nullptr, nullptr, grad_v, nullptr, P, D, N, C, st);
     return hip_status(e, "grad_v reduce");
 }
 
@@ -256,7 +257,8 @@ int qlka_seg_sort(const float* keys, float* sorted, uint32_t* perm, int num_segs
     if ((int64_t)num_segs * seg_len > (int64_t)INT32_MAX) return fail(QLKA_EINVAL, "num_segs*seg_len must fit int32");
     if (!keys || !sorted || !perm) return fail(QLKA_EINVAL, "keys, sorted and perm must be non-null");
     if (int e = check_ws(ws, ws_bytes, qlka_seg_sort_ws_bytes(num_segs, seg_len))) return e;
-    return hip_status(seg_sort(keys, sorted, perm, num_segs, seg_len, ws, (hipStream_t)stream), "segmented sort");
+    return hip_status(seg_sort(keys, sorted, perm, nullptr, num_segs, seg_len, ws, (hipStream_t)stream),
+                      "segmented sort");
 }
 
 size_t qlka_merge_rank_ws_bytes(int num_segs, int N, int M) {

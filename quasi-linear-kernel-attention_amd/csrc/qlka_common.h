@@ -112,6 +112,16 @@ __device__ __forceinline__ int wave_upper_bound(const float* __restrict__ a, int
     return lo;
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin (block b runs on XCD b % 8), each XCD with its own L2. This
+// maps the hardware block id to a logical work id such that every XCD processes one contiguous slice of the logical
+// order, so work items that share data (the segments of one p share its v rows) run on the same XCD and L2.
+constexpr int NUM_XCD = 8;
+__device__ __forceinline__ int xcd_slice_block(int b, int nb) {
+    const int x = b % NUM_XCD, i = b / NUM_XCD;
+    const int per = nb / NUM_XCD, rem = nb % NUM_XCD;
+    return x * per + min(x, rem) + i;
+}
+
 // Raw buffer access with a uniform base (descriptor) + SGPR offset + per-lane VGPR offset: the per-row part of an
 // address stays in SGPRs, so a row gather/store costs no per-lane address arithmetic and rewrites no address VGPRs.
 // `bytes` bounds the descriptor (out-of-range lanes read 0 / drop their store); every caller's region is < 4 GB.
@@ -126,6 +136,10 @@ __device__ __forceinline__ float buf_load(rsrc_t r, int voff, int soff) {
 }
 __device__ __forceinline__ void buf_store(float x, rsrc_t r, int voff, int soff) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 0);
+}
+// Store that is not re-read by this kernel (streaming output): non-temporal cache policy.
+__device__ __forceinline__ void buf_store_stream(float x, rsrc_t r, int voff, int soff) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 2 /* slc */);
 }
 
 // Relaxed agent-scope fp32 add with no return value (lowers to global_atomic_add_f32 without glc).

@@ -105,7 +105,7 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     const float* __restrict__ v, float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
                     const int S, const int D, const int N, const int M, const int C, const int G)  // ta/tb: summaries
 {
-    const long wv = (long)blockIdx.x * WPB + wave_in_block();
+    const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / D, l = lane_id();
@@ -248,7 +248,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     float* __restrict__ slab, float* __restrict__ uslab,
                     const int S, const int D, const int N, const int M, const int C, const int CR, const int G)
 {
-    const long wv = (long)blockIdx.x * WPB + wave_in_block();
+    const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / D, l = lane_id();
@@ -358,7 +358,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 #pragma unroll
                 for (int jj = 0; jj < NV; ++jj) {
                     const int c = l + WAVE * jj;
-                    if (c < C) buf_store(el * Lc[jj] + er * R[tt][jj], sr_, c * 4, so);
+                    if (c < C) buf_store_stream(el * Lc[jj] + er * R[tt][jj], sr_, c * 4, so);
                 }
             }
             const float dp = bcast(dprev, tt);
@@ -371,7 +371,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 #pragma unroll
             for (int jj = 0; jj < NV; ++jj) {
                 const int c = l + WAVE * jj;
-                if (c < C) buf_store(el * Lc[jj], sr_, c * 4, so);
+                if (c < C) buf_store_stream(el * Lc[jj], sr_, c * 4, so);
             }
         }
     }
@@ -422,7 +422,7 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
                     const int S, const int D, const int Ns, const int Mq, const int C, const int G)
 {
-    const long wv = (long)blockIdx.x * WPB + wave_in_block();
+    const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / D, l = lane_id();
@@ -552,7 +552,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     constexpr bool NEED_B = ROW || ONES;
     constexpr bool NEED_W = ROW || DOT;
     const int S = a.P * a.D, C = a.C, Ns = a.Ns, Mq = a.Mq;
-    const long wv = (long)blockIdx.x * WPB + wave_in_block();
+    const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / a.D, l = lane_id();
@@ -659,7 +659,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
 #pragma unroll
                 for (int jj = 0; jj < NV; ++jj) {
                     const int c = l + WAVE * jj;
-                    if (c < C) buf_store(2.f * (lqj * pw[jj] + bv[jj]) - Bt[jj] - qmj * Wt[jj], sr_, c * 4, so);
+                    if (c < C) buf_store_stream(2.f * (lqj * pw[jj] + bv[jj]) - Bt[jj] - qmj * Wt[jj], sr_, c * 4, so);
                 }
             }
             if constexpr (ONES) {
