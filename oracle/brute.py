@@ -120,6 +120,37 @@ def abs_backward(q, k, v, g_w, g_u=None):
     return (gq, gk, gv), (nq, nk, nv)
 
 
+def abs_backward_sub(q, k, v, g_w, g_u, qidx, kidx):
+    """abs_backward restricted to subsamples: grad_q / nq for the queries qidx (P, mq), grad_k / nk and grad_v / nv
+    for the keys kidx (P, nk); every term still runs over all keys (grad_q) or all queries (grad_k, grad_v)."""
+    q, k, v, g_w = _f64(q), _f64(k), _f64(v), _f64(g_w)
+    g_u = None if g_u is None else _f64(g_u)
+    P, D, M = q.shape
+    C = v.shape[2]
+    mq, nk_ = qidx.shape[1], kidx.shape[1]
+    gq = np.zeros((P, D, mq)); nq = np.zeros_like(gq)
+    gk = np.zeros((P, D, nk_)); nk = np.zeros_like(gk)
+    gv = np.zeros((P, nk_, C)); nv = np.zeros_like(gv)
+    for p in range(P):
+        qi, ki = qidx[p], kidx[p]
+        Bq = g_w[p][qi] @ v[p].T                          # (mq, N)
+        Bk = g_w[p] @ v[p][ki].T                          # (M, nk)
+        if g_u is not None:
+            Bq = Bq + g_u[p][qi][:, None]
+            Bk = Bk + g_u[p][:, None]
+        for d in range(D):
+            xq = q[p, d][qi][:, None] - k[p, d][None, :]  # (mq, N)
+            gq[p, d] = (np.where(xq > 0, 1.0, -1.0) * Bq).sum(axis=1)
+            nq[p, d] = np.abs(Bq).sum(axis=1)
+            xk = k[p, d][ki][None, :] - q[p, d][:, None]  # (M, nk) = k_n - q_m
+            gk[p, d] = (np.where(xk > 0, 1.0, -1.0) * Bk).sum(axis=0)
+            nk[p, d] = np.abs(Bk).sum(axis=0)
+            A = np.abs(xk)                                # |k_n - q_m|
+            gv[p] += A.T @ g_w[p]
+            nv[p] += A.T @ np.abs(g_w[p])
+    return (gq, gk, gv), (nq, nk, nv)
+
+
 # ------------------------------------------------------------------------------------------- sort / rank contracts
 def stable_sort(x):
     """(sorted, perm) along the last axis: np.argsort(kind="stable") on the fp32 values, -0.0 == +0.0, sorted values

@@ -1,0 +1,139 @@
+"""GPU parity at the five BASELINE.json configurations, at their real shapes.
+
+The fp64 oracle runs on every query when N <= 600 and on a seeded subsample of queries (and keys, for the
+backward) otherwise; bars as in test_gpu_parity.py: 1e-5 of the sum of |term| per element.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute, dense, inputs
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _rel(got, want, norm, what):
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    err = float(brute.rel_err(got, want, norm).max())
+    assert err <= REL, f"{what}: max rel err {err:.3e} > {REL}"
+
+
+def _sub(a, idx, axis):
+    return np.stack([np.take(a[p], idx[p], axis=axis) for p in range(a.shape[0])])
+
+
+def test_config0_abs_fwd_bwd_full(dev):
+    from weighted_abs_sum import weighted_abs_sum_full
+    d = inputs.config(0, grads=True)
+    q, k, v, g_w, g_u = d["q"], d["k"], d["v"], d["g_w"], d["g_u"]
+    tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+    w, u = weighted_abs_sum_full(tq, tk, tv)
+    ((w * _t(g_w, dev)).sum() + (u * _t(g_u, dev)).sum()).backward()
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _rel(_np(w), ow, nw, "cfg0 out_w")
+    _rel(_np(u), ou, ou, "cfg0 out_u")
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u)
+    _rel(_np(tq.grad), wq, nq, "cfg0 grad_q")
+    _rel(_np(tk.grad), wk, nk, "cfg0 grad_k")
+    _rel(_np(tv.grad), wv, nv, "cfg0 grad_v")
+
+
+def test_config1_vit_many_small_segments(dev):
+    from weighted_abs_sum import weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+    d = inputs.config(1)
+    q, k, v = d["q"], d["k"], d["v"]
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    lw, lu = weighted_laplace_sum(tq, tk, tv)
+    aw, au = weighted_abs_sum_full(tq, tk, tv, backend="keops")   # the reference picks keops at S < 256
+    ow, ou, nw = brute.laplace_sum(q, k, v)
+    _rel(_np(lw), ow, nw, "cfg1 laplace out_w")
+    _rel(_np(lu), ou, ou, "cfg1 laplace out_u")
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _rel(_np(aw), ow, nw, "cfg1 abs out_w")
+    _rel(_np(au), ou, ou, "cfg1 abs out_u")
+
+
+def test_config2_laplace_text_inference(dev):
+    from weighted_laplace_sum import weighted_laplace_sum
+    d = inputs.config(2)
+    q, k, v = d["q"], d["k"], d["v"]
+    w, u = weighted_laplace_sum(_t(q, dev), _t(k, dev), _t(v, dev))
+    idx = inputs.query_subsample(q.shape[0], q.shape[2], per_p=16)
+    ow, ou, nw = brute.laplace_sum(q, k, v, qidx=idx)
+    _rel(_sub(_np(w), idx, 0), ow, nw, "cfg2 out_w")
+    _rel(_sub(_np(u), idx, 0), ou, ou, "cfg2 out_u")
+
+
+def test_config3_headline_ops_and_layers(dev):
+    from weighted_abs_sum import weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+    d = inputs.config(3)
+    q, k, v = d["q"], d["k"], d["v"]
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    idx = inputs.query_subsample(q.shape[0], q.shape[2], per_p=8)
+    lw, lu = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v, qidx=idx)
+    _rel(_sub(_np(lw), idx, 0), ow, nw, "cfg3 laplace out_w")
+    _rel(_sub(_np(lu), idx, 0), ou, ou, "cfg3 laplace out_u")
+    aw, au = weighted_abs_sum_full(tq, tk, tv)
+    ow, ou, nw = brute.abs_sum(q, k, v, qidx=idx)
+    _rel(_sub(_np(aw), idx, 0), ow, nw, "cfg3 abs out_w")
+    _rel(_sub(_np(au), idx, 0), ou, ou, "cfg3 abs out_u")
+    # the attention layers of the reference (attention.py:67-126) over these ops, B=1 H=12 S=16384 D=64, against
+    # the normalised dense kernel matrix on the query subsample (float64 on the host)
+    B, H, S, Dh = 1, 12, 16384, 64
+    qa = torch.from_numpy(q).reshape(B, H, Dh, S).transpose(2, 3).contiguous()
+    ka = torch.from_numpy(k).reshape(B, H, Dh, S).transpose(2, 3).contiguous()
+    va = torch.from_numpy(v).reshape(B, H, S, Dh).contiguous()
+    for kernel in ("add_laplace", "add_riesz", "add_bump"):
+        tau = dense.TAU[kernel]
+        out = dense.attention(qa.to(dev), ka.to(dev), va.to(dev), kernel, tau, weighted_abs_sum_full,
+                              weighted_laplace_sum)
+        out = _np(out).reshape(B * H, S, Dh)
+        q64 = torch.from_numpy(q).double()
+        k64 = torch.from_numpy(k).double()
+        v64 = torch.from_numpy(v).double()
+        for p in range(0, B * H, 4):
+            qs = q64[p:p + 1][:, :, idx[p]]
+            A = dense.dense_kernel_matrix(kernel, qs, k64[p:p + 1], tau)        # (1, mq, S)
+            ref = (A @ v64[p:p + 1]) / A.sum(dim=2, keepdim=True).clamp_min(dense.CLAMP)
+            np.testing.assert_allclose(out[p][idx[p]], ref[0].numpy(), rtol=2e-4, atol=2e-5,
+                                       err_msg=f"{kernel} layer, p={p}")
+
+
+def test_config4_stress_global_sort_heavy_ties(dev):
+    from weighted_abs_sum import _ext
+    from weighted_laplace_sum import weighted_laplace_sum
+    d = inputs.config(4, grads=True)
+    q, k, v, g_w, g_u = d["q"], d["k"], d["v"], d["g_w"], d["g_u"]
+    P, M, N = q.shape[0], q.shape[2], k.shape[2]
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    qidx = inputs.query_subsample(P, M, per_p=4, seed=2)
+    kidx = inputs.query_subsample(P, N, per_p=4, seed=3)
+    lw, lu = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v, qidx=qidx)
+    _rel(_sub(_np(lw), qidx, 0), ow, nw, "cfg4 laplace out_w")
+    _rel(_sub(_np(lu), qidx, 0), ou, ou, "cfg4 laplace out_u")
+    del lw, lu
+    aw, au = _ext.weighted_abs_sum_full_forward(tq, tk, tv)
+    ow, ou, nw = brute.abs_sum(q, k, v, qidx=qidx)
+    _rel(_sub(_np(aw), qidx, 0), ow, nw, "cfg4 abs out_w")
+    _rel(_sub(_np(au), qidx, 0), ou, ou, "cfg4 abs out_u")
+    del aw, au
+    gq, gk, gv = _ext.weighted_abs_sum_full_backward(tq, tk, tv, _t(g_w, dev), _t(g_u, dev))
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward_sub(q, k, v, g_w, g_u, qidx, kidx)
+    _rel(_sub(_np(gq), qidx, 1), wq, nq, "cfg4 grad_q")
+    _rel(_sub(_np(gk), kidx, 1), wk, nk, "cfg4 grad_k")
+    _rel(_sub(_np(gv), kidx, 0), wv, nv, "cfg4 grad_v")

@@ -245,3 +245,20 @@ def test_inputs_are_seeded():
     m = inputs.make(1, 2, 5000, 10, 2, kind="mixture")
     lv = m["k"][np.abs(m["k"] * 16 - np.round(m["k"] * 16)) == 0]
     assert lv.size > 0.4 * m["k"].size                   # about half the keys sit on the 256 exact levels
+
+
+def test_backward_subsample_matches_full():
+    P, D, N, M, C = 2, 3, 9, 7, 4
+    q, k, v = _rand(P, D, N, M, C, seed=16, ties=True)
+    rng = np.random.default_rng(5)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    qidx = np.stack([np.array([0, 3, 6])] * P)
+    kidx = np.stack([np.array([1, 2, 8])] * P)
+    (fq, fk, fv), (nfq, nfk, nfv) = brute.abs_backward(q, k, v, g_w, g_u)
+    (sq, sk, sv), (nsq, nsk, nsv) = brute.abs_backward_sub(q, k, v, g_w, g_u, qidx, kidx)
+    np.testing.assert_allclose(sq, fq[:, :, qidx[0]], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(sk, fk[:, :, kidx[0]], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(sv, fv[:, kidx[0]], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(nsq, nfq[:, :, qidx[0]], rtol=1e-12)
+    np.testing.assert_allclose(nsv, nfv[:, kidx[0]], rtol=1e-12)
