@@ -46,7 +46,7 @@ def make_inputs(dev, seed=0):
     return [torch.from_numpy(a).to(dev) for a in (q, k, v)]
 
 
-def cpu_baseline(seed=0, mq=8, reps=3):
+def cpu_baseline(seed=0, mq=256, reps=3):
     """The reference's dense PyTorch path (kernels.py:73,81 restated in oracle/dense.py), torch-CPU fp32 eager, on a
     seeded sample of mq queries per p against all N keys of the headline workload. Cost is linear in the number of
     queries, so query-feature sums/s = 2 * P * mq * D / t (both ops)."""
@@ -103,7 +103,19 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        dev = torch.device("cuda", 0)
+        x = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 3}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); this build has no multi-GPU path "
               "(sharding over P or over d is described in DESIGN.md).", file=sys.stderr)
