@@ -142,9 +142,15 @@ __device__ __forceinline__ void buf_store_stream(float x, rsrc_t r, int voff, in
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, voff, soff, 2 /* slc */);
 }
 
-// Relaxed agent-scope fp32 add with no return value (lowers to global_atomic_add_f32 without glc).
-__device__ __forceinline__ void atomic_add_f32(float* p, float v) {
-    __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// 16-byte accesses (buffer_load/store_dwordx4): voff must be 16-byte aligned relative to a 16-byte aligned base.
+typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4_t buf_load4(rsrc_t r, int voff, int soff) {
+    return __builtin_bit_cast(f4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+// Non-temporal: rows that are not re-read by the kernel storing them, so they do not evict its L2-resident gathers.
+__device__ __forceinline__ void buf_store4_stream(f4_t x, rsrc_t r, int voff, int soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4_t, x), r, voff, soff, 2 /* slc */);
 }
 
 }  // namespace qlka

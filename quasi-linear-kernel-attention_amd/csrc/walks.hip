@@ -8,14 +8,15 @@
 //   *_range_scan   one wave per segment: turns the summaries into each range's entry state (exclusive prefix over
 //                  the ranges to the left) and, for the Laplace sum, exit state (exclusive suffix to the right).
 //   *_range_walk   one wave per range: gathers the range's RK value rows into registers (lane = channel), runs the
-//                  recurrences key by key and emits every owned query once.
+//                  recurrences key by key in 4 chunks, stages each chunk's state rows in wave-private LDS and emits
+//                  the owned queries ranked in the chunk from there, 64 / LQ query rows per 16-byte-per-lane store.
 //
 // Laplace (Weighted_Laplace_Sum/csrc/laplace_kernels.cu:5-29 states the same math): with sorted keys k_0..k_{N-1}
 //   L_j = e^{-(k_j - k_{j-1})} L_{j-1} + v_j,   R_j = v_j + e^{-(k_{j+1} - k_j)} R_{j+1},
 //   query q of rank r gets  e^{-(q - k_{r-1})} L_{r-1} + e^{-(k_r - q)} R_r.
 // Every exponent argument is <= 0 and every decay factor is <= 1, so nothing overflows and nothing cancels. The walk
-// keeps R for all RK keys of its range in registers (computed backwards from the range's exit state), so v is
-// gathered twice per key and feature (sums + walk) instead of the reference's three times.
+// keeps R only at its chunk boundaries (computed backwards from the range's exit state) and rebuilds each chunk's R
+// rows from there, so v is gathered twice per key and feature (sums + walk) instead of the reference's three times.
 //
 // Abs family (Weighted_Abs_Sum/csrc/abs_kernels.cu:9-19 and sgn_kernels.cu:8-15 state the same identities): the
 // stream state after the keys below q is PW = sum w_n and B = sum (k_prev - k_n) w_n, all distances measured from
@@ -26,8 +27,8 @@
 // Distances from k_prev and k_max (instead of raw k*v sums) keep the walk translation invariant. Only a prefix is
 // needed, so the abs walks gather each row once in the walk plus once in the sums.
 //
-// Outputs of the row emissions are summed over the D features of a p with relaxed fp32 atomics (one coalesced
-// 4*C-byte atomic per query and feature); the scalar emissions of the sgn walks have exactly one writer and store.
+// Row emissions go to a per-feature slab (one row per query and feature, reduce.hip sums the D features of a p in a
+// fixed order); scalar emissions (v == 1 sums, dots, ranks) have exactly one writer each and are plain stores.
 #include "qlka_common.h"
 #include "qlka_internal.h"
 
@@ -240,6 +241,37 @@ void lap_range_scan(const float* __restrict__ ks, const float* __restrict__ sa, 
     }
 }
 
+// Emission through LDS. Each wave owns a private slice of its workgroup's LDS: the state rows of one chunk of
+// CH = RK / 4 keys (plus one row for rank RK) and one record per query of the current block of 64 queries. After the
+// wave has written a chunk's rows, the queries ranked in the chunk are emitted with LQ lanes per query (LQ * 4 >= CR
+// channels, one 16-byte store per lane), i.e. 64 / LQ query rows per store instruction, with no per-query scalar
+// broadcasts. LDS operations of one wave complete in program order, so the wave-private slice needs no barrier.
+template <int NV, int RK>
+struct alignas(16) WalkLds {
+    static constexpr int CH = RK / 4;
+    static constexpr int RS = WAVE * NV;           // floats per state row (lane = channel, pads included)
+    float a[(CH + 1) * RS];
+    float b[(CH + 1) * RS];
+    f4_t par[WAVE];
+};
+
+// Lane layout of the emission: lane = grp * LQ + sub owns channels c4 .. c4 + 3 (c4 = 4 * sub) of query row grp.
+struct EmitLanes {
+    int sh, qpi, grp, c4;
+    bool ok;
+    __device__ __forceinline__ explicit EmitLanes(int CR) {
+        sh  = (CR <= 32) ? 3 : (CR <= 64) ? 4 : 5;     // LQ = 1 << sh lanes per query row
+        qpi = WAVE >> sh;                               // query rows per instruction
+        const int l = lane_id();
+        grp = l >> sh;
+        c4  = (l & ((1 << sh) - 1)) * 4;
+        ok  = c4 < CR;
+    }
+};
+
+
+constexpr int RPW = 1;             // consecutive key ranges walked by one wave of a walk kernel
+
 template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
 void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
@@ -248,130 +280,200 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     float* __restrict__ slab, float* __restrict__ uslab,
                     const int S, const int D, const int N, const int M, const int C, const int CR, const int G)
 {
+    using Lds = WalkLds<NV, RK>;
+    constexpr int CH = Lds::CH, RS = Lds::RS;
+    __shared__ Lds lds[WPB];
+    const int GW = (G + RPW - 1) / RPW;
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
-    if (wv >= (long)S * G) return;
-    const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
+    if (wv >= (long)S * GW) return;
+    Lds& sm = lds[wave_in_block()];
+    const int s = (int)(wv / GW), gw = (int)(wv - (long)s * GW);
     const int p = s / D, l = lane_id();
-    const int base = g * RK, nk = min(RK, N - base);
     const float* kseg = ks + (size_t)s * N;
+    const uint32_t* kpseg = kp + (size_t)s * N;
     const float* qseg = qs + (size_t)s * M;
     const uint32_t* qpseg = qp + (size_t)s * M;
-
-    const int li = base + min(l, nk - 1);
-    const float kl = kseg[li];
-    const uint32_t pl = kp[(size_t)s * N + li];
-    const bool real = l < nk;
-    const bool has_prev = g > 0, has_next = g < G - 1;
-    const float kbefore = has_prev ? kseg[base - 1] : 0.f;
-    const float kafter  = has_next ? kseg[base + RK] : 0.f;
-
-    // value rows of the range (pads: zero rows, keys equal to the last real key)
     const rsrc_t vr = make_rsrc(v + (size_t)p * N * C, (uint32_t)((size_t)N * C * 4));
-    float x[RK][NV];
+    const rsrc_t sr_ = make_rsrc(slab + (size_t)s * M * CR, (uint32_t)((size_t)M * CR * 4));
+    float* useg = uslab + (size_t)s * M;
+    const int CS = range_stride(C);
+    const EmitLanes el_(CR);
+
+    const int g_end = min(G, gw * RPW + RPW);
+    for (int g = gw * RPW; g < g_end; ++g) {
+        const int base = g * RK, nk = min(RK, N - base);
+        const int li = base + min(l, nk - 1);
+        const float kl = kseg[li];
+        const bool real = l < nk;
+        const bool has_prev = g > 0, has_next = g < G - 1;
+        const float kbefore = has_prev ? kseg[base - 1] : 0.f;
+        const float kafter  = has_next ? kseg[base + RK] : 0.f;
+
+        // value rows of the range, lane = channel (pad keys and pad channels: zero). The row indices are read with
+        // scalar loads straight into SGPRs (the buffer offset of each row gather).
+        float x[RK][NV];
+        if (nk == RK) {
 #pragma unroll
-    for (int t = 0; t < RK; ++t) {
-        const uint32_t row = bcast(pl, t);
-        const float keep = (t < nk) ? 1.f : 0.f;
+            for (int t = 0; t < RK; ++t) {
+                const int rowoff = (int)(kpseg[base + t] * C * 4);
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    x[t][j] = buf_load(vr, min(l + WAVE * j, C - 1) * 4, rowoff);   // unconditional gather
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < RK; ++t) {
+                const int rowoff = (int)(kpseg[base + min(t, nk - 1)] * C * 4);
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    x[t][j] = buf_load(vr, min(l + WAVE * j, C - 1) * 4, rowoff);
+            }
+        }
+        if (nk < RK || C < RS) {                          // partial last range or pad channels (uniform branch)
+#pragma unroll
+            for (int t = 0; t < RK; ++t)
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    x[t][j] = (t < nk && l + WAVE * j < C) ? x[t][j] : 0.f;
+        }
+
+        const float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
+        const float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
+        float L[NV], Rx[NV];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = l + WAVE * j;
-            const float xr = buf_load(vr, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
-            x[t][j] = (c < C) ? xr * keep : 0.f;
+            L[j]  = (c < C) ? ra[min(c, C - 1)] : 0.f;
+            Rx[j] = (c < C) ? rb[min(c, C - 1)] : 0.f;
         }
-    }
+        const float L1in = ra[C], R1out = rb[C];
 
-    const int CS = range_stride(C);
-    const float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
-    const float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
-    float L[NV], Rx[NV];
+        // lane t: decay into key t from the key before it, and from key t to the key after it. Both go to LDS, from
+        // where the key loops read four at a time as a broadcast (no per-key lane-to-scalar moves).
+        float kbef = __shfl_up(kl, 1, WAVE);
+        if (l == 0) kbef = kbefore;
+        const float dprev = (l == 0 && !has_prev) ? 0.f : __expf(-(kl - kbef));
+        float kaft = __shfl_down(kl, 1, WAVE);
+        if (l == RK - 1) kaft = kafter;
+        const float dnext = (l == RK - 1 && !has_next) ? 0.f : __expf(-(kaft - kl));
+
+        // v == 1 channel: L1 after key t and R1 at key t, as lane-t values of two affine scans
+        float a1 = (l < RK) ? dprev : 1.f, b1 = real ? 1.f : 0.f;
+        wave_affine_scan_fwd(a1, b1);
+        const float l1 = a1 * L1in + b1;
+        float a2 = (l < RK) ? dnext : 1.f, b2 = real ? 1.f : 0.f;
+        wave_affine_scan_bwd(a2, b2);
+        const float r1 = a2 * R1out + b2;
+
+        // R at the chunk boundaries, R_{CH}, R_{2CH}, R_{3CH} (R_{RK} is the exit state Rx): each chunk later rebuilds
+        // its own R rows backwards from its right boundary, so R never occupies RK rows of registers.
+        float Rc[3][NV];
+        {
+            float r[NV];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int c = l + WAVE * j;
-        L[j]  = (c < C) ? ra[min(c, C - 1)] : 0.f;
-        Rx[j] = (c < C) ? rb[min(c, C - 1)] : 0.f;
-    }
-    const float L1in = ra[C], R1out = rb[C];
-
-    // lane t: decay into key t from the key before it, and from key t to the key after it
-    float kbef = __shfl_up(kl, 1, WAVE);
-    if (l == 0) kbef = kbefore;
-    const float dprev = (l == 0 && !has_prev) ? 0.f : __expf(-(kl - kbef));
-    float kaft = __shfl_down(kl, 1, WAVE);
-    if (l == RK - 1) kaft = kafter;
-    const float dnext = (l == RK - 1 && !has_next) ? 0.f : __expf(-(kaft - kl));
-
-    // v == 1 channel: L1 after key t and R1 at key t, as lane-t values of two affine scans
-    float a1 = (l < RK) ? dprev : 1.f, b1 = real ? 1.f : 0.f;
-    wave_affine_scan_fwd(a1, b1);
-    const float l1 = a1 * L1in + b1;
-    float a2 = (l < RK) ? dnext : 1.f, b2 = real ? 1.f : 0.f;
-    wave_affine_scan_bwd(a2, b2);
-    const float r1 = a2 * R1out + b2;
-
-    // R_t for all keys of the range, backwards from the exit state; x is still needed for L
-    float R[RK][NV];
+            for (int j = 0; j < NV; ++j) r[j] = Rx[j];
 #pragma unroll
-    for (int t = RK - 1; t >= 0; --t) {
-        const float dn = bcast(dnext, t);
+            for (int t = RK - 1; t >= CH; --t) {
+                const float dn = bcast(dnext, t);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) R[t][j] = x[t][j] + dn * (t == RK - 1 ? Rx[j] : R[t + 1][j]);
-    }
-
-    // Owned queries [q0, q1) of the sorted queries, in blocks of 64. Per block, lane i first takes query i and
-    // computes its rank t inside the range and its two decay factors (one v_exp each for all 64 queries); then the
-    // wave walks the keys with lane = channel and writes each query's contribution row.
-    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
-    const int q1 = has_next ? qb[(size_t)s * G + g] : M;
-    // this segment's contribution rows (indexed by query) and v == 1 contributions (sorted order)
-    const rsrc_t sr_ = make_rsrc(slab + (size_t)s * M * CR, (uint32_t)((size_t)M * CR * 4));
-    float* useg = uslab + (size_t)s * M;
-
-    for (int qb0 = q0; qb0 < q1; qb0 += WAVE) {
-        const int nq = min(WAVE, q1 - qb0);
-        const bool act = l < nq;
-        const int qi = min(qb0 + l, q1 - 1);              // clamped: unconditional loads
-        const float qv = qseg[qi];
-        const uint32_t mq = qpseg[qi];
-        const int t = range_rank<RK>(kl, nk, qv);
-        const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
-        const float knv = __shfl(kl, min(t, RK - 1), WAVE);
-        const float l1p = __shfl(l1, max(t - 1, 0), WAVE);
-        const float r1n = __shfl(r1, min(t, RK - 1), WAVE);
-        const bool lft = t > 0 || has_prev;
-        const float eL = lft ? __expf(-(qv - (t > 0 ? kpv : kbefore))) : 0.f;
-        const float eR = (t < nk) ? __expf(-(knv - qv)) : 0.f;
-        if (act) useg[qb0 + l] = eL * (t > 0 ? l1p : L1in) + eR * r1n;
-        // byte offset of each query's slab row, computed here so no load result is first used inside the store loop
-        // (vmcnt also counts stores: a late first use of a load would wait for every store issued before it)
-        const int rowoff = (int)(mq * CR * 4);
-
-        float Lc[NV];
+                for (int j = 0; j < NV; ++j) r[j] = x[t][j] + dn * r[j];
+                if (t % CH == 0) {
 #pragma unroll
-        for (int jj = 0; jj < NV; ++jj) Lc[jj] = L[jj];
-        int j = 0;
-#pragma unroll
-        for (int tt = 0; tt < RK; ++tt) {
-            const int cnt = __popcll(__ballot(act && t == tt));
-            for (int r = 0; r < cnt; ++r, ++j) {
-                const float el = bcast(eL, j), er = bcast(eR, j);
-                const int so = bcast(rowoff, j);
-#pragma unroll
-                for (int jj = 0; jj < NV; ++jj) {
-                    const int c = l + WAVE * jj;
-                    if (c < C) buf_store_stream(el * Lc[jj] + er * R[tt][jj], sr_, c * 4, so);
+                    for (int j = 0; j < NV; ++j) Rc[t / CH - 1][j] = r[j];
                 }
             }
-            const float dp = bcast(dprev, tt);
-#pragma unroll
-            for (int jj = 0; jj < NV; ++jj) Lc[jj] = dp * Lc[jj] + x[tt][jj];
         }
-        for (; j < nq; ++j) {                         // rank RK: above every key of a full last range
-            const float el = bcast(eL, j);
-            const int so = bcast(rowoff, j);
+
+        // Owned queries [q0, q1) of the sorted queries, in blocks of 64. Per block, lane i takes query i: its rank t
+        // inside the range, its two decay factors and its v == 1 sum; its record (row offset of rank t in the chunk
+        // buffers, slab row offset, eL, eR) goes to LDS. Then the keys are walked in 4 chunks of CH: the chunk's rows
+        // L_{t-1} (state before key t) and R_t go to LDS and the queries ranked in the chunk are emitted as
+        // eL * L_{t-1} + eR * R_t, several query rows per store instruction.
+        const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+        const int q1 = has_next ? qb[(size_t)s * G + g] : M;
+        for (int qb0 = q0; qb0 < q1; qb0 += WAVE) {
+            const int nq = min(WAVE, q1 - qb0);
+            const bool act = l < nq;
+            const int qi = min(qb0 + l, q1 - 1);          // clamped: unconditional loads
+            const float qv = qseg[qi];
+            const uint32_t mq = qpseg[qi];
+            const int t = range_rank<RK>(kl, nk, qv);
+            const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
+            const float knv = __shfl(kl, min(t, RK - 1), WAVE);
+            const float l1p = __shfl(l1, max(t - 1, 0), WAVE);
+            const float r1n = __shfl(r1, min(t, RK - 1), WAVE);
+            const bool lft = t > 0 || has_prev;
+            const float eL = lft ? __expf(-(qv - (t > 0 ? kpv : kbefore))) : 0.f;
+            const float eR = (t < nk) ? __expf(-(knv - qv)) : 0.f;
+            if (act) useg[qb0 + l] = eL * (t > 0 ? l1p : L1in) + eR * r1n;
+            sm.par[l] = f4_t{__int_as_float(t * RS * 4), __int_as_float((int)(mq * CR * 4)), eL, eR};
+
+            float Lc[NV];
 #pragma unroll
-            for (int jj = 0; jj < NV; ++jj) {
-                const int c = l + WAVE * jj;
-                if (c < C) buf_store_stream(el * Lc[jj], sr_, c * 4, so);
+            for (int j = 0; j < NV; ++j) Lc[j] = L[j];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int t0 = c * CH;
+                const int j0 = (c == 0) ? 0 : __popcll(__ballot(act && t < t0));
+                const int j1 = (c == 3) ? nq : __popcll(__ballot(act && t < t0 + CH));
+                if (j1 > j0) {
+                    // the chunk's decays, once into SGPRs: dnext of key t0+i, and dprev of key t0+i+1 is the same value
+                    float dn[CH];
+#pragma unroll
+                    for (int i = 0; i < CH; ++i) dn[i] = bcast(dnext, t0 + i);
+                    float r[NV];
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) r[j] = (c == 3) ? Rx[j] : Rc[c][j];
+#pragma unroll
+                    for (int i = CH - 1; i >= 0; --i) {
+#pragma unroll
+                        for (int j = 0; j < NV; ++j) {
+                            r[j] = x[t0 + i][j] + dn[i] * r[j];
+                            sm.b[i * RS + l + WAVE * j] = r[j];
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < CH; ++i) {
+                        const float dp = (i == 0) ? bcast(dprev, t0) : dn[i - 1];
+#pragma unroll
+                        for (int j = 0; j < NV; ++j) {
+                            sm.a[i * RS + l + WAVE * j] = Lc[j];
+                            Lc[j] = dp * Lc[j] + x[t0 + i][j];
+                        }
+                    }
+                    if (c == 3) {                         // rank RK: above every key of a full last range
+#pragma unroll
+                        for (int j = 0; j < NV; ++j) {
+                            sm.a[CH * RS + l + WAVE * j] = Lc[j];
+                            sm.b[CH * RS + l + WAVE * j] = 0.f;
+                        }
+                    }
+                    // Branch-free batches of EU iterations: every lane reads a record and two rows (indices clamped into
+                    // the buffers), and only the stores of queries j0 .. j1-1 (ranks in [t0, t0 + CH]) are kept.
+                    constexpr int EU = 4;
+                    const int rlo = t0 * RS * 4, rhi = (t0 + CH) * RS * 4;
+                    for (int jb = j0; jb < j1; jb += EU * el_.qpi) {
+                        f4_t pr[EU];
+#pragma unroll
+                        for (int u = 0; u < EU; ++u) pr[u] = sm.par[min(jb + u * el_.qpi + el_.grp, WAVE - 1)];
+#pragma unroll
+                        for (int u = 0; u < EU; ++u) {
+                            const int j = jb + u * el_.qpi + el_.grp;
+                            const int ro = min(max(__float_as_int(pr[u].x), rlo), rhi) - rlo + el_.c4 * 4;
+                            const f4_t av = *reinterpret_cast<const f4_t*>(reinterpret_cast<const char*>(sm.a) + ro);
+                            const f4_t bv = *reinterpret_cast<const f4_t*>(reinterpret_cast<const char*>(sm.b) + ro);
+                            const f4_t o = pr[u].z * av + pr[u].w * bv;
+                            if (j < j1 && el_.ok) buf_store4_stream(o, sr_, __float_as_int(pr[u].y) + el_.c4 * 4, 0);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < CH; ++i) {
+                        const float dp = bcast(dprev, t0 + i);
+#pragma unroll
+                        for (int j = 0; j < NV; ++j) Lc[j] = dp * Lc[j] + x[t0 + i][j];
+                    }
+                }
             }
         }
     }
@@ -396,8 +498,10 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
                            ks, ra.sa, ra.sb, ra.ta, ra.tb, S, N, C, G);
     }
     {
+        const long walk_waves = (long)S * ((G + RPW - 1) / RPW);
+        const unsigned walk_blocks = (unsigned)((walk_waves + WPB - 1) / WPB);
         StageTimer t("lap_range_walk", st);
-        hipLaunchKernelGGL((lap_range_walk<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
+        hipLaunchKernelGGL((lap_range_walk<NV, RK>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
                            ks, kp, qs, qp, v, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C), G);
     }
     return (int)hipGetLastError();
@@ -549,84 +653,119 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
 {
     constexpr bool ROW = MODE & ABS_ROW, ONES = MODE & ABS_ONES, DOT = MODE & ABS_DOT;
     constexpr bool X1 = MODE & ABS_DOTX1, X2 = MODE & ABS_DOTX2, RANK = MODE & ABS_RANK;
-    constexpr bool NEED_B = ROW || ONES;
-    constexpr bool NEED_W = ROW || DOT;
+    constexpr bool EMIT = ROW || DOT;                     // rows gathered, states staged in LDS, emission
+    constexpr bool EXTRA = X1 || X2;
+    using Lds = WalkLds<NV, RK>;
+    constexpr int CH = Lds::CH, RS = Lds::RS;
+    __shared__ Lds lds[EMIT ? WPB : 1];
+    __shared__ float exs[EXTRA ? WPB : 1][WAVE];          // per-query scalar added to the dot (X1 / X2)
     const int S = a.P * a.D, C = a.C, Ns = a.Ns, Mq = a.Mq;
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
+    Lds& sm = lds[EMIT ? wave_in_block() : 0];
+    float* ex = exs[EXTRA ? wave_in_block() : 0];
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
     const int p = s / a.D, l = lane_id();
     const int base = g * RK, nk = min(RK, Ns - base);
     const float* kseg = a.ks + (size_t)s * Ns;
+    const uint32_t* kpseg = a.kp + (size_t)s * Ns;
     const float* qseg = a.qs + (size_t)s * Mq;
     const uint32_t* qpseg = a.qp + (size_t)s * Mq;
 
     const int li = base + min(l, nk - 1);
     const float kl = kseg[li];
-    const uint32_t pl = a.kp[(size_t)s * Ns + li];
     const bool real = l < nk;
     const bool has_prev = g > 0, has_next = g < G - 1;
     const float kbefore = has_prev ? kseg[base - 1] : 0.f;
     const float kmax = kseg[Ns - 1];
 
-    const rsrc_t wr_ = make_rsrc(a.w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
+    // weight rows of the range, lane = channel (pad keys and pad channels: zero); row indices by scalar loads
     float x[RK][NV];
+    if constexpr (EMIT) {
+        const rsrc_t wr_ = make_rsrc(a.w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
+        if (nk == RK) {
 #pragma unroll
-    for (int t = 0; t < RK; ++t) {
-        const uint32_t row = bcast(pl, t);
-        const float keep = (t < nk) ? 1.f : 0.f;
+            for (int t = 0; t < RK; ++t) {
+                const int rowoff = (int)(kpseg[base + t] * C * 4);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int c = l + WAVE * j;
-            x[t][j] = 0.f;
-            if constexpr (NEED_W) {
-                const float xr = buf_load(wr_, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
-                x[t][j] = (c < C) ? xr * keep : 0.f;
+                for (int j = 0; j < NV; ++j)
+                    x[t][j] = buf_load(wr_, min(l + WAVE * j, C - 1) * 4, rowoff);   // unconditional gather
             }
+        } else {
+#pragma unroll
+            for (int t = 0; t < RK; ++t) {
+                const int rowoff = (int)(kpseg[base + min(t, nk - 1)] * C * 4);
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    x[t][j] = buf_load(wr_, min(l + WAVE * j, C - 1) * 4, rowoff);
+            }
+        }
+        if (nk < RK || C < RS) {                          // partial last range or pad channels (uniform branch)
+#pragma unroll
+            for (int t = 0; t < RK; ++t)
+#pragma unroll
+                for (int j = 0; j < NV; ++j)
+                    x[t][j] = (t < nk && l + WAVE * j < C) ? x[t][j] : 0.f;
         }
     }
     float ul = 0.f;
     if constexpr (X2) {
-        const float ur = a.u[(size_t)p * Ns + pl];
+        const float ur = a.u[(size_t)p * Ns + kpseg[li]];
         ul = real ? ur : 0.f;
     }
 
     float kbef = __shfl_up(kl, 1, WAVE);
     if (l == 0) kbef = kbefore;
-    const float gap = (real && (l > 0 || has_prev)) ? (kl - kbef) : 0.f;
+    const float gap = (real && (l > 0 || has_prev)) ? (kl - kbef) : 0.f;   // distance from the key before
 
     const int CS = range_stride(C);
     const float* rowA = ta + ((size_t)s * (G + 1) + g) * CS;
     const float* rowB = tb + ((size_t)s * (G + 1) + g) * CS;
     const float* totA = ta + ((size_t)s * (G + 1) + G) * CS;
     const float* totB = tb + ((size_t)s * (G + 1) + G) * CS;
-    float PW[NV], Bv[NV], Wt[NV], Bt[NV];
+    float PW[NV], Bv[NV], Bt[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = l + WAVE * j;
         const bool ok = c < C;
         const int cc = min(c, C - 1);
-        PW[j] = ok ? rowA[cc] : 0.f;
-        Wt[j] = ok ? totA[cc] : 0.f;
-        Bv[j] = (NEED_B && ok) ? rowB[cc] : 0.f;
-        Bt[j] = (NEED_B && ok) ? totB[cc] : 0.f;
+        PW[j] = (EMIT && ok) ? rowA[cc] : 0.f;
+        Bv[j] = (ROW && ok) ? rowB[cc] : 0.f;
+        Bt[j] = (ROW && ok) ? totB[cc] : 0.f;
     }
     float PU = 0.f, Ut = 0.f, B1 = 0.f, B1t = 0.f;
     if constexpr (X2) { PU = rowA[C]; Ut = totA[C]; }
     if constexpr (ONES) { B1 = rowB[C]; B1t = totB[C]; }
     const float Nf = (float)Ns;
 
+    // Emission lanes: channels c4 .. c4+3 of one query row; Wtot of those channels
+    const EmitLanes el_(slab_stride(C));
+    f4_t wt4 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (EMIT) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wt4[i] = (el_.c4 + i < C) ? totA[min(el_.c4 + i, C - 1)] : 0.f;
+    }
+    const bool g_vec4 = DOT && (C % 4 == 0) && ((((uintptr_t)a.g) & 15) == 0);
+
+    // Lane-parallel prefixes over the range's keys for the scalar emissions (exclusive prefix at rank t = inclusive
+    // value of lane t-1): b1 state  sum_{i<t} gap_i * (base + i)  and u prefix  sum_{i<t} u_i.
+    float gci = 0.f, uli = 0.f;
+    if constexpr (ONES) gci = wave_prefix_sum(gap * (float)(base + l));
+    if constexpr (X2) uli = wave_prefix_sum(ul);
+
     const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
     const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
-    // contribution rows of this segment (ROW) and rows dotted at emission (DOT)
     const rsrc_t sr_ = ROW ? make_rsrc(a.slab + (size_t)s * Mq * a.CR, (uint32_t)((size_t)Mq * a.CR * 4))
                            : make_rsrc(nullptr, 0);
     const rsrc_t gr_ = DOT ? make_rsrc(a.g + (size_t)p * Mq * C, (uint32_t)((size_t)Mq * C * 4))
                            : make_rsrc(nullptr, 0);
     float* useg = ONES ? a.uslab + (size_t)s * Mq : nullptr;        // v == 1 contributions, sorted order
 
-    // Owned queries in blocks of 64: lane i takes query i for its rank inside the range and its distances, then the
-    // wave walks the keys (lane = channel) carrying the prefix state and emits each query at its rank.
+    // Owned queries in blocks of 64. Lane i takes query i: its rank t inside the range, its distances and its scalar
+    // outputs (v == 1 sum, rank, dot extras) from the lane-parallel prefixes; its record (row offset of rank t in the
+    // chunk buffers, query index, 2 (q - k_prev), q - k_max) goes to LDS. Then the keys are walked in 4 chunks of CH:
+    // the chunk's states PW and 2B - Btot before each key go to LDS and the queries ranked in the chunk are emitted,
+    //   row:  2 (q - k_prev) PW + (2B - Btot) - (q - k_max) Wtot,     dot:  <g_q, 2 PW - Wtot> + extra.
     for (int qb0 = q0; qb0 < q1; qb0 += WAVE) {
         const int nq = min(WAVE, q1 - qb0);
         const bool act = l < nq;
@@ -637,69 +776,110 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
         const float lq = qv - (t > 0 ? kpv : kbefore);   // distance to the last key below q (unused when none)
         const float qm = qv - kmax;
-        // per-query byte offsets of the slab row / dotted row, computed before any store is issued (see above)
-        const int rowoff = (int)(mq * (ROW ? a.CR : 0) * 4);
-        const int goff = (int)(mq * C * 4);
-        float uqv = 0.f;
-        if constexpr (X1) uqv = a.uq[(size_t)p * Mq + mq];
+        const float cnt = (float)(base + min(t, nk));    // keys below q
         if constexpr (RANK) {
             if (act) a.out_rank[(size_t)s * Mq + mq] = base + t;
         }
+        if constexpr (ONES) {
+            const float gp = __shfl(gci, max(t - 1, 0), WAVE);
+            const float b1 = B1 + (t > 0 ? gp : 0.f);
+            if (act) useg[qb0 + l] = 2.f * (lq * cnt + b1) - B1t - qm * Nf;
+        }
+        if constexpr (EXTRA) {
+            float e = 0.f;
+            if constexpr (X1) e += a.uq[(size_t)p * Mq + mq] * (2.f * cnt - Nf);
+            if constexpr (X2) {
+                const float up = __shfl(uli, max(t - 1, 0), WAVE);
+                e += 2.f * (PU + (t > 0 ? up : 0.f)) - Ut;
+            }
+            ex[l] = e;
+        }
+        if constexpr (!EMIT) continue;
+        sm.par[l] = f4_t{__int_as_float(t * RS * 4), __int_as_float((int)mq), 2.f * lq, qm};
 
         float pw[NV], bv[NV];
 #pragma unroll
-        for (int jj = 0; jj < NV; ++jj) { pw[jj] = PW[jj]; bv[jj] = Bv[jj]; }
-        float cnt = (float)base, b1 = B1, pu = PU, ubuf = 0.f;
-
-        auto emit = [&](const int j) {
-            const float lqj = bcast(lq, j), qmj = bcast(qm, j);
-            const uint32_t m = bcast(mq, j);
-            if constexpr (ROW) {
-                const int so = bcast(rowoff, j);
+        for (int j = 0; j < NV; ++j) { pw[j] = PW[j]; bv[j] = Bv[j]; }
 #pragma unroll
-                for (int jj = 0; jj < NV; ++jj) {
-                    const int c = l + WAVE * jj;
-                    if (c < C) buf_store_stream(2.f * (lqj * pw[jj] + bv[jj]) - Bt[jj] - qmj * Wt[jj], sr_, c * 4, so);
+        for (int c = 0; c < 4; ++c) {
+            const int t0 = c * CH;
+            const int j0 = (c == 0) ? 0 : __popcll(__ballot(act && t < t0));
+            const int j1 = (c == 3) ? nq : __popcll(__ballot(act && t < t0 + CH));
+            if (j1 > j0) {
+#pragma unroll
+                for (int i = 0; i < CH; ++i) {
+                    const float gt = bcast(gap, t0 + i);
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) {
+                        sm.a[i * RS + l + WAVE * j] = pw[j];
+                        if constexpr (ROW) {
+                            sm.b[i * RS + l + WAVE * j] = 2.f * bv[j] - Bt[j];
+                            bv[j] += gt * pw[j];
+                        }
+                        pw[j] += x[t0 + i][j];
+                    }
+                }
+                if (c == 3) {                             // rank RK: above every key of a full last range
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) {
+                        sm.a[CH * RS + l + WAVE * j] = pw[j];
+                        if constexpr (ROW) sm.b[CH * RS + l + WAVE * j] = 2.f * bv[j] - Bt[j];
+                    }
+                }
+                // Branch-free batches of EU iterations (indices clamped into the buffers); only queries j0 .. j1-1
+                // (ranks in [t0, t0 + CH]) store.
+                constexpr int EU = 4;
+                const int rlo = t0 * RS * 4, rhi = (t0 + CH) * RS * 4;
+                for (int jb = j0; jb < j1; jb += EU * el_.qpi) {
+                    f4_t pr[EU];
+#pragma unroll
+                    for (int u = 0; u < EU; ++u) pr[u] = sm.par[min(jb + u * el_.qpi + el_.grp, WAVE - 1)];
+                    f4_t gv[EU];
+                    if constexpr (DOT) {
+#pragma unroll
+                        for (int u = 0; u < EU; ++u) {
+                            const int goff = __float_as_int(pr[u].y) * C * 4 + el_.c4 * 4;
+                            if (g_vec4) {
+                                gv[u] = buf_load4(gr_, goff, 0);
+                            } else {
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) gv[u][i] = buf_load(gr_, goff + i * 4, 0);
+                            }
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) gv[u][i] = (el_.c4 + i < C) ? gv[u][i] : 0.f;
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < EU; ++u) {
+                        const int j = jb + u * el_.qpi + el_.grp;
+                        const int ro = min(max(__float_as_int(pr[u].x), rlo), rhi) - rlo + el_.c4 * 4;
+                        const f4_t av = *reinterpret_cast<const f4_t*>(reinterpret_cast<const char*>(sm.a) + ro);
+                        const int m = __float_as_int(pr[u].y);
+                        if constexpr (ROW) {
+                            const f4_t bw = *reinterpret_cast<const f4_t*>(reinterpret_cast<const char*>(sm.b) + ro);
+                            const f4_t o = pr[u].z * av + bw - pr[u].w * wt4;
+                            if (j < j1 && el_.ok) buf_store4_stream(o, sr_, m * a.CR * 4 + el_.c4 * 4, 0);
+                        }
+                        if constexpr (DOT) {
+                            const f4_t w2 = 2.f * av - wt4;
+                            float d = gv[u][0] * w2[0] + gv[u][1] * w2[1] + gv[u][2] * w2[2] + gv[u][3] * w2[3];
+                            for (int off = 1 << (el_.sh - 1); off >= 1; off >>= 1) d += __shfl_xor(d, off, WAVE);
+                            if constexpr (EXTRA) d += ex[min(j, WAVE - 1)];
+                            if (j < j1 && el_.c4 == 0) a.out_dot[(size_t)s * Mq + m] = a.sign * d;
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < CH; ++i) {
+                    const float gt = bcast(gap, t0 + i);
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) {
+                        if constexpr (ROW) bv[j] += gt * pw[j];
+                        pw[j] += x[t0 + i][j];
+                    }
                 }
             }
-            if constexpr (ONES) {
-                if (l == j) ubuf = 2.f * (lqj * cnt + b1) - B1t - qmj * Nf;
-            }
-            if constexpr (DOT) {
-                float acc = 0.f;
-#pragma unroll
-                for (int jj = 0; jj < NV; ++jj) {
-                    const int c = l + WAVE * jj;
-                    const float gv = buf_load(gr_, min(c, C - 1) * 4, bcast(goff, j));
-                    if (c < C) acc += gv * (2.f * pw[jj] - Wt[jj]);
-                }
-                acc = wave_sum(acc);
-                if constexpr (X1) acc += bcast(uqv, j) * (2.f * cnt - Nf);
-                if constexpr (X2) acc += 2.f * pu - Ut;
-                if (l == 0) a.out_dot[(size_t)s * Mq + m] = a.sign * acc;
-            }
-        };
-
-        int j = 0;
-        if constexpr (ROW || ONES || DOT) {
-#pragma unroll
-            for (int tt = 0; tt < RK; ++tt) {
-                const int n_at = __popcll(__ballot(act && t == tt));
-                for (int r = 0; r < n_at; ++r, ++j) emit(j);
-                const float gt = bcast(gap, tt);
-#pragma unroll
-                for (int jj = 0; jj < NV; ++jj) {
-                    if constexpr (NEED_B) bv[jj] += gt * pw[jj];
-                    pw[jj] += x[tt][jj];
-                }
-                if constexpr (ONES) b1 += gt * cnt;
-                if constexpr (X2) pu += bcast(ul, tt);
-                cnt += (tt < nk) ? 1.f : 0.f;
-            }
-            for (; j < nq; ++j) emit(j);                // rank RK: above every key of a full last range
-        }
-        if constexpr (ONES) {
-            if (act) useg[qb0 + l] = ubuf;
         }
     }
 }
