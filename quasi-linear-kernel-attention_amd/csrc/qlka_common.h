@@ -95,10 +95,9 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
 // 64-ary search: every round each lane probes one of 64 evenly spaced split points, so n = 2^17 needs 3 rounds of
 // dependent loads instead of 17. The predicate a[i] <= x is monotone, so the probes that pass form a lane prefix.
 // Must be called by all 64 lanes with the same (a, n, x).
-__device__ __forceinline__ int wave_upper_bound(const float* __restrict__ a, int n, float x) {
+__device__ __forceinline__ int wave_upper_bound_from(const float* __restrict__ a, int lo, int hi, float x) {
     const int l = lane_id();
-    int lo = 0, hi = n;                                   // answer in [lo, hi]
-    while (lo < hi) {
+    while (lo < hi) {                                     // answer in [lo, hi]
         const int span   = hi - lo;
         const int stride = (span + WAVE - 1) / WAVE;      // >= 1
         const int idx    = lo + (l + 1) * stride - 1;     // last element of lane l's block
@@ -111,6 +110,35 @@ __device__ __forceinline__ int wave_upper_bound(const float* __restrict__ a, int
     }
     return lo;
 }
+__device__ __forceinline__ int wave_upper_bound(const float* __restrict__ a, int n, float x) {
+    return wave_upper_bound_from(a, 0, n, x);
+}
+
+// The first round of an upper bound split in two so that a caller can issue other loads between them: probe()
+// loads the last element of each of 256 blocks of stride ceil(n / 256) (4 per lane), finish() counts the blocks
+// entirely <= x and continues with the 64-ary rounds inside the first block that is not.
+struct UpperBoundProbe {
+    int stride;
+    float v[4];
+    bool in[4];
+    __device__ __forceinline__ void probe(const float* __restrict__ a, int n) {
+        stride = (n + 4 * WAVE - 1) / (4 * WAVE);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int idx = (lane_id() + WAVE * r + 1) * stride - 1;
+            in[r] = idx < n;
+            v[r] = (n > 0) ? a[min(idx, n - 1)] : 0.f;    // clamped, unconditional for n > 0: all four in flight
+        }
+    }
+    __device__ __forceinline__ int finish(const float* __restrict__ a, int n, float x) const {
+        if (n <= 0) return 0;
+        int c = 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) c += __popcll(__ballot(in[r] && v[r] <= x));   // monotone in block index
+        const int lo = c * stride;
+        return wave_upper_bound_from(a, lo, min(n, lo + stride - 1), x);
+    }
+};
 
 // Workgroups are dispatched to the 8 XCDs round-robin (block b runs on XCD b % 8), each XCD with its own L2. This
 // maps the hardware block id to a logical work id such that every XCD processes one contiguous slice of the logical

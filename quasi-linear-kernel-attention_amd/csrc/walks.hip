@@ -148,97 +148,129 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
         const int c = l + WAVE * j;
         if (c < C) { ra[c] = sl[j]; rb[c] = sr[j]; }
     }
-    if (l == 0) { ra[C] = l1; rb[C] = r1; }
+    if (l == 0) {
+        ra[C] = l1;
+        rb[C] = r1;
+        // slot C+1: the scan's decays into this range from the one before (L) and after (R)
+        ra[C + 1] = (g > 0) ? __expf(-(klast - kseg[base - 1])) : 0.f;
+        rb[C + 1] = (g < G - 1) ? __expf(-(kseg[base + RK] - kfirst)) : 0.f;
+    }
 
     const int ub = wave_upper_bound(qs + (size_t)s * M, M, klast);
     if (l == 0) qb[(size_t)s * G + g] = ub;
 }
 
-// Entry L state of every range (relative to the key before the range) and exit R state (relative to the key after
-// it), in place. One wave per segment walks its G ranges; rows are prefetched in batches of 8.
+// The range scans run one workgroup of SCAN_W waves per segment. Each wave owns a contiguous piece of the segment's
+// ranges: pass 1 runs its piece from a zero state to the piece's aggregate (an affine map of the incoming state), the
+// waves exchange aggregates through LDS and compose those of the pieces before (or after) their own, and pass 2 runs
+// the piece again from the true incoming state, writing every range's entry (exit) state. Slot C+1 of every summary
+// row holds the range's link to its neighbour (a decay factor or a key gap, written by the sums kernel), so the scan
+// loop is loads and FMAs only.
+constexpr int SCAN_W = 8;
+constexpr int SCAN_BATCH = 8;      // rows loaded ahead in a piece
+
+template <int NV>
+__device__ __forceinline__ void load_scan_row(const float* __restrict__ row, const int C, float (&r)[NV + 1],
+                                              float& link) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) r[j] = row[min(lane_id() + WAVE * j, C - 1)];   // lanes >= C are never stored
+    r[NV] = row[C];
+    link = row[C + 1];
+}
+
+template <int NV>
+__device__ __forceinline__ void store_scan_row(float* __restrict__ row, const int C, const float (&r)[NV + 1]) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = lane_id() + WAVE * j;
+        if (c < C) row[c] = r[j];
+    }
+    if (lane_id() == 0) row[C] = r[NV];
+}
+
+// Laplace: entry L state of every range (relative to the last key before the range) and exit R state (relative to
+// the first key after it). Forward: L <- a_g + e^{-(klast_g - klast_{g-1})} L; backward: R <- b_g +
+// e^{-(kfirst_{g+1} - kfirst_g)} R. A piece composes to  out = local + (product of its decays) in.
 template <int NV, int RK>
-__global__ __launch_bounds__(WPB * WAVE)
-void lap_range_scan(const float* __restrict__ ks, const float* __restrict__ sa, const float* __restrict__ sb,
-                    float* __restrict__ ta, float* __restrict__ tb, const int S, const int N, const int C, const int G)
+__global__ __launch_bounds__(SCAN_W * WAVE)
+void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ ta,
+                    float* __restrict__ tb, const int S, const int C, const int G)
 {
-    const int s = blockIdx.x * WPB + wave_in_block();
-    if (s >= S) return;
-    const int l = lane_id();
+    __shared__ float agg[2][SCAN_W][NV + 1][WAVE];
+    __shared__ float span[2][SCAN_W];
+    const int s = blockIdx.x, w = wave_in_block(), l = lane_id();
     const int CS = range_stride(C);
-    const float* kseg = ks + (size_t)s * N;
     const float* SA = sa + (size_t)s * (G + 1) * CS;
     const float* SB = sb + (size_t)s * (G + 1) * CS;
     float* A = ta + (size_t)s * (G + 1) * CS;
     float* B = tb + (size_t)s * (G + 1) * CS;
-    constexpr int BATCH = 8;
+    const int per = (G + SCAN_W - 1) / SCAN_W;
+    const int glo = min(G, w * per), ghi = min(G, w * per + per);
 
-    // forward (L): entry(g) = sum over ranges < g, relative to k_last(g-1)
-    float cur[NV + 1];
+    // forward piece walk from state cur; writes entry states when OUT; returns the product of the piece's decays
+    auto fwd = [&](float (&cur)[NV + 1], const bool out) {
+        float prod = 1.f;
+        for (int g0 = glo; g0 < ghi; g0 += SCAN_BATCH) {
+            float a[SCAN_BATCH][NV + 1], dec[SCAN_BATCH];
 #pragma unroll
-    for (int j = 0; j <= NV; ++j) cur[j] = 0.f;
-    float kprev = 0.f;
-    for (int g0 = 0; g0 < G; g0 += BATCH) {
-        float a[BATCH][NV + 1], kk[BATCH];
+            for (int b = 0; b < SCAN_BATCH; ++b) load_scan_row<NV>(SA + (size_t)min(g0 + b, ghi - 1) * CS, C, a[b], dec[b]);
 #pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int g = min(g0 + b, G - 1);
+            for (int b = 0; b < SCAN_BATCH; ++b) {
+                const int g = g0 + b;
+                if (g >= ghi) break;
+                if (out) store_scan_row<NV>(A + (size_t)g * CS, C, cur);
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                a[b][j] = SA[(size_t)g * CS + min(c, C - 1)];
+                for (int j = 0; j <= NV; ++j) cur[j] = a[b][j] + dec[b] * cur[j];
+                prod *= dec[b];
             }
-            a[b][NV] = SA[(size_t)g * CS + C];
-            kk[b] = kseg[min(N, (g + 1) * RK) - 1];
         }
+        return prod;
+    };
+    // backward piece walk from state cur; writes exit states when OUT; returns the product of the piece's decays
+    auto bwd = [&](float (&cur)[NV + 1], const bool out) {
+        float prod = 1.f;
+        for (int g0 = ghi - 1; g0 >= glo; g0 -= SCAN_BATCH) {
+            float b_[SCAN_BATCH][NV + 1], dec[SCAN_BATCH];
 #pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int g = g0 + b;
-            if (g >= G) break;
-            const float dec = (g == 0) ? 0.f : __expf(-(kk[b] - kprev));
+            for (int b = 0; b < SCAN_BATCH; ++b) load_scan_row<NV>(SB + (size_t)max(g0 - b, glo) * CS, C, b_[b], dec[b]);
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                if (c < C) A[(size_t)g * CS + c] = cur[j];
+            for (int b = 0; b < SCAN_BATCH; ++b) {
+                const int g = g0 - b;
+                if (g < glo) break;
+                if (out) store_scan_row<NV>(B + (size_t)g * CS, C, cur);
+#pragma unroll
+                for (int j = 0; j <= NV; ++j) cur[j] = b_[b][j] + dec[b] * cur[j];
+                prod *= dec[b];
             }
-            if (l == 0) A[(size_t)g * CS + C] = cur[NV];
-#pragma unroll
-            for (int j = 0; j <= NV; ++j) cur[j] = a[b][j] + dec * cur[j];
-            kprev = kk[b];
         }
+        return prod;
+    };
+
+    float cf[NV + 1], cb[NV + 1];
+#pragma unroll
+    for (int j = 0; j <= NV; ++j) { cf[j] = 0.f; cb[j] = 0.f; }
+    const float pf = fwd(cf, false), pb = bwd(cb, false);
+#pragma unroll
+    for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = cf[j]; agg[1][w][j][l] = cb[j]; }
+    if (l == 0) { span[0][w] = pf; span[1][w] = pb; }
+    __syncthreads();
+
+    // incoming states: compose the aggregates of the pieces to the left (forward) and to the right (backward);
+    // empty pieces have product 1 and aggregate 0
+#pragma unroll
+    for (int j = 0; j <= NV; ++j) { cf[j] = 0.f; cb[j] = 0.f; }
+    for (int ww = 0; ww < w; ++ww) {
+        const float d = span[0][ww];
+#pragma unroll
+        for (int j = 0; j <= NV; ++j) cf[j] = agg[0][ww][j][l] + d * cf[j];
     }
-    // backward (R): exit(g) = sum over ranges > g, relative to k_first(g+1)
+    for (int ww = SCAN_W - 1; ww > w; --ww) {
+        const float d = span[1][ww];
 #pragma unroll
-    for (int j = 0; j <= NV; ++j) cur[j] = 0.f;
-    float knext = 0.f;
-    for (int g0 = G - 1; g0 >= 0; g0 -= BATCH) {
-        float b_[BATCH][NV + 1], kk[BATCH];
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int g = max(g0 - b, 0);
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                b_[b][j] = SB[(size_t)g * CS + min(c, C - 1)];
-            }
-            b_[b][NV] = SB[(size_t)g * CS + C];
-            kk[b] = kseg[g * RK];
-        }
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int g = g0 - b;
-            if (g < 0) break;
-            const float dec = (g == G - 1) ? 0.f : __expf(-(knext - kk[b]));
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                if (c < C) B[(size_t)g * CS + c] = cur[j];
-            }
-            if (l == 0) B[(size_t)g * CS + C] = cur[NV];
-#pragma unroll
-            for (int j = 0; j <= NV; ++j) cur[j] = b_[b][j] + dec * cur[j];
-            knext = kk[b];
-        }
+        for (int j = 0; j <= NV; ++j) cb[j] = agg[1][ww][j][l] + d * cb[j];
     }
+    fwd(cf, true);
+    bwd(cb, true);
 }
 
 // Emission through LDS. Each wave owns a private slice of its workgroup's LDS: the state rows of one chunk of
@@ -494,8 +526,8 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
     }
     {
         StageTimer t("lap_range_scan", st);
-        hipLaunchKernelGGL((lap_range_scan<NV, RK>), dim3((S + WPB - 1) / WPB), dim3(WPB * WAVE), 0, st,
-                           ks, ra.sa, ra.sb, ra.ta, ra.tb, S, N, C, G);
+        hipLaunchKernelGGL((lap_range_scan<NV, RK>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
+                           ra.sa, ra.sb, ra.ta, ra.tb, S, C, G);
     }
     {
         const long walk_waves = (long)S * ((G + RPW - 1) / RPW);
@@ -526,45 +558,64 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
                     const int S, const int D, const int Ns, const int Mq, const int C, const int G)
 {
+    __shared__ f4_t wts[WPB][2][RK / 4];                  // per-key weights, read four at a time as broadcasts
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
-    const int p = s / D, l = lane_id();
+    const int p = s / D, l = lane_id(), wi = wave_in_block();
     const int base = g * RK, nk = min(RK, Ns - base);
     const float* kseg = ks + (size_t)s * Ns;
+    const uint32_t* kpseg = kp + (size_t)s * Ns;
+    const float* qseg = qs + (size_t)s * Mq;
+    const float klast = kseg[base + nk - 1];
+
+    // query boundary of the range (#queries <= klast): the first probe round is in flight during the row gathers
+    UpperBoundProbe ubp;
+    ubp.probe(qseg, Mq);
 
     const int li = base + min(l, nk - 1);
     const float kl = kseg[li];
-    const uint32_t pl = kp[(size_t)s * Ns + li];
-    const float klast = kseg[base + nk - 1];
     const bool real = l < nk;
     const float dl = real ? (klast - kl) : 0.f;
+    float* wf = reinterpret_cast<float*>(wts[wi]);
+    if (l < RK) {
+        wf[l] = real ? 1.f : 0.f;                         // pad keys weigh 0
+        wf[RK + l] = dl;
+    }
 
-    const rsrc_t wr_ = make_rsrc(w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
     float sw[NV], sb[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) { sw[j] = 0.f; sb[j] = 0.f; }
+    if constexpr (WANT_W) {
+        // all RK row gathers in flight first (row indices by scalar loads), then the weighted sums
+        const rsrc_t wr_ = make_rsrc(w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
+        float x[RK][NV];
+        auto gather = [&](auto row_of) {
 #pragma unroll
-    for (int t = 0; t < RK; ++t) {
-        const uint32_t row = bcast(pl, t);
-        const float dt = bcast(dl, t);
-        const float keep = (t < nk) ? 1.f : 0.f;
+            for (int t = 0; t < RK; ++t) {
+                const int rowoff = (int)(row_of(t) * C * 4);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int c = l + WAVE * j;
-            float xv = 0.f;
-            if constexpr (WANT_W) {
-                const float xr = buf_load(wr_, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
-                xv = (c < C) ? xr * keep : 0.f;
+                for (int j = 0; j < NV; ++j) x[t][j] = buf_load(wr_, min(l + WAVE * j, C - 1) * 4, rowoff);
             }
-            sw[j] += xv;
-            sb[j] += dt * xv;
+        };
+        if (nk == RK) gather([&](int t) { return kpseg[base + t]; });
+        else          gather([&](int t) { return kpseg[base + min(t, nk - 1)]; });
+#pragma unroll
+        for (int t4 = 0; t4 < RK / 4; ++t4) {
+            const f4_t k4 = wts[wi][0][t4], d4 = wts[wi][1][t4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < NV; ++j) {            // lanes >= C are never stored
+                    sw[j] += k4[i] * x[4 * t4 + i][j];
+                    sb[j] += d4[i] * x[4 * t4 + i][j];
+                }
         }
     }
     const float b1 = wave_sum(dl);
     float u1 = 0.f;
     if constexpr (WANT_U) {
-        const float ur = u[(size_t)p * Ns + pl];
+        const float ur = u[(size_t)p * Ns + kpseg[li]];
         u1 = wave_sum(real ? ur : 0.f);
     }
 
@@ -576,74 +627,94 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
         const int c = l + WAVE * j;
         if (c < C) { ra[c] = sw[j]; rb[c] = sb[j]; }
     }
-    if (l == 0) { ra[C] = u1; rb[C] = b1; }
+    if (l == 0) {
+        ra[C] = u1;
+        rb[C] = b1;
+        ra[C + 1] = (g > 0) ? (klast - kseg[base - 1]) : 0.f;   // slot C+1: the scan's key gap into this range
+    }
 
-    const int ub = wave_upper_bound(qs + (size_t)s * Mq, Mq, klast);
+    const int ub = ubp.finish(qseg, Mq, klast);
     if (l == 0) qb[(size_t)s * G + g] = ub;
 }
 
-// Entry state (PW, B relative to the key before the range; slot C: PU, B1) of every range in place, and the totals
-// (Wtot, Btot relative to k_max; Utot, B1tot) in row G.
+// Abs: entry prefix state of every range and the segment totals (row G). State (PW, B, cnt) with B relative to the
+// last key absorbed: at range g, B <- b_g + B + gap_g PW, PW <- PW + a_g, cnt <- cnt + n_g (slot C of B uses cnt in
+// place of PW; gap_g = klast_g - klast_{g-1}). A piece composes to  PW = PW_in + sum a,  B = B_in + B_local +
+// (sum of its gaps) PW_in.
 template <int NV, int RK>
-__global__ __launch_bounds__(WPB * WAVE)
-void abs_range_scan(const float* __restrict__ ks, const float* __restrict__ sa, const float* __restrict__ sb,
-                    float* __restrict__ ta, float* __restrict__ tb, const int S, const int Ns, const int C, const int G)
+__global__ __launch_bounds__(SCAN_W * WAVE)
+void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ ta,
+                    float* __restrict__ tb, const int S, const int Ns, const int C, const int G)
 {
-    const int s = blockIdx.x * WPB + wave_in_block();
-    if (s >= S) return;
-    const int l = lane_id();
+    __shared__ float agg[2][SCAN_W][NV + 1][WAVE];
+    __shared__ float span[SCAN_W];
+    const int s = blockIdx.x, w = wave_in_block(), l = lane_id();
     const int CS = range_stride(C);
-    const float* kseg = ks + (size_t)s * Ns;
     const float* SA = sa + (size_t)s * (G + 1) * CS;
     const float* SB = sb + (size_t)s * (G + 1) * CS;
     float* A = ta + (size_t)s * (G + 1) * CS;
     float* B = tb + (size_t)s * (G + 1) * CS;
-    constexpr int BATCH = 8;
+    const int per = (G + SCAN_W - 1) / SCAN_W;
+    auto lo_of = [&](int ww) { return min(G, ww * per); };
+    auto hi_of = [&](int ww) { return min(G, ww * per + per); };
+    const int glo = lo_of(w), ghi = hi_of(w);
 
-    float pw[NV + 1], bb[NV + 1];   // slot NV: PU / B1
+    // piece walk from (pw, bb, cnt); writes entry states when OUT; returns the sum of the piece's gaps
+    auto walk = [&](float (&pw)[NV + 1], float (&bb)[NV + 1], float& cnt, const bool out) {
+        float gsum = 0.f;
+        for (int g0 = glo; g0 < ghi; g0 += SCAN_BATCH) {
+            float a[SCAN_BATCH][NV + 1], b_[SCAN_BATCH][NV + 1], gap[SCAN_BATCH], unused;
+#pragma unroll
+            for (int b = 0; b < SCAN_BATCH; ++b) {
+                const int g = min(g0 + b, ghi - 1);
+                load_scan_row<NV>(SA + (size_t)g * CS, C, a[b], gap[b]);
+                load_scan_row<NV>(SB + (size_t)g * CS, C, b_[b], unused);
+            }
+#pragma unroll
+            for (int b = 0; b < SCAN_BATCH; ++b) {
+                const int g = g0 + b;
+                if (g >= ghi) break;
+                if (out) {
+                    store_scan_row<NV>(A + (size_t)g * CS, C, pw);
+                    store_scan_row<NV>(B + (size_t)g * CS, C, bb);
+                }
+#pragma unroll
+                for (int j = 0; j < NV; ++j) { bb[j] = b_[b][j] + bb[j] + gap[b] * pw[j]; pw[j] += a[b][j]; }
+                bb[NV] = b_[b][NV] + bb[NV] + gap[b] * cnt;
+                pw[NV] += a[b][NV];
+                cnt += (float)min(RK, Ns - g * RK);
+                gsum += gap[b];
+            }
+        }
+        return gsum;
+    };
+
+    float pw[NV + 1], bb[NV + 1], cnt = 0.f;
 #pragma unroll
     for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
-    float cnt = 0.f, kprev = 0.f;
-    for (int g0 = 0; g0 < G; g0 += BATCH) {
-        float a[BATCH][NV + 1], b_[BATCH][NV + 1], kk[BATCH];
+    const float gs = walk(pw, bb, cnt, false);
 #pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int g = min(g0 + b, G - 1);
+    for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = pw[j]; agg[1][w][j][l] = bb[j]; }
+    if (l == 0) span[w] = gs;
+    __syncthreads();
+
+    // incoming state: compose the aggregates of the pieces to the left (empty pieces: all zero)
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                a[b][j]  = SA[(size_t)g * CS + min(c, C - 1)];   // unconditional; lanes >= C never stored
-                b_[b][j] = SB[(size_t)g * CS + min(c, C - 1)];
-            }
-            a[b][NV]  = SA[(size_t)g * CS + C];
-            b_[b][NV] = SB[(size_t)g * CS + C];
-            kk[b] = kseg[min(Ns, (g + 1) * RK) - 1];
-        }
+    for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
+    cnt = 0.f;
+    for (int ww = 0; ww < w; ++ww) {
+        const float sp = span[ww];
 #pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int g = g0 + b;
-            if (g >= G) break;
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                if (c < C) { A[(size_t)g * CS + c] = pw[j]; B[(size_t)g * CS + c] = bb[j]; }
-            }
-            if (l == 0) { A[(size_t)g * CS + C] = pw[NV]; B[(size_t)g * CS + C] = bb[NV]; }
-            const float gap = (g == 0) ? 0.f : (kk[b] - kprev);
-#pragma unroll
-            for (int j = 0; j < NV; ++j) { bb[j] = b_[b][j] + bb[j] + gap * pw[j]; pw[j] += a[b][j]; }
-            bb[NV] = b_[b][NV] + bb[NV] + gap * cnt;
-            pw[NV] += a[b][NV];
-            cnt += (float)min(RK, Ns - g * RK);
-            kprev = kk[b];
-        }
+        for (int j = 0; j < NV; ++j) { bb[j] += agg[1][ww][j][l] + sp * pw[j]; pw[j] += agg[0][ww][j][l]; }
+        bb[NV] += agg[1][ww][NV][l] + sp * cnt;
+        pw[NV] += agg[0][ww][NV][l];
+        cnt += (float)(min(Ns, hi_of(ww) * RK) - min(Ns, lo_of(ww) * RK));
     }
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int c = l + WAVE * j;
-        if (c < C) { A[(size_t)G * CS + c] = pw[j]; B[(size_t)G * CS + c] = bb[j]; }
+    walk(pw, bb, cnt, true);
+    if (ghi == G && glo < G) {                            // the wave whose piece ends the segment writes the totals
+        store_scan_row<NV>(A + (size_t)G * CS, C, pw);
+        store_scan_row<NV>(B + (size_t)G * CS, C, bb);
     }
-    if (l == 0) { A[(size_t)G * CS + C] = pw[NV]; B[(size_t)G * CS + C] = bb[NV]; }
 }
 
 template <int NV, int RK, int MODE>
@@ -913,8 +984,8 @@ static int abs_walk_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_
     }
     {
         StageTimer t("abs_range_scan", st);
-        hipLaunchKernelGGL((abs_range_scan<NV, RK>), dim3((S + WPB - 1) / WPB), dim3(WPB * WAVE), 0, st,
-                           a.ks, ra.sa, ra.sb, ra.ta, ra.tb, S, a.Ns, a.C, G);
+        hipLaunchKernelGGL((abs_range_scan<NV, RK>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
+                           ra.sa, ra.sb, ra.ta, ra.tb, S, a.Ns, a.C, G);
     }
     switch (mode) {
         case ABS_ROW:                         launch_abs_walk<NV, RK, ABS_ROW>(a, ra, G, st); break;
