@@ -42,11 +42,15 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
     const int lane = tid & (WAVE - 1);
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (WAVE - lane));
 
+    float f[ITEMS];
+#pragma unroll
+    for (int r = 0; r < ITEMS; ++r) f[r] = src[min(tid + r * THREADS, len - 1)];   // clamped: all ITEMS in flight
 #pragma unroll
     for (int r = 0; r < ITEMS; ++r) {
         const int i = tid + r * THREADS;
-        const float f = src[min(i, len - 1)];             // unconditional (clamped) load: all ITEMS stay in flight
-        skey[i] = (i < len) ? float_to_ordered(f) : 0xffffffffu;   // pads sort after every finite or infinite key
+        // pads become 0xffffffff and sort after every key; f is used unconditionally so that the compiler keeps
+        // the loads above unpredicated (a predicated load would wait for each one in turn)
+        skey[i] = float_to_ordered(f[r]) | ((i < len) ? 0u : 0xffffffffu);
         sidx[i] = (uint32_t)i;                            // index inside the run (< 16384)
     }
 
