@@ -160,12 +160,16 @@ def main():
     units = P * M * D
     value = 2 * units / (ms_per_step / 1e3)
 
-    # dominant kernel and its roofline (per-unit algorithmic bytes x units per launch / launch duration)
-    dom = max(stages, key=lambda s: stages[s]["ms_total"])
+    # Dominant kernel = longest launch; its roofline = algorithmic bytes per launch / launch duration. A walk launch
+    # reads the sorted k and q segments, streams v once in sorted order and emits the M*C contributions + M scalars of
+    # one op call: exactly B_scan (per-unit figure x P*D*M units). Other kernels get their own algorithmic bytes.
+    dom = max(stages, key=lambda s: stages[s]["ms_per_launch"])
     per_unit = bscan_bytes_per_unit(N, M, C)
-    bytes_per_launch = per_unit * units
-    if dom in ("lds_radix_sort",):   # sort: read keys, write sorted keys + perm (12 B per key)
-        bytes_per_launch = 12.0 * P * D * N
+    algo_bytes = {
+        "lds_radix_sort": 12.0 * P * D * N,                  # read keys, write sorted keys + perm
+        "slab_reduce": 4.0 * P * M * C * (D + 1),            # read D contribution rows, write one row per query
+    }
+    bytes_per_launch = algo_bytes.get(dom, per_unit * units)
     achieved = bytes_per_launch / (stages[dom]["ms_per_launch"] / 1e3) / 1e9
     roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(dom),
