@@ -195,6 +195,18 @@ def main():
     bscan = per_unit * units
     op_roof = {kk: round(bscan / (vv / 1e3) / 1e9 / HBM_PEAK_GBS, 4) for kk, vv in op_ms.items()}
 
+    # The three attention layers of configs[3] on the same q, k, v (already tau-scaled inputs do not change the
+    # work): fused (one library call: ops + epilogue, add_bump's three abs sums sharing one sort) vs the reference's
+    # composition (separate op calls + torch epilogue, attention.py:67-92).
+    from qlka import layers
+    layer_ms = {}
+    with torch.no_grad():
+        for kern in layers.KINDS:
+            layer_ms[kern] = {
+                "fused": round(op_time(lambda: layers.layer_forward(kern, q, k, v)), 4),
+                "unfused": round(op_time(lambda: layers.unfused(kern, q, k, v)), 4),
+            }
+
     out = {
         "metric": METRIC,
         "value": value,
@@ -214,6 +226,7 @@ def main():
         "roofline": roof,
         "op_ms": {kk: round(vv, 4) for kk, vv in op_ms.items()},
         "op_bscan_roofline_frac": op_roof,
+        "layer_ms": layer_ms,
         "stages": {kk: round(vv["ms_per_launch"], 4) for kk, vv in stages.items()},
         "device": torch.cuda.get_device_name(dev),
     }

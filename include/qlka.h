@@ -70,6 +70,26 @@ int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g,
                  int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Fused additive-kernel attention layer, forward: the op(s) plus the normalising epilogue in one call.
+ *   kind QLKA_ADD_LAPLACE: out = w / clamp(u - n_pad sum_d e^{-|q_d|}, 1e-6), (w, u) = weighted_laplace_sum(q, k, v)
+ *   kind QLKA_ADD_RIESZ:   out = ((|q|_1 + 1e-3) sum_n v_n + sum_n |k_n|_1 v_n - w)
+ *                               / clamp((|q|_1 + 1e-3) M + sum_n |k_n|_1 - u - 1e-3 n_pad, 1e-6),
+ *                          (w, u) = weighted_abs_sum_full(q, k, v)
+ *   kind QLKA_ADD_BUMP:    out = ((w+ + w-)/2 - w0) / clamp((u+ + u-)/2 - u0 - n_pad sum_d max(0, 1 - |q_d|), 1e-6),
+ *                          (w0, u0), (w+, u+), (w-, u-) = weighted_abs_sum_full at q, q + 1, q - 1; the three share one
+ *                          sort of k and q and one set of key-range summaries.
+ * q (P, D, M) and k (P, D, N) already divided by tau, k and v already multiplied by the key mask; n_pad (P) is the
+ * number of masked keys per p (NULL: none); out (P, M, C). No gradient.
+ * Replaces _add_laplace / _add_riesz / _add_bump (Experiments/kernel_attention/attention.py:67-92).
+ */
+#define QLKA_ADD_LAPLACE 0
+#define QLKA_ADD_RIESZ   1
+#define QLKA_ADD_BUMP    2
+size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C);
+int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad, float* out,
+                   int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Test entry: stable ascending sort of num_segs contiguous segments of seg_len fp32 keys; perm[i] is the in-segment
  * index of the i-th smallest key (np.argsort(kind="stable"); -0.0 ties +0.0 and is written as +0.0).
  * Replaces launch_iota + launch_cub_sort (Weighted_Abs_Sum/csrc/sort_utils.cu:85-117).

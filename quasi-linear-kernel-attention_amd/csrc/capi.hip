@@ -244,6 +244,121 @@ int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g,
     return hip_status(e, "sgn walk");
 }
 
+// ------------------------------------------------------------------------------------------- fused attention layers
+// Workspace: the op's (sorted k/q, ranges, slab) + per op evaluation a (P, M, C) + (P, M) pair of out_w / out_u
+// (three for add_bump) + the add_riesz prefixes + the query boundaries of add_bump's two shifted query sets.
+namespace {
+struct LayerWs {
+    SortedWs op;
+    float* w[3]; float* u[3];
+    void* pre; int* qb[2];
+    float* qt;
+};
+
+size_t layer_part(int kind, const WsSpec& s, int i) {
+    const size_t PMC = (size_t)s.P * s.M * s.C, PM = (size_t)s.P * s.M;
+    const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
+    switch (i) {
+        case 0: return ws_bytes(s);
+        case 1: return nev * (align256(PMC * 4) + align256(PM * 4)) + align256(PM * 4);   // + per-query terms
+        case 2: return kind == LAYER_ADD_RIESZ ? align256(riesz_prefix_bytes(s.P, s.N, s.C)) : 0;
+        case 3: return kind == LAYER_ADD_BUMP
+                       ? 2 * align256((size_t)s.P * s.D * range_count(s.N, s.C) * sizeof(int)) : 0;
+    }
+    return 0;
+}
+
+size_t layer_ws_bytes(int kind, const WsSpec& s) {
+    size_t b = 0;
+    for (int i = 0; i < 4; ++i) b += layer_part(kind, s, i);
+    return b;
+}
+
+LayerWs carve_layer(int kind, void* ws, const WsSpec& s) {
+    LayerWs r{};
+    char* b = (char*)ws;
+    r.op = carve(b, s);
+    b += layer_part(kind, s, 0);
+    const size_t PMC = (size_t)s.P * s.M * s.C, PM = (size_t)s.P * s.M;
+    const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
+    for (int e = 0; e < nev; ++e) {
+        r.w[e] = (float*)b; b += align256(PMC * 4);
+        r.u[e] = (float*)b; b += align256(PM * 4);
+    }
+    r.qt = (float*)b; b += align256(PM * 4);
+    r.pre = layer_part(kind, s, 2) ? (void*)b : nullptr;
+    b += layer_part(kind, s, 2);
+    if (kind == LAYER_ADD_BUMP) {
+        const size_t qbb = align256((size_t)s.P * s.D * range_count(s.N, s.C) * sizeof(int));
+        r.qb[0] = (int*)b; b += qbb;
+        r.qb[1] = (int*)b;
+    }
+    return r;
+}
+}  // namespace
+
+size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C) {
+    if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || kind < 0 || kind > 2) return 0;
+    return layer_ws_bytes(kind, WsSpec{P, D, N, M, C, N, M, true});
+}
+
+int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad, float* out,
+                   int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
+    g_err.clear();
+    if (kind < 0 || kind > 2) return fail(QLKA_EINVAL, "kind must be 0 (add_laplace), 1 (add_riesz) or 2 (add_bump)");
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !out) return fail(QLKA_EINVAL, "q, k, v and out must be non-null");
+    const WsSpec spec{P, D, N, M, C, N, M, true};
+    if (int e = check_ws(ws, ws_bytes_given, layer_ws_bytes(kind, spec))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    const int S = P * D;
+    LayerWs L = carve_layer(kind, ws, spec);
+    SortedWs& w = L.op;
+    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+    int e = 0;
+    if (kind == LAYER_ADD_LAPLACE) {
+        e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+        if (e) return hip_status(e, "laplace walk");
+        e = reduce_slabs(w.slab, w.uslab, w.qinv, L.w[0], L.u[0], P, D, M, C, st);
+        if (e) return hip_status(e, "laplace reduce");
+    } else {
+        AbsWalkArgs a{};
+        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
+        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
+        a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
+        a.out_dot = nullptr; a.out_rank = nullptr;
+        a.sign = 1.f; a.P = P; a.D = D; a.C = C; a.qshift = 0.f;
+        const int mode = ABS_ROW | ABS_ONES;
+        // one sort of k and q, one set of range summaries and one scan serve every query shift: q + s has the sorted
+        // order of q, and the key side does not depend on the queries
+        e = abs_prepare(a, mode, w.ra, st);
+        if (e) return hip_status(e, "abs ranges");
+        const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
+        const float shift[3] = {0.f, 1.f, -1.f};
+        for (int ev = 0; ev < nev; ++ev) {
+            RangeArrays ra = w.ra;
+            a.qshift = shift[ev];
+            if (ev > 0) {
+                ra.qb = L.qb[ev - 1];
+                e = range_bounds(a, ra.qb, st);
+                if (e) return hip_status(e, "query bounds");
+            }
+            e = abs_emit(a, mode, ra, st);
+            if (e) return hip_status(e, "abs walk");
+            e = reduce_slabs(w.slab, w.uslab, w.qinv, L.w[ev], L.u[ev], P, D, M, C, st);
+            if (e) return hip_status(e, "abs reduce");
+        }
+        if (kind == LAYER_ADD_RIESZ) {
+            e = riesz_prefix(k, v, L.pre, P, D, N, C, st);
+            if (e) return hip_status(e, "riesz prefixes");
+        }
+    }
+    const bool bump = kind == LAYER_ADD_BUMP;
+    e = layer_epilogue(kind, q, n_pad, L.w[0], L.u[0], bump ? L.w[1] : nullptr, bump ? L.u[1] : nullptr,
+                       bump ? L.w[2] : nullptr, bump ? L.u[2] : nullptr, L.pre, L.qt, out, P, D, N, M, C, st);
+    return hip_status(e, "layer epilogue");
+}
+
 // ------------------------------------------------------------------------------------------------ test entries
 size_t qlka_seg_sort_ws_bytes(int num_segs, int seg_len) {
     if (num_segs <= 0 || seg_len <= 0) return 0;

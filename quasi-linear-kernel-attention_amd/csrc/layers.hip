@@ -1,0 +1,193 @@
+// Fused epilogues of the three additive-kernel attention layers around the operators
+// (Experiments/kernel_attention/attention.py:67-92, the branch attention.py:119-125 takes for add_laplace,
+// add_riesz and add_bump):
+//
+//   add_laplace:  out = w / clamp(u - n_pad * sum_d e^{-|q_d|}, CLAMP)                       (attention.py:67-72)
+//   add_riesz:    num = (|q|_1 + EPS) * sum_n v_n + sum_n |k_n|_1 v_n - w
+//                 den = (|q|_1 + EPS) * S + sum_n |k_n|_1 - u - EPS * n_pad,  out = num / clamp(den, CLAMP)
+//                                                                                            (attention.py:75-81)
+//   add_bump:     num = (w+ + w-) / 2 - w0,  den = (u+ + u-) / 2 - u0 - n_pad * sum_d max(0, 1 - |q_d|)
+//                 out = num / clamp(den, CLAMP), with (w, u) of the abs op at q, q + 1 and q - 1  (attention.py:84-92)
+//
+// with CLAMP = 1e-6 (attention.py:20), EPS = 1e-3 (kernels.py:9) and S = q.shape[2] (the number of queries, as the
+// reference writes it). Every expression keeps the reference's operation order in fp32. The per-query d-reductions
+// (sum_d e^{-|q_d|}, |q|_1, sum_d max(0, 1 - |q_d|)) are computed once per query before the per-channel pass.
+#include "qlka_common.h"
+#include "qlka_internal.h"
+
+namespace qlka {
+
+constexpr float LAYER_CLAMP = 1e-6f;
+constexpr float LAYER_EPS = 1e-3f;
+constexpr int RZ_NB = 64;          // key chunks per p of the add_riesz prefix pass
+constexpr int RZ_T = 256;          // threads per block of the layer kernels
+
+static inline size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// pre layout: vsum (P, C) | akv (P, C) | sak (P) | partials (P, RZ_NB, 2C + 1)
+size_t riesz_prefix_bytes(int P, int N, int C) {
+    (void)N;
+    return 2 * al256((size_t)P * C * 4) + al256((size_t)P * 4) + al256((size_t)P * RZ_NB * (2 * C + 1) * 4);
+}
+
+// One block per (p, key chunk): |k_n|_1 of the chunk's keys into LDS, then per channel the chunk's sum_n v and
+// sum_n |k_n|_1 v (G = RZ_T / C row groups per channel, combined in LDS), and the chunk's sum_n |k_n|_1.
+__global__ __launch_bounds__(RZ_T)
+void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ part,
+                    const int D, const int N, const int C)
+{
+    __shared__ float aks[(131072 + RZ_NB - 1) / RZ_NB];
+    __shared__ float red[2][RZ_T];
+    const int p = blockIdx.x / RZ_NB, b = blockIdx.x - p * RZ_NB, tid = threadIdx.x;
+    const int chunk = (N + RZ_NB - 1) / RZ_NB;
+    const int n0 = min(N, b * chunk), n1 = min(N, n0 + chunk);
+    const float* kp = k + (size_t)p * D * N;
+    float sak = 0.f;
+    for (int n = n0 + tid; n < n1; n += RZ_T) {
+        float a = 0.f;
+        for (int d = 0; d < D; ++d) a += fabsf(kp[(size_t)d * N + n]);
+        aks[n - n0] = a;
+        sak += a;
+    }
+    __syncthreads();
+    const int G = RZ_T / C;                               // >= 2 for C <= 128
+    const int c = tid % C, rg = tid / C;
+    float sv = 0.f, skv = 0.f;
+    if (rg < G) {
+        const float* vp = v + (size_t)p * N * C;
+        for (int n = n0 + rg; n < n1; n += G) {
+            const float x = vp[(size_t)n * C + c];
+            sv += x;
+            skv += aks[n - n0] * x;
+        }
+    }
+    red[0][tid] = sv;
+    red[1][tid] = skv;
+    __syncthreads();
+    float* out = part + ((size_t)p * RZ_NB + b) * (2 * C + 1);
+    if (tid < C) {
+        float a0 = 0.f, a1 = 0.f;
+        for (int r = 0; r < G; ++r) { a0 += red[0][r * C + tid]; a1 += red[1][r * C + tid]; }
+        out[tid] = a0;
+        out[C + tid] = a1;
+    }
+    __syncthreads();
+    red[0][tid] = sak;
+    __syncthreads();
+    for (int off = RZ_T / 2; off >= 1; off >>= 1) {
+        if (tid < off) red[0][tid] += red[0][tid + off];
+        __syncthreads();
+    }
+    if (tid == 0) out[2 * C] = red[0][0];
+}
+
+// Chunk partials summed in chunk order (deterministic): one thread per (p, j), j < 2C + 1.
+__global__ __launch_bounds__(RZ_T)
+void riesz_finish(const float* __restrict__ part, float* __restrict__ vsum, float* __restrict__ akv,
+                  float* __restrict__ sak, const int P, const int C)
+{
+    const int W = 2 * C + 1;
+    const int i = blockIdx.x * RZ_T + threadIdx.x;
+    if (i >= P * W) return;
+    const int p = i / W, j = i - p * W;
+    float a = 0.f;
+    for (int b = 0; b < RZ_NB; ++b) a += part[((size_t)p * RZ_NB + b) * W + j];
+    if (j < C) vsum[(size_t)p * C + j] = a;
+    else if (j < 2 * C) akv[(size_t)p * C + (j - C)] = a;
+    else sak[p] = a;
+}
+
+int riesz_prefix(const float* k, const float* v, void* pre, int P, int D, int N, int C, hipStream_t st) {
+    char* b = (char*)pre;
+    float* vsum = (float*)b;  b += al256((size_t)P * C * 4);
+    float* akv = (float*)b;   b += al256((size_t)P * C * 4);
+    float* sak = (float*)b;   b += al256((size_t)P * 4);
+    float* part = (float*)b;
+    StageTimer t("riesz_prefix", st);
+    hipLaunchKernelGGL(riesz_partials, dim3((unsigned)(P * RZ_NB)), dim3(RZ_T), 0, st, k, v, part, D, N, C);
+    const int n = P * (2 * C + 1);
+    hipLaunchKernelGGL(riesz_finish, dim3((unsigned)((n + RZ_T - 1) / RZ_T)), dim3(RZ_T), 0, st, part, vsum, akv, sak,
+                       P, C);
+    return (int)hipGetLastError();
+}
+
+// Per (p, m): the reduction over d of the layer's query-only term (e^{-|q|}, |q| or max(0, 1 - |q|)); one thread per
+// query, d in order, coalesced across m.
+template <int KIND>
+__global__ __launch_bounds__(RZ_T)
+void layer_query_terms(const float* __restrict__ q, float* __restrict__ qt, const int P, const int D, const int M)
+{
+    const long i = (long)blockIdx.x * RZ_T + threadIdx.x;
+    if (i >= (long)P * M) return;
+    const int p = (int)(i / M), m = (int)(i - (long)p * M);
+    const float* qc = q + (size_t)p * D * M + m;
+    float a = 0.f;
+    for (int d = 0; d < D; ++d) {
+        const float x = fabsf(qc[(size_t)d * M]);
+        if constexpr (KIND == LAYER_ADD_LAPLACE) a += expf(-x);
+        else if constexpr (KIND == LAYER_ADD_RIESZ) a += x;
+        else a += fmaxf(1.f - x, 0.f);
+    }
+    qt[i] = a;
+}
+
+// Every channel of the output rows: one thread per (p, m, c).
+template <int KIND>
+__global__ __launch_bounds__(RZ_T)
+void layer_epilogue_kernel(const float* __restrict__ qt, const float* __restrict__ n_pad,
+                           const float* __restrict__ w0, const float* __restrict__ u0,
+                           const float* __restrict__ wp, const float* __restrict__ up,
+                           const float* __restrict__ wm, const float* __restrict__ um,
+                           const float* __restrict__ vsum, const float* __restrict__ akv, const float* __restrict__ sak,
+                           float* __restrict__ out, const int P, const int M, const int C)
+{
+    const long i = (long)blockIdx.x * RZ_T + threadIdx.x;
+    if (i >= (long)P * M * C) return;
+    const long pm = i / C;
+    const int c = (int)(i - pm * C);
+    const int p = (int)(pm / M);
+    const float np = n_pad ? n_pad[p] : 0.f;
+    float num, den;
+    if constexpr (KIND == LAYER_ADD_LAPLACE) {
+        num = w0[i];
+        den = u0[pm] - np * qt[pm];
+    } else if constexpr (KIND == LAYER_ADD_RIESZ) {
+        const float aqe = qt[pm] + LAYER_EPS;
+        num = aqe * vsum[(size_t)p * C + c] + akv[(size_t)p * C + c] - w0[i];
+        den = aqe * (float)M + sak[p] - u0[pm] - LAYER_EPS * np;
+    } else {
+        num = (wp[i] + wm[i]) / 2.f - w0[i];
+        den = (up[pm] + um[pm]) / 2.f - u0[pm] - np * qt[pm];
+    }
+    out[i] = num / fmaxf(den, LAYER_CLAMP);
+}
+
+int layer_epilogue(int kind, const float* q, const float* n_pad, const float* w0, const float* u0,
+                   const float* wp, const float* up, const float* wm, const float* um, const void* pre, float* qt,
+                   float* out, int P, int D, int N, int M, int C, hipStream_t st) {
+    const float *vsum = nullptr, *akv = nullptr, *sak = nullptr;
+    if (kind == LAYER_ADD_RIESZ) {
+        const char* b = (const char*)pre;
+        vsum = (const float*)b;  b += al256((size_t)P * C * 4);
+        akv = (const float*)b;   b += al256((size_t)P * C * 4);
+        sak = (const float*)b;
+    }
+    (void)N;
+    const long nq = (long)P * M, n = nq * C;
+    const unsigned qblocks = (unsigned)((nq + RZ_T - 1) / RZ_T), blocks = (unsigned)((n + RZ_T - 1) / RZ_T);
+    StageTimer t("layer_epilogue", st);
+#define QLKA_LAYER_LAUNCH(K)                                                                                        \
+    hipLaunchKernelGGL(layer_query_terms<K>, dim3(qblocks), dim3(RZ_T), 0, st, q, qt, P, D, M);                    \
+    hipLaunchKernelGGL(layer_epilogue_kernel<K>, dim3(blocks), dim3(RZ_T), 0, st, qt, n_pad, w0, u0, wp, up, wm, um, \
+                       vsum, akv, sak, out, P, M, C)
+    switch (kind) {
+        case LAYER_ADD_LAPLACE: QLKA_LAYER_LAUNCH(LAYER_ADD_LAPLACE); break;
+        case LAYER_ADD_RIESZ:   QLKA_LAYER_LAUNCH(LAYER_ADD_RIESZ); break;
+        case LAYER_ADD_BUMP:    QLKA_LAYER_LAUNCH(LAYER_ADD_BUMP); break;
+        default: return (int)hipErrorInvalidValue;
+    }
+#undef QLKA_LAYER_LAUNCH
+    return (int)hipGetLastError();
+}
+
+}  // namespace qlka

@@ -95,13 +95,15 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
 // 64-ary search: every round each lane probes one of 64 evenly spaced split points, so n = 2^17 needs 3 rounds of
 // dependent loads instead of 17. The predicate a[i] <= x is monotone, so the probes that pass form a lane prefix.
 // Must be called by all 64 lanes with the same (a, n, x).
-__device__ __forceinline__ int wave_upper_bound_from(const float* __restrict__ a, int lo, int hi, float x) {
+// With a shift, the array searched is a[i] + shift (fp32 addition is monotone, so it is still ascending).
+__device__ __forceinline__ int wave_upper_bound_from(const float* __restrict__ a, int lo, int hi, float x,
+                                                     float shift = 0.f) {
     const int l = lane_id();
     while (lo < hi) {                                     // answer in [lo, hi]
         const int span   = hi - lo;
         const int stride = (span + WAVE - 1) / WAVE;      // >= 1
         const int idx    = lo + (l + 1) * stride - 1;     // last element of lane l's block
-        const bool ok    = (idx < hi) && (a[idx] <= x);
+        const bool ok    = (idx < hi) && (a[idx] + shift <= x);
         const int c      = __popcll(__ballot(ok));        // blocks entirely <= x
         const int nlo    = lo + c * stride;
         const int nhi    = min(hi, nlo + stride - 1);
@@ -130,13 +132,13 @@ struct UpperBoundProbe {
             v[r] = (n > 0) ? a[min(idx, n - 1)] : 0.f;    // clamped, unconditional for n > 0: all four in flight
         }
     }
-    __device__ __forceinline__ int finish(const float* __restrict__ a, int n, float x) const {
+    __device__ __forceinline__ int finish(const float* __restrict__ a, int n, float x, float shift = 0.f) const {
         if (n <= 0) return 0;
         int c = 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) c += __popcll(__ballot(in[r] && v[r] <= x));   // monotone in block index
+        for (int r = 0; r < 4; ++r) c += __popcll(__ballot(in[r] && v[r] + shift <= x));   // monotone in block
         const int lo = c * stride;
-        return wave_upper_bound_from(a, lo, min(n, lo + stride - 1), x);
+        return wave_upper_bound_from(a, lo, min(n, lo + stride - 1), x, shift);
     }
 };
 

@@ -91,7 +91,28 @@ struct AbsWalkArgs {
     int32_t* out_rank;       // (P, D, Mq)
     float sign;
     int P, D, C;
+    float qshift;            // added to every query value (0: the queries as given); the sorted order is unchanged
 };
+// sums + scan + walk
 int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
+// the two halves of abs_walk: range summaries, query boundaries (for a.qshift) and scan; then the walk alone, which
+// may run several times over one prepared ra with different qshift / ra.qb
+int abs_prepare(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
+int abs_emit(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
+// query boundaries of every key range for queries shifted by qshift (what abs_prepare writes to ra.qb for a.qshift)
+int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st);
+int range_count(int Ns, int C);          // key ranges per segment
+
+// Fused attention-layer epilogues (layers.hip)
+enum LayerKind { LAYER_ADD_LAPLACE = 0, LAYER_ADD_RIESZ = 1, LAYER_ADD_BUMP = 2 };
+size_t riesz_prefix_bytes(int P, int N, int C);
+// add_riesz per-p constants: vsum[p][c] = sum_n v, akv[p][c] = sum_n |k_n|_1 v_n, sak[p] = sum_n |k_n|_1 (pre must
+// hold riesz_prefix_bytes)
+int riesz_prefix(const float* k, const float* v, void* pre, int P, int D, int N, int C, hipStream_t st);
+// out[p][m][:] from the op outputs: w0/u0 (and, for add_bump, w+/u+ and w-/u- of q + 1 and q - 1)
+// qt: (P, M) scratch for the per-query d-reductions
+int layer_epilogue(int kind, const float* q, const float* n_pad, const float* w0, const float* u0,
+                   const float* wp, const float* up, const float* wm, const float* um, const void* pre, float* qt,
+                   float* out, int P, int D, int N, int M, int C, hipStream_t st);
 
 }  // namespace qlka

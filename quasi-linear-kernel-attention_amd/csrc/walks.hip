@@ -556,7 +556,8 @@ __global__ __launch_bounds__(WPB * WAVE)
 void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
                     const float* __restrict__ w, const float* __restrict__ u,
                     float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
-                    const int S, const int D, const int Ns, const int Mq, const int C, const int G)
+                    const int S, const int D, const int Ns, const int Mq, const int C, const int G,
+                    const float qshift)
 {
     __shared__ f4_t wts[WPB][2][RK / 4];                  // per-key weights, read four at a time as broadcasts
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
@@ -633,8 +634,25 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
         ra[C + 1] = (g > 0) ? (klast - kseg[base - 1]) : 0.f;   // slot C+1: the scan's key gap into this range
     }
 
-    const int ub = ubp.finish(qseg, Mq, klast);
+    const int ub = ubp.finish(qseg, Mq, klast, qshift);
     if (l == 0) qb[(size_t)s * G + g] = ub;
+}
+
+// Query boundaries alone (what the sums kernels write to qb), for queries shifted by qshift: one wave per range.
+template <int RK>
+__global__ __launch_bounds__(WPB * WAVE)
+void range_bounds_kernel(const float* __restrict__ ks, const float* __restrict__ qs, int* __restrict__ qb,
+                         const float qshift, const int S, const int Ns, const int Mq, const int G)
+{
+    const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
+    if (wv >= (long)S * G) return;
+    const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
+    const float klast = ks[(size_t)s * Ns + min(Ns, (g + 1) * RK) - 1];
+    const float* qseg = qs + (size_t)s * Mq;
+    UpperBoundProbe ubp;
+    ubp.probe(qseg, Mq);
+    const int ub = ubp.finish(qseg, Mq, klast, qshift);
+    if (lane_id() == 0) qb[(size_t)s * G + g] = ub;
 }
 
 // Abs: entry prefix state of every range and the segment totals (row G). State (PW, B, cnt) with B relative to the
@@ -841,7 +859,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         const int nq = min(WAVE, q1 - qb0);
         const bool act = l < nq;
         const int qi = min(qb0 + l, q1 - 1);              // clamped: unconditional loads
-        const float qv = qseg[qi];
+        const float qv = qseg[qi] + a.qshift;
         const uint32_t mq = qpseg[qi];
         const int t = range_rank<RK>(kl, nk, qv);
         const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
@@ -965,7 +983,7 @@ static void launch_abs_walk(const AbsWalkArgs& a, RangeArrays ra, int G, hipStre
 }
 
 template <int NV, int RK>
-static int abs_walk_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
+static int abs_prepare_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
     const int S = a.P * a.D;
     const int G = (a.Ns + RK - 1) / RK;
     const long waves = (long)S * G;
@@ -974,19 +992,25 @@ static int abs_walk_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_
         StageTimer t("abs_range_sums", st);
         if (mode & ABS_DOTX2)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, true>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G, a.qshift);
         else if (mode == ABS_RANK)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, false, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G, a.qshift);
         else
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G);
+                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G, a.qshift);
     }
     {
         StageTimer t("abs_range_scan", st);
         hipLaunchKernelGGL((abs_range_scan<NV, RK>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
                            ra.sa, ra.sb, ra.ta, ra.tb, S, a.Ns, a.C, G);
     }
+    return (int)hipGetLastError();
+}
+
+template <int NV, int RK>
+static int abs_emit_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
+    const int G = (a.Ns + RK - 1) / RK;
     switch (mode) {
         case ABS_ROW:                         launch_abs_walk<NV, RK, ABS_ROW>(a, ra, G, st); break;
         case ABS_ROW | ABS_ONES:              launch_abs_walk<NV, RK, ABS_ROW | ABS_ONES>(a, ra, G, st); break;
@@ -1001,9 +1025,39 @@ static int abs_walk_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_
     return (int)hipGetLastError();
 }
 
+int range_count(int Ns, int C) {
+    const int RK = range_keys(C);
+    return (Ns + RK - 1) / RK;
+}
+
+int abs_prepare(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
+    if (a.C <= WAVE) return abs_prepare_t<1, 64>(a, mode, ra, st);
+    return abs_prepare_t<2, 32>(a, mode, ra, st);
+}
+
+int abs_emit(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
+    if (a.C <= WAVE) return abs_emit_t<1, 64>(a, mode, ra, st);
+    return abs_emit_t<2, 32>(a, mode, ra, st);
+}
+
 int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
-    if (a.C <= WAVE) return abs_walk_t<1, 64>(a, mode, ra, st);
-    return abs_walk_t<2, 32>(a, mode, ra, st);
+    if (int e = abs_prepare(a, mode, ra, st)) return e;
+    return abs_emit(a, mode, ra, st);
+}
+
+int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st) {
+    const int S = a.P * a.D;
+    const int G = range_count(a.Ns, a.C);
+    const long waves = (long)S * G;
+    const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
+    StageTimer t("range_bounds", st);
+    if (a.C <= WAVE)
+        hipLaunchKernelGGL((range_bounds_kernel<64>), dim3(blocks), dim3(WPB * WAVE), 0, st, a.ks, a.qs, qb, a.qshift,
+                           S, a.Ns, a.Mq, G);
+    else
+        hipLaunchKernelGGL((range_bounds_kernel<32>), dim3(blocks), dim3(WPB * WAVE), 0, st, a.ks, a.qs, qb, a.qshift,
+                           S, a.Ns, a.Mq, G);
+    return (int)hipGetLastError();
 }
 
 }  // namespace qlka

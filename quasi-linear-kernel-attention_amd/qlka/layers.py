@@ -1,0 +1,141 @@
+"""Fused additive-kernel attention layers (add_laplace, add_riesz, add_bump) over libqlka's qlka_layer_fwd.
+
+Mirrors Experiments/kernel_attention/attention.py:
+  * add_laplace / add_riesz / add_bump(q, k, v, n_pad) are attention.py:67-92 (`_add_laplace`, `_add_riesz`,
+    `_add_bump`): q (P, D, S) and k (P, D, N) already divided by tau, k and v already multiplied by the key mask,
+    n_pad the number of masked keys per p (0 or a (P,) / (P, 1) tensor); returns (P, S, C).
+  * attention(q, k, v, kernel, tau, keep=None) is the additive-kernel branch of attention() (attention.py:95-126):
+    (B, H, S, D) in and out, tau scaling, key mask.
+
+Forward through one library call per layer: the op(s) and the normalising epilogue run on the GPU in one stream of
+kernels, and add_bump's three abs sums (q, q + 1, q - 1) share one sort of k and q and one set of key-range
+summaries. The fused call has no gradient. When a gradient is needed, add_riesz and add_bump evaluate the reference's
+own formulas over the differentiable weighted_abs_sum_full (the same arithmetic as attention.py:75-92); add_laplace
+raises like weighted_laplace_sum, which has no backward (attention.py:110-114 routes that case elsewhere).
+"""
+
+import torch
+
+from . import _lib
+
+CLAMP = 1e-6    # attention.py:20
+EPS = 1e-3      # kernels.py:9
+KINDS = {"add_laplace": 0, "add_riesz": 1, "add_bump": 2}
+
+
+def _check(q, k, v):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not t.is_cuda:
+            raise RuntimeError(f"{name} must be a CUDA tensor")
+        if t.dtype != torch.float32:
+            raise RuntimeError(f"{name} must be float32")
+        if t.dim() != 3:
+            raise RuntimeError(f"{name} must be 3D")
+    if q.shape[0] != k.shape[0] or q.shape[1] != k.shape[1] or v.shape[0] != q.shape[0] or v.shape[1] != k.shape[2]:
+        raise RuntimeError("expected q (P, D, M), k (P, D, N), v (P, N, C)")
+    if not (q.device == k.device == v.device):
+        raise RuntimeError("q, k and v must be on the same device")
+
+
+def _n_pad(n_pad, P, device):
+    if n_pad is None or (isinstance(n_pad, (int, float)) and n_pad == 0):
+        return None
+    t = torch.as_tensor(n_pad, dtype=torch.float32, device=device)
+    if t.numel() == 1:
+        t = t.reshape(1).expand(P)
+    return t.reshape(P).contiguous()
+
+
+def layer_forward(kernel, q, k, v, n_pad=0):
+    """One fused forward of `kernel` in ("add_laplace", "add_riesz", "add_bump"); returns (P, M, C). No autograd."""
+    if kernel not in KINDS:
+        raise ValueError(f"unknown additive kernel {kernel!r}")
+    _check(q, k, v)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    P, D, M = q.shape
+    N, C = k.shape[2], v.shape[2]
+    npad = _n_pad(n_pad, P, q.device)
+    out = torch.empty(P, M, C, dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    kind = KINDS[kernel]
+    with torch.cuda.device(q.device):
+        nbytes = lib.qlka_layer_fwd_ws_bytes(kind, P, D, N, M, C)
+        ws = _lib.workspace(nbytes, q.device)
+        _lib.check(lib.qlka_layer_fwd(kind, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(npad), _lib.ptr(out),
+                                      P, D, N, M, C, _lib.ptr(ws), nbytes, _lib.stream_of(q.device)))
+    return out
+
+
+def _needs_grad(*ts):
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
+def add_laplace(q, k, v, n_pad=0):
+    """attention.py:67-72: weighted_laplace_sum normalised by its row sum (padded keys removed). Forward only."""
+    if _needs_grad(q, k, v):
+        raise RuntimeError("add_laplace: weighted_laplace_sum has no backward (forward-only operator)")
+    return layer_forward("add_laplace", q, k, v, n_pad)
+
+
+def unfused(kernel, q, k, v, n_pad=0):
+    """The reference's own composition (attention.py:67-92): separate op calls and a torch epilogue. Differentiable
+    for add_riesz / add_bump through weighted_abs_sum_full's autograd."""
+    from weighted_abs_sum import weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+    if kernel == "add_laplace":
+        out_w, out_u = weighted_laplace_sum(q.contiguous(), k.contiguous(), v.contiguous())
+        den = out_u - n_pad * (-q.abs()).exp().sum(dim=1)
+        return out_w / den.clamp_min(CLAMP)[:, :, None]
+    if kernel == "add_riesz":
+        out_w, out_u = weighted_abs_sum_full(q.contiguous(), k.contiguous(), v.contiguous())
+        aq, ak, S = q.abs().sum(dim=1), k.abs().sum(dim=1), q.shape[2]
+        num = (aq + EPS)[:, :, None] * v.sum(dim=1)[:, None, :] + (ak[:, :, None] * v).sum(dim=1)[:, None, :] - out_w
+        den = (aq + EPS) * S + ak.sum(dim=1, keepdim=True) - out_u - EPS * n_pad
+        return num / den.clamp_min(CLAMP)[:, :, None]
+    if kernel == "add_bump":
+        w0, u0 = weighted_abs_sum_full(q.contiguous(), k.contiguous(), v.contiguous())
+        wp, up = weighted_abs_sum_full((q + 1).contiguous(), k.contiguous(), v.contiguous())
+        wm, um = weighted_abs_sum_full((q - 1).contiguous(), k.contiguous(), v.contiguous())
+        num = (wp + wm) / 2 - w0
+        den = (up + um) / 2 - u0 - n_pad * (1 - q.abs()).clamp_min(0).sum(dim=1)
+        return num / den.clamp_min(CLAMP)[:, :, None]
+    raise ValueError(f"unknown additive kernel {kernel!r}")
+
+
+def add_riesz(q, k, v, n_pad=0):
+    """attention.py:75-81: A = |q|_1 + |k|_1 - |q - k|_1 + eps through one weighted_abs_sum_full."""
+    if _needs_grad(q, k, v):
+        return unfused("add_riesz", q, k, v, n_pad)
+    return layer_forward("add_riesz", q, k, v, n_pad)
+
+
+def add_bump(q, k, v, n_pad=0):
+    """attention.py:84-92: max(0, 1 - |x|) = |x + 1| / 2 + |x - 1| / 2 - |x| through three abs sums."""
+    if _needs_grad(q, k, v):
+        return unfused("add_bump", q, k, v, n_pad)
+    return layer_forward("add_bump", q, k, v, n_pad)
+
+
+LAYERS = {"add_laplace": add_laplace, "add_riesz": add_riesz, "add_bump": add_bump}
+
+
+def attention(q, k, v, kernel, tau, keep=None):
+    """The additive-kernel branch of attention() (attention.py:95-126): q, k, v (B, H, S, D) fp32 -> (B, H, S, D).
+
+    keep (B, S) marks the real keys (bool or 0/1); masked keys become k = 0, v = 0 and are removed from the row sums.
+    """
+    if kernel not in LAYERS:
+        raise ValueError(f"attention: kernel {kernel!r} is not one of {sorted(LAYERS)}")
+    assert q.dtype == k.dtype == v.dtype == torch.float32, "kernel attention runs in fp32 only"
+    B, H, S, D = q.shape
+    P = B * H
+    q = q.transpose(2, 3).reshape(P, D, S)
+    k = k.transpose(2, 3).reshape(P, D, S)
+    v = v.reshape(P, S, D)
+    keep = None if keep is None else keep.repeat_interleave(H, dim=0)       # (P, S)
+    q, k, n_pad = q / tau, k / tau, 0
+    if keep is not None:
+        k, v = k * keep[:, None, :], v * keep[:, :, None]
+        n_pad = S - keep.sum(dim=1, keepdim=True)
+    out = LAYERS[kernel](q, k, v, n_pad)
+    return out.view(B, H, S, D)

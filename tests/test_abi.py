@@ -81,3 +81,24 @@ def test_path_and_workspace_errors(lib):
     assert rc == 2 and "workspace too small" in lib.qlka_last_error().decode()
     rc = lib.qlka_laplace_fwd(None, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
     assert rc == 1 and "non-null" in lib.qlka_last_error().decode()
+
+
+def test_layer_workspace_and_validation(lib):
+    dims = (12, 64, 16384, 16384, 64)
+    op = lib.qlka_abs_fwd_ws_bytes(*dims)
+    lap, riesz, bump = (lib.qlka_layer_fwd_ws_bytes(kind, *dims) for kind in (0, 1, 2))
+    one_eval = 12 * 16384 * 64 * 4 + 12 * 16384 * 4          # out_w + out_u of one op evaluation
+    assert lap >= lib.qlka_laplace_fwd_ws_bytes(*dims) + one_eval
+    assert riesz >= op + one_eval
+    assert bump >= op + 3 * one_eval                          # three shifted evaluations, one shared slab
+    assert bump < 2 * op
+    assert lib.qlka_layer_fwd_ws_bytes(3, *dims) == 0
+    dummy = ctypes.c_void_p(16)     # never dereferenced: validation fails first
+    rc = lib.qlka_layer_fwd(3, dummy, dummy, dummy, None, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
+    assert rc == 1 and "kind must be" in lib.qlka_last_error().decode()
+    rc = lib.qlka_layer_fwd(2, dummy, dummy, dummy, None, dummy, 1, 1, 8, 8, 129, dummy, 1 << 40, None)
+    assert rc == 1 and "C (v.size(2)) must be in [1, 128]" in lib.qlka_last_error().decode()
+    rc = lib.qlka_layer_fwd(0, dummy, dummy, dummy, None, dummy, 1, 1, 8, 8, 4, dummy, 16, None)
+    assert rc == 2 and "workspace too small" in lib.qlka_last_error().decode()
+    rc = lib.qlka_layer_fwd(1, dummy, dummy, dummy, None, None, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
+    assert rc == 1 and "non-null" in lib.qlka_last_error().decode()

@@ -137,3 +137,26 @@ def test_config4_stress_global_sort_heavy_ties(dev):
     _rel(_sub(_np(gq), qidx, 1), wq, nq, "cfg4 grad_q")
     _rel(_sub(_np(gk), kidx, 1), wk, nk, "cfg4 grad_k")
     _rel(_sub(_np(gv), kidx, 0), wv, nv, "cfg4 grad_v")
+
+
+def test_config3_fused_layers(dev):
+    """The fused layers (one library call each, add_bump's three abs sums sharing one sort) at the headline shape,
+    against the normalised float64 kernel matrix on a query subsample."""
+    from qlka import layers
+    d = inputs.config(3)
+    q, k, v = d["q"], d["k"], d["v"]
+    idx = inputs.query_subsample(q.shape[0], q.shape[2], per_p=8)
+    B, H, S, Dh = 1, 12, 16384, 64
+    qa = torch.from_numpy(q).reshape(B, H, Dh, S).transpose(2, 3).contiguous()
+    ka = torch.from_numpy(k).reshape(B, H, Dh, S).transpose(2, 3).contiguous()
+    va = torch.from_numpy(v).reshape(B, H, S, Dh).contiguous()
+    q64, k64, v64 = (torch.from_numpy(a).double() for a in (q, k, v))
+    for kernel in ("add_laplace", "add_riesz", "add_bump"):
+        tau = dense.TAU[kernel]
+        with torch.no_grad():
+            out = _np(layers.attention(qa.to(dev), ka.to(dev), va.to(dev), kernel, tau)).reshape(B * H, S, Dh)
+        for p in range(0, B * H, 4):
+            A = dense.dense_kernel_matrix(kernel, q64[p:p + 1][:, :, idx[p]], k64[p:p + 1], tau)
+            ref = (A @ v64[p:p + 1]) / A.sum(dim=2, keepdim=True).clamp_min(dense.CLAMP)
+            np.testing.assert_allclose(out[p][idx[p]], ref[0].numpy(), rtol=2e-4, atol=2e-5,
+                                       err_msg=f"fused {kernel} layer, p={p}")

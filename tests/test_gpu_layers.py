@@ -1,0 +1,128 @@
+"""GPU parity of the fused attention layers (qlka.layers, qlka_layer_fwd) for add_laplace, add_riesz and add_bump.
+
+* Against the same ops with the reference's torch epilogue (oracle/dense.py's add_*_layer, attention.py:67-92): the
+  fused call must reproduce them to fp32 rounding of the epilogue.
+* Against the float64 normalised kernel matrix (kernels.py:68-89 restated in oracle/dense.py), with and without a
+  key mask (attention.py:119-124), at sizes where the matrix is cheap.
+* The gradient path of add_riesz / add_bump (the reference's formulas over the differentiable op) and the
+  forward-only add_laplace.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import dense
+
+pytestmark = pytest.mark.gpu
+
+KERNELS = ("add_laplace", "add_riesz", "add_bump")
+SHAPES = [  # P, D, N, M, C
+    (2, 3, 40, 40, 8),
+    (3, 5, 257, 190, 5),        # M != N, odd C
+    (2, 4, 1000, 1000, 64),
+    (1, 2, 300, 300, 128),      # two channel slots per lane
+]
+
+
+def _inputs(P, D, N, M, C, seed, dev, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(P, D, M, generator=g) * scale).to(dev)
+    k = (torch.randn(P, D, N, generator=g) * scale).to(dev)
+    v = torch.randn(P, N, C, generator=g).to(dev)
+    return q, k, v
+
+
+def _ops():
+    from weighted_abs_sum import weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+    return weighted_abs_sum_full, weighted_laplace_sum
+
+
+def _op_layer(kernel, q, k, v, n_pad):
+    abs_full, lap = _ops()
+    if kernel == "add_laplace":
+        return dense.add_laplace_layer(q, k, v, n_pad, lap)
+    if kernel == "add_riesz":
+        return dense.add_riesz_layer(q, k, v, n_pad, abs_full)
+    return dense.add_bump_layer(q, k, v, n_pad, abs_full)
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+@pytest.mark.parametrize("shape", SHAPES)
+def test_fused_layer_matches_op_layer(dev, kernel, shape):
+    from qlka import layers
+    P, D, N, M, C = shape
+    q, k, v = _inputs(P, D, N, M, C, seed=sum(shape), dev=dev, scale=0.7)
+    for n_pad in (0, torch.arange(P, device=dev, dtype=torch.float32).reshape(P, 1) * 0.25):
+        got = layers.layer_forward(kernel, q, k, v, n_pad)
+        want = _op_layer(kernel, q, k, v, n_pad)
+        assert got.shape == (P, M, C)
+        np.testing.assert_allclose(got.cpu().numpy(), want.cpu().numpy(), rtol=2e-5, atol=2e-6,
+                                   err_msg=f"{kernel} {shape} n_pad={n_pad if isinstance(n_pad, int) else 'per-p'}")
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+@pytest.mark.parametrize("masked", [False, True])
+def test_attention_vs_float64_kernel_matrix(dev, kernel, masked):
+    from qlka import layers
+    B, H, S, Dh = 2, 3, 200, 16
+    g = torch.Generator().manual_seed(11)
+    qa, ka, va = (torch.randn(B, H, S, Dh, generator=g) for _ in range(3))
+    keep = None
+    if masked:
+        keep = torch.ones(B, S, dtype=torch.bool)
+        keep[0, 150:] = False
+        keep[1, 37:60] = False
+    tau = dense.TAU[kernel]
+    out = layers.attention(qa.to(dev), ka.to(dev), va.to(dev), kernel, tau,
+                           None if keep is None else keep.to(dev)).cpu()
+    q64 = qa.double().transpose(2, 3).reshape(B * H, Dh, S)
+    k64 = ka.double().transpose(2, 3).reshape(B * H, Dh, S)
+    v64 = va.double().reshape(B * H, S, Dh)
+    mask = None if keep is None else keep.repeat_interleave(H, dim=0).double()
+    A = dense.dense_kernel_matrix(kernel, q64, k64, tau, mask)
+    ref = (A @ v64) / A.sum(dim=2, keepdim=True).clamp_min(dense.CLAMP)
+    np.testing.assert_allclose(out.reshape(B * H, S, Dh).numpy(), ref.numpy(), rtol=2e-4, atol=2e-5,
+                               err_msg=f"{kernel} masked={masked}")
+
+
+@pytest.mark.parametrize("kernel", ("add_riesz", "add_bump"))
+def test_layer_gradient_path(dev, kernel):
+    from qlka import layers
+    P, D, N, M, C = 2, 3, 60, 60, 4
+    q, k, v = _inputs(P, D, N, M, C, seed=5, dev=dev, scale=0.8)
+    fused = layers.LAYERS[kernel](q, k, v, 0)
+    qg, kg, vg = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = layers.LAYERS[kernel](qg, kg, vg, 0)
+    np.testing.assert_allclose(out.detach().cpu().numpy(), fused.cpu().numpy(), rtol=2e-5, atol=2e-6)
+    wgt = torch.randn(out.shape, generator=torch.Generator().manual_seed(9)).to(dev)
+    (out * wgt).sum().backward()
+    # float64 reference through autograd of the dense layer
+    q64, k64, v64 = (t.detach().cpu().double().requires_grad_(True) for t in (q, k, v))
+    A = dense.dense_kernel_matrix(kernel, q64, k64)
+    ref = (A @ v64) / A.sum(dim=2, keepdim=True).clamp_min(dense.CLAMP)
+    (ref * wgt.cpu().double()).sum().backward()
+    for name, got, want in (("q", qg.grad, q64.grad), ("k", kg.grad, k64.grad), ("v", vg.grad, v64.grad)):
+        scale = want.abs().max().item()
+        np.testing.assert_allclose(got.cpu().numpy(), want.numpy(), rtol=1e-3, atol=1e-4 * scale,
+                                   err_msg=f"{kernel} grad_{name}")
+
+
+def test_add_laplace_is_forward_only(dev):
+    from qlka import layers
+    q, k, v = _inputs(1, 2, 16, 16, 4, seed=1, dev=dev)
+    with pytest.raises(RuntimeError, match="no backward"):
+        layers.add_laplace(q.requires_grad_(True), k, v)
+    with torch.no_grad():
+        assert layers.add_laplace(q, k, v).shape == (1, 16, 4)
+
+
+def test_layer_validation(dev):
+    from qlka import layers
+    q, k, v = _inputs(1, 2, 16, 16, 4, seed=1, dev=dev)
+    with pytest.raises(ValueError):
+        layers.layer_forward("softmax", q, k, v)
+    with pytest.raises(RuntimeError, match="float32"):
+        layers.layer_forward("add_riesz", q.double(), k, v)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        layers.layer_forward("add_riesz", q.cpu(), k, v)
