@@ -34,6 +34,7 @@ int qlka_version(void);
 /*
  * weighted_laplace_sum forward.
  *   out_w[p,m,c] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|) v[p,n,c],  out_u[p,m] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|)
+ * max(N, M) <= 256 runs the dense evaluation of qlka_direct_fwd (the workspace is then unused).
  * Replaces _ext.weighted_laplace_sum_forward (Weighted_Laplace_Sum/csrc/binding.cpp:63-100).
  */
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C);
@@ -43,7 +44,8 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
 /*
  * weighted_abs_sum forward; out_u == NULL gives the plain op, out_u != NULL the _full op.
  *   out_w[p,m,c] = sum_{d,n} |k[p,d,n] - q[p,d,m]| v[p,n,c],  out_u[p,m] = sum_{d,n} |k[p,d,n] - q[p,d,m]|
- * path: -1 auto, 0 global, 1 fused (the fused path exists for max(N, M) <= 4096 only, as in the reference).
+ * path: -1 auto, 0 global, 1 fused (the fused path exists for max(N, M) <= 4096 only, as in the reference). Under
+ * auto, max(N, M) <= 256 runs the dense evaluation of qlka_direct_fwd (the workspace is then unused).
  * Replaces _ext.weighted_abs_sum_forward / weighted_abs_sum_full_forward (Weighted_Abs_Sum/csrc/binding.cpp:229-239).
  */
 size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C);
@@ -68,6 +70,18 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
 size_t qlka_sgn_fwd_ws_bytes(int P, int D, int N, int M, int C);
 int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g, float* out,
                  int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Dense evaluation for short segments: A[m,n] = sum_d f(q[p,d,m] - k[p,d,n]) with f = |x| (kind 0, the weighted abs
+ * sum) or exp(-|x|) (kind 1, the weighted Laplace sum), out_w[p,m,:] = sum_n A[m,n] v[p,n,:], out_u[p,m] = sum_n
+ * A[m,n] (out_u may be NULL). Same values as qlka_abs_fwd / qlka_laplace_fwd; no sort and no workspace, O(N M D)
+ * work, so it is the faster route only for short segments (the ops pick it by size). The role of the reference's
+ * KeOps backend below KEOPS_CUTOFF (Weighted_Abs_Sum/weighted_abs_sum/keops_backend.py:19-35).
+ */
+#define QLKA_DIRECT_ABS     0
+#define QLKA_DIRECT_LAPLACE 1
+int qlka_direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                    int P, int D, int N, int M, int C, void* stream);
 
 /*
  * Fused additive-kernel attention layer, forward: the op(s) plus the normalising epilogue in one call.

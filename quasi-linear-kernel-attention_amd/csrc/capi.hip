@@ -32,6 +32,11 @@ int hip_status(int e, const char* where) {
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+// Up to this max(N, M) the dense evaluation (direct.hip) beats sort + scans + walk + reduce, whose cost there is
+// launch and per-segment overhead (measured on MI355X: 4-5x at N = 65, 2-2.6x at N = 256, break-even near 600).
+constexpr int DIRECT_MAX = 256;
+inline bool use_direct(int N, int M) { return std::max(N, M) <= DIRECT_MAX; }
+
 // Same limits and wording as check_qkv (Weighted_Abs_Sum/csrc/binding.cpp:79-83).
 int check_dims(int P, int D, int N, int M, int C) {
     if (P <= 0) return fail(QLKA_EINVAL, "P must be > 0");
@@ -130,6 +135,8 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     const WsSpec spec = laplace_spec(P, D, N, M, C);
     if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
+    if (use_direct(N, M))
+        return hip_status(direct_fwd(1, q, k, v, out_w, out_u, P, D, N, M, C, st), "laplace direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
@@ -161,6 +168,8 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
     const WsSpec spec = abs_fwd_spec(P, D, N, M, C, true);
     if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
+    if (path == -1 && use_direct(N, M))
+        return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
@@ -242,6 +251,16 @@ int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g,
     a.out_dot = out; a.sign = -1.f; a.P = P; a.D = D; a.C = C;
     int e = abs_walk(a, ABS_DOT, w.ra, st);
     return hip_status(e, "sgn walk");
+}
+
+// -------------------------------------------------------------------------------------------- direct evaluation
+int qlka_direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                    int P, int D, int N, int M, int C, void* stream) {
+    g_err.clear();
+    if (kind < 0 || kind > 1) return fail(QLKA_EINVAL, "kind must be 0 (abs) or 1 (laplace)");
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !out_w) return fail(QLKA_EINVAL, "q, k, v and out_w must be non-null");
+    return hip_status(direct_fwd(kind, q, k, v, out_w, out_u, P, D, N, M, C, (hipStream_t)stream), "direct sum");
 }
 
 // ------------------------------------------------------------------------------------------- fused attention layers

@@ -103,6 +103,10 @@ int abs_emit(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
 int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st);
 int range_count(int Ns, int C);          // key ranges per segment
 
+// Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null
+int direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
+               int P, int D, int N, int M, int C, hipStream_t st);
+
 // Fused attention-layer epilogues (layers.hip)
 enum LayerKind { LAYER_ADD_LAPLACE = 0, LAYER_ADD_RIESZ = 1, LAYER_ADD_BUMP = 2 };
 size_t riesz_prefix_bytes(int P, int N, int C);

@@ -28,6 +28,7 @@ _SIGNATURES = {
     "qlka_abs_bwd": (_c_int, [_c_ptr] * 8 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_sgn_fwd_ws_bytes": (_c_size, [_c_int] * 5),
     "qlka_sgn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
+    "qlka_direct_fwd": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr]),
     "qlka_layer_fwd_ws_bytes": (_c_size, [_c_int] * 6),
     "qlka_layer_fwd": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_seg_sort_ws_bytes": (_c_size, [_c_int] * 2),

@@ -82,6 +82,21 @@ def weighted_abs_sum_full_forward(q, k, v, path=-1):
     return _forward(q, k, v, path, full=True)
 
 
+def weighted_abs_sum_direct_forward(q, k, v, full):
+    """Dense evaluation (qlka_direct_fwd): the same (out_w, out_u) without a sort, for the "keops" route (the
+    reference's KeOps backend, Weighted_Abs_Sum/weighted_abs_sum/keops_backend.py:19-35). Not in the reference's
+    pybind module; out_u is None unless full."""
+    P, D, N, M, C = _check_qkv(q, k, v)
+    lib = _lib.load()
+    dev = q.device
+    with torch.cuda.device(dev):
+        out = torch.empty((P, M, C), dtype=q.dtype, device=dev)
+        out_u = torch.empty((P, M), dtype=q.dtype, device=dev) if full else None
+        _lib.check(lib.qlka_direct_fwd(0, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(out_u),
+                                       P, D, N, M, C, _lib.stream_of(dev)))
+    return out, out_u
+
+
 def _backward(q, k, v, g_w, g_u):
     P, D, N, M, C = _check_qkv(q, k, v)
     _check_grad("g_w", g_w, q, (P, M, C))

@@ -5,9 +5,12 @@ runs the native gfx950 kernels of libqlka.so:
 
 * "cuda" / "cuda-global" -> path -1 / 0, "cuda-fused" -> path 1 (which, as in the reference, raises for
   max(N, M) > 4096).
-* "keops" (passed by Experiments/kernel_attention/attention.py:63 for S < 256) has no pykeops behind it on ROCm; it runs
-  the same native walk. The only semantic difference from pykeops is the sign of an exact tie in weighted_sgn_sum
-  (pykeops: sign(0) = 0, keops_backend.py:40-41; the walk: a tie counts as +1 there, as the reference's CUDA path).
+* "keops" (passed by Experiments/kernel_attention/attention.py:63 for S < 256) has no pykeops behind it on ROCm. Its
+  forward runs the native dense evaluation (qlka_direct_fwd: A = sum_d |q_d - k_d| reduced against [v, 1], the
+  computation keops_backend.py:19-35 describes), on contiguous copies as KeOps makes them; its backward and
+  weighted_sgn_sum run the native walk. The only semantic difference from pykeops is the sign of an exact tie in
+  those gradients and in weighted_sgn_sum (pykeops: sign(0) = 0, keops_backend.py:40-41; the walk: the reference's
+  CUDA convention).
 * "auto" behaves as in the reference: "keops" strictly below KEOPS_CUTOFF, else "cuda".
 """
 
@@ -16,7 +19,8 @@ import torch
 from weighted_abs_sum import _ext as _C
 
 _BACKENDS = ("auto", "keops", "cuda", "cuda-fused", "cuda-global")
-_PATH = {"cuda": -1, "cuda-fused": 1, "cuda-global": 0, "keops": -1}
+_DIRECT = "direct"      # forward of the keops route: dense evaluation
+_PATH = {"cuda": -1, "cuda-fused": 1, "cuda-global": 0, "keops": _DIRECT}
 
 # "auto" uses the keops route strictly below this max(N,M)
 KEOPS_CUTOFF = 512
@@ -44,8 +48,12 @@ def _resolve(backend, q, k, v):
 class _WeightedAbsSum(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, path):
+        if path == _DIRECT:
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         ctx.save_for_backward(q, k, v)
         ctx.set_materialize_grads(False)
+        if path == _DIRECT:
+            return _C.weighted_abs_sum_direct_forward(q, k, v, full=False)[0]
         return _C.weighted_abs_sum_forward(q, k, v, path)
 
     @staticmethod
@@ -58,8 +66,12 @@ class _WeightedAbsSum(torch.autograd.Function):
 class _WeightedAbsSumFull(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, path):
+        if path == _DIRECT:
+            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         ctx.save_for_backward(q, k, v)
         ctx.set_materialize_grads(False)
+        if path == _DIRECT:
+            return _C.weighted_abs_sum_direct_forward(q, k, v, full=True)
         return _C.weighted_abs_sum_full_forward(q, k, v, path)
 
     @staticmethod

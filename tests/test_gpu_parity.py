@@ -300,3 +300,64 @@ def test_workspace_contents_do_not_matter(dev, shape, fill):
     _assert_rel(_np(gq), wq, nq, "grad_q (poisoned ws)")
     _assert_rel(_np(gk), wk, nk, "grad_k (poisoned ws)")
     _assert_rel(_np(gv), wv, nv, "grad_v (poisoned ws)")
+
+
+# ------------------------------------------------------------------------------------------ dense (direct) route
+DIRECT_SHAPES = [  # P, D, N, M, C: tiles of 64 queries / keys and 32 features, partial tiles on every axis
+    (1, 1, 1, 1, 1),
+    (3, 5, 65, 63, 33),
+    (2, 33, 130, 200, 64),
+    (2, 70, 64, 64, 65),
+    (1, 2, 257, 300, 128),
+    (4, 32, 65, 65, 32),      # the ViT segment shape of BASELINE configs[1]
+    (2, 4, 1500, 900, 16),    # long segments: the dense route is valid at any size
+]
+
+
+@pytest.mark.parametrize("shape", DIRECT_SHAPES)
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_direct_forward(dev, shape, kind):
+    from qlka import _lib
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 9, kind=kind)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    lib = _lib.load()
+    for op, oracle in ((0, brute.abs_sum), (1, brute.laplace_sum)):
+        ow, ou, nw = oracle(q, k, v)
+        for with_u in (True, False):
+            w = torch.empty(P, M, C, device=dev)
+            u = torch.empty(P, M, device=dev) if with_u else None
+            _lib.check(lib.qlka_direct_fwd(op, _lib.ptr(tq), _lib.ptr(tk), _lib.ptr(tv), _lib.ptr(w), _lib.ptr(u),
+                                           P, D, N, M, C, _lib.stream_of(dev)))
+            _assert_rel(_np(w), ow, nw, f"direct kind {op} out_w")
+            if with_u:
+                _assert_rel(_np(u), ou, ou, f"direct kind {op} out_u")
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_keops_route_forward_and_autograd(dev, full):
+    # "keops": dense forward on contiguous copies, gradients from the walk backward
+    from weighted_abs_sum import weighted_abs_sum, weighted_abs_sum_full
+    P, D, N, M, C = 3, 6, 120, 100, 12
+    q, k, v = _data(P, D, N, M, C, seed=31)
+    rng = np.random.default_rng(6)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    # non-contiguous views, as a KeOps caller may pass them
+    tq = _t(np.ascontiguousarray(q.transpose(0, 2, 1)), dev).transpose(1, 2).requires_grad_(True)
+    tk, tv = (_t(a, dev).requires_grad_(True) for a in (k, v))
+    if full:
+        w, u = weighted_abs_sum_full(tq, tk, tv, backend="keops")
+        loss = (w * _t(g_w, dev)).sum() + (u * _t(g_u, dev)).sum()
+    else:
+        w = weighted_abs_sum(tq, tk, tv, backend="keops")
+        loss = (w * _t(g_w, dev)).sum()
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, "keops route out_w")
+    if full:
+        _assert_rel(_np(u), ou, ou, "keops route out_u")
+    loss.backward()
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u if full else None)
+    _assert_rel(_np(tq.grad), wq, nq, "keops route grad_q")
+    _assert_rel(_np(tk.grad), wk, nk, "keops route grad_k")
+    _assert_rel(_np(tv.grad), wv, nv, "keops route grad_v")
