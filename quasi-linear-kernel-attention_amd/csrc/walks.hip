@@ -559,64 +559,44 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     const int S, const int D, const int Ns, const int Mq, const int C, const int G,
                     const float qshift)
 {
-    __shared__ f4_t wts[WPB][2][RK / 4];                  // per-key weights, read four at a time as broadcasts
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
     const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
-    const int p = s / D, l = lane_id(), wi = wave_in_block();
+    const int p = s / D, l = lane_id();
     const int base = g * RK, nk = min(RK, Ns - base);
     const float* kseg = ks + (size_t)s * Ns;
-    const uint32_t* kpseg = kp + (size_t)s * Ns;
-    const float* qseg = qs + (size_t)s * Mq;
-    const float klast = kseg[base + nk - 1];
-
-    // query boundary of the range (#queries <= klast): the first probe round is in flight during the row gathers
-    UpperBoundProbe ubp;
-    ubp.probe(qseg, Mq);
 
     const int li = base + min(l, nk - 1);
     const float kl = kseg[li];
+    const uint32_t pl = kp[(size_t)s * Ns + li];
+    const float klast = kseg[base + nk - 1];
     const bool real = l < nk;
+    const float kw = real ? 1.f : 0.f;                   // pad keys weigh 0
     const float dl = real ? (klast - kl) : 0.f;
-    float* wf = reinterpret_cast<float*>(wts[wi]);
-    if (l < RK) {
-        wf[l] = real ? 1.f : 0.f;                         // pad keys weigh 0
-        wf[RK + l] = dl;
-    }
 
     float sw[NV], sb[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) { sw[j] = 0.f; sb[j] = 0.f; }
     if constexpr (WANT_W) {
-        // all RK row gathers in flight first (row indices by scalar loads), then the weighted sums
         const rsrc_t wr_ = make_rsrc(w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
-        float x[RK][NV];
-        auto gather = [&](auto row_of) {
 #pragma unroll
-            for (int t = 0; t < RK; ++t) {
-                const int rowoff = (int)(row_of(t) * C * 4);
+        for (int t = 0; t < RK; ++t) {
+            const uint32_t row = bcast(pl, t);
+            const float a = bcast(kw, t), b = bcast(dl, t);
 #pragma unroll
-                for (int j = 0; j < NV; ++j) x[t][j] = buf_load(wr_, min(l + WAVE * j, C - 1) * 4, rowoff);
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                const float xr = buf_load(wr_, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
+                const float x = (c < C) ? xr : 0.f;
+                sw[j] += a * x;
+                sb[j] += b * x;
             }
-        };
-        if (nk == RK) gather([&](int t) { return kpseg[base + t]; });
-        else          gather([&](int t) { return kpseg[base + min(t, nk - 1)]; });
-#pragma unroll
-        for (int t4 = 0; t4 < RK / 4; ++t4) {
-            const f4_t k4 = wts[wi][0][t4], d4 = wts[wi][1][t4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < NV; ++j) {            // lanes >= C are never stored
-                    sw[j] += k4[i] * x[4 * t4 + i][j];
-                    sb[j] += d4[i] * x[4 * t4 + i][j];
-                }
         }
     }
     const float b1 = wave_sum(dl);
     float u1 = 0.f;
     if constexpr (WANT_U) {
-        const float ur = u[(size_t)p * Ns + kpseg[li]];
+        const float ur = u[(size_t)p * Ns + pl];
         u1 = wave_sum(real ? ur : 0.f);
     }
 
@@ -634,7 +614,8 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
         ra[C + 1] = (g > 0) ? (klast - kseg[base - 1]) : 0.f;   // slot C+1: the scan's key gap into this range
     }
 
-    const int ub = ubp.finish(qseg, Mq, klast, qshift);
+    const float* qseg = qs + (size_t)s * Mq;
+    const int ub = wave_upper_bound_from(qseg, 0, Mq, klast, qshift);
     if (l == 0) qb[(size_t)s * G + g] = ub;
 }
 
