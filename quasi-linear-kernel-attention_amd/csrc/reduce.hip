@@ -35,14 +35,18 @@ void u_gather(const float* __restrict__ uslab, const uint32_t* __restrict__ qinv
 }
 
 // One thread per (p, m, 4 channels) (V4, C % 4 == 0) or per (p, m, channel); features summed in order d = 0..D-1.
-template <bool V4>
+// With WITH_U (V4 and C / 4 a power of two, so the C / 4 lanes of one query row are aligned within a wave) the row's
+// lanes also produce out_u: lane j sums features d = j, j + C/4, ... of the v == 1 contributions through the inverse
+// permutation and the partial sums are combined with lane shuffles (fixed order, deterministic).
+template <bool V4, bool WITH_U>
 __global__ __launch_bounds__(RT)
 void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const int P, const int D, const int M,
-                 const int C, const int CR)
+                 const int C, const int CR, const float* __restrict__ uslab, const uint32_t* __restrict__ qinv,
+                 float* __restrict__ out_u)
 {
     const int CQ = V4 ? C / 4 : C;
     const long i = (long)blockIdx.x * RT + threadIdx.x;
-    if (i >= (long)P * M * CQ) return;
+    if (i >= (long)P * M * CQ) return;                 // WITH_U: P*M*CQ is a multiple of CQ, so whole rows return
     const int c = (int)(i % CQ);
     const long pm = i / CQ;
     const int p = (int)(pm / M);
@@ -57,6 +61,16 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
 #pragma unroll 8
         for (int d = 0; d < D; ++d) a += __builtin_nontemporal_load(s4 + (size_t)d * d4);   // streamed once
         reinterpret_cast<f4*>(out + pm * C)[c] = a;
+        if constexpr (WITH_U) {
+            const size_t base = (size_t)p * D * M;
+            float u = 0.f;
+            for (int d = c; d < D; d += CQ) {
+                const size_t so = base + (size_t)d * M;
+                u += uslab[so + qinv[so + m]];
+            }
+            for (int off = CQ >> 1; off >= 1; off >>= 1) u += __shfl_xor(u, off, WAVE);
+            if (c == 0) out_u[pm] = u;
+        }
     } else {
         float a = 0.f;
 #pragma unroll 8
@@ -67,20 +81,27 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
 
 int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qinv, float* out, float* out_u,
                  int P, int D, int M, int C, hipStream_t st) {
-    if (out_u) {
+    const int CR = slab_stride(C);
+    const bool v4 = (C % 4) == 0;
+    const int cq = C / 4;
+    const bool fused_u = out_u && v4 && (cq & (cq - 1)) == 0;     // row lanes aligned within a wave
+    if (out_u && !fused_u) {
         StageTimer t("u_gather", st);
         const long n = (long)P * M;
         hipLaunchKernelGGL(u_gather, dim3((unsigned)((n + RT - 1) / RT)), dim3(RT), 0, st, uslab, qinv, out_u, P, D, M);
     }
-    const int CR = slab_stride(C);
-    const bool v4 = (C % 4) == 0;
     const long threads = (long)P * M * (v4 ? C / 4 : C);
     const unsigned blocks = (unsigned)((threads + RT - 1) / RT);
     StageTimer t("slab_reduce", st);
-    if (v4)
-        hipLaunchKernelGGL(slab_reduce<true>, dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR);
+    if (fused_u)
+        hipLaunchKernelGGL((slab_reduce<true, true>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR, uslab,
+                           qinv, out_u);
+    else if (v4)
+        hipLaunchKernelGGL((slab_reduce<true, false>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR,
+                           nullptr, nullptr, nullptr);
     else
-        hipLaunchKernelGGL(slab_reduce<false>, dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR);
+        hipLaunchKernelGGL((slab_reduce<false, false>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR,
+                           nullptr, nullptr, nullptr);
     return (int)hipGetLastError();
 }
 
