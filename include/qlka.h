@@ -84,6 +84,17 @@ int qlka_direct_fwd(int kind, const float* q, const float* k, const float* v, fl
                     int P, int D, int N, int M, int C, void* stream);
 
 /*
+ * Dense evaluation of the abs backward and of weighted_sgn_sum with an explicit value `tie` of sign(0): the
+ * formulas of qlka_abs_bwd / qlka_sgn_fwd with s(0) = tie (0: the KeOps convention of keops_backend.py:40-41 and of
+ * autograd through the KeOps forward; -1 for the gradients / +1 for the sgn sum: the walk's convention). g_u may be
+ * NULL. No workspace; O(N M (D + C)) work, for short segments.
+ */
+int qlka_direct_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                    float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, void* stream);
+int qlka_direct_sgn(float tie, const float* q, const float* k, const float* v, const float* g, float* out,
+                    int P, int D, int N, int M, int C, void* stream);
+
+/*
  * Fused additive-kernel attention layer, forward: the op(s) plus the normalising epilogue in one call.
  *   kind QLKA_ADD_LAPLACE: out = w / clamp(u - n_pad sum_d e^{-|q_d|}, 1e-6), (w, u) = weighted_laplace_sum(q, k, v)
  *   kind QLKA_ADD_RIESZ:   out = ((|q|_1 + 1e-3) sum_n v_n + sum_n |k_n|_1 v_n - w)

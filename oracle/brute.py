@@ -13,7 +13,7 @@ abs_sum                        ops.py:107-126, keops_backend.py:19-36           
 laplace_sum                    weighted_laplace_sum/__init__.py:4-13, laplace_kernels.cu:5-29   fp64 two-sided recurrence (pure Python),
                                                                                                single key, ties -> 1, underflow, v==1
 sgn_sum                        ops.py:129-139, binding.cpp:383-439 (tie +1), keops 40-41 (0)    hand-built ties, == -grad_q, autograd
-abs_backward                   binding.cpp:242-380, sgn_kernels.cu:8-15 (tie -1)                torch.autograd.gradcheck of a dense fp64
+abs_backward                   binding.cpp:242-380, sgn_kernels.cu:8-15 (tie -1; keops: 0)      torch.autograd.gradcheck of a dense fp64
                                                                                                forward (tie-free), grad_v == abs_sum(k, q, g_w)
 stable_sort / merge_rank       sort_utils.cu:85-87, walk_common.cuh:10-20                       pure-Python stable sort / brute-force counts
 """
@@ -94,10 +94,11 @@ def sgn_sum(q, k, v, g, tie=1.0, qidx=None):
     return out, norm
 
 
-def abs_backward(q, k, v, g_w, g_u=None):
-    """(grad_q, grad_k, grad_v) of weighted_abs_sum(_full) with the reference's tie convention: the derivative of
-    |k - q| w.r.t. q is s(q - k) and w.r.t. k is s(k - q), with s(x) = +1 for x > 0 and -1 otherwise
-    (sgn_kernels.cu:8-15, binding.cpp:242-245). Also returns the normalisers (nq, nk, nv)."""
+def abs_backward(q, k, v, g_w, g_u=None, tie=-1.0):
+    """(grad_q, grad_k, grad_v) of weighted_abs_sum(_full): the derivative of |k - q| w.r.t. q is s(q - k) and w.r.t.
+    k is s(k - q), with s(x) = sign(x) and s(0) = tie. tie = -1 is the reference CUDA extension's convention
+    (sgn_kernels.cu:8-15, binding.cpp:242-245), tie = 0 the gradient of the KeOps forward (keops_backend.py:40-41).
+    Also returns the normalisers (nq, nk, nv)."""
     q, k, v, g_w = _f64(q), _f64(k), _f64(v), _f64(g_w)
     g_u = None if g_u is None else _f64(g_u)
     P, D, M = q.shape
@@ -110,8 +111,8 @@ def abs_backward(q, k, v, g_w, g_u=None):
             Bm = Bm + g_u[p][:, None]
         for d in range(D):
             x = q[p, d][:, None] - k[p, d][None, :]        # (M, N) = q_m - k_n
-            sq = np.where(x > 0, 1.0, -1.0)                # s(q - k)
-            sk = np.where(-x > 0, 1.0, -1.0)               # s(k - q)
+            sq = np.where(x > 0, 1.0, np.where(x < 0, -1.0, tie))     # s(q - k)
+            sk = np.where(x < 0, 1.0, np.where(x > 0, -1.0, tie))     # s(k - q)
             gq[p, d] = (sq * Bm).sum(axis=1)
             gk[p, d] = (sk * Bm).sum(axis=0)
             nq[p, d] = np.abs(Bm).sum(axis=1)

@@ -263,6 +263,26 @@ int qlka_direct_fwd(int kind, const float* q, const float* k, const float* v, fl
     return hip_status(direct_fwd(kind, q, k, v, out_w, out_u, P, D, N, M, C, (hipStream_t)stream), "direct sum");
 }
 
+int qlka_direct_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                    float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
+        return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
+    return hip_status(direct_bwd(tie, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, (hipStream_t)stream),
+                      "direct backward");
+}
+
+int qlka_direct_sgn(float tie, const float* q, const float* k, const float* v, const float* g, float* out,
+                    int P, int D, int N, int M, int C, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !g || !out) return fail(QLKA_EINVAL, "q, k, v, g and out must be non-null");
+    // sum_n s(k - q) <v_n, g_m> with s(0) = tie  ==  -(sum_n s'(q - k) <g_m, v_n>) with s'(0) = -tie
+    return hip_status(direct_sign(true, q, k, g, v, nullptr, out, -tie, -1.f, P, D, M, N, C, (hipStream_t)stream),
+                      "direct sgn sum");
+}
+
 // ------------------------------------------------------------------------------------------- fused attention layers
 // Workspace: the op's (sorted k/q, ranges, slab) + per op evaluation a (P, M, C) + (P, M) pair of out_w / out_u
 // (three for add_bump) + the add_riesz prefixes + the query boundaries of add_bump's two shifted query sets.

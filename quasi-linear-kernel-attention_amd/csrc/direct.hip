@@ -137,4 +137,129 @@ int direct_fwd(int kind, const float* q, const float* k, const float* v, float* 
     return (int)hipGetLastError();
 }
 
+// Dense sign sums, the gradients of the dense abs sum (and weighted_sgn_sum):
+//
+//   out[d, i] = scale * sum_j s(a[d, i] - b[d, j]) * (<x[i, :], y[j, :]> + gu),   s(z) = sign(z), s(0) = tie
+//
+// with gu = g_u[i] (GU_OWN) or g_u[j] (otherwise), or 0 without g_u:
+//   grad_q:  a = q, b = k, x = g_w, y = v, gu = g_u[m]  (own)
+//   grad_k:  a = k, b = q, x = v, y = g_w, gu = g_u[m]  (other)
+//   weighted_sgn_sum (KeOps convention): grad_q with g for g_w, no g_u, tie 0, scale -1 (keops_backend.py:38-48).
+// tie = 0 is KeOps' sign(0) (keops_backend.py:40-41); tie = -1 is the reference CUDA walk's convention.
+// One workgroup per (p, tile of 64 outputs i) walks the j in tiles of 64: the 64 x 64 tile of <x_i, y_j> + gu is
+// formed 4 x 4 per thread from LDS rows into LDS, then lane i of wave w accumulates features d = w, w + 4, ... (16
+// per pass over 64 features) against b values read as LDS broadcasts.
+template <bool GU_OWN, int CT>
+__global__ __launch_bounds__(DTHREADS)
+void direct_sign_kernel(const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ x,
+                        const float* __restrict__ y, const float* __restrict__ gu, float* __restrict__ out,
+                        const float tie, const float scale, const int D, const int I, const int J, const int C,
+                        const int itiles)
+{
+    constexpr int CW = 16 * CT;
+    constexpr int DC = 64;                                // features per pass
+    __shared__ float xs[DT][CW];
+    __shared__ float ys[DT][CW];
+    __shared__ float bt[DT][DT + 1];                      // [i][j], stride 65: conflict-free column reads
+    __shared__ float bsm[DC][DT];                         // b[d0 + dd][j0 + j]
+
+    const int p = blockIdx.x / itiles, it = blockIdx.x - p * itiles;
+    const int i0 = it * DT, tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
+    const int lane = tid % DT, wv = tid / DT;             // sign-sum mapping: output i = i0 + lane, d = d0 + wv + 4 jj
+    const float* ap = a + (size_t)p * D * I;
+    const float* bp = b + (size_t)p * D * J;
+    const float* xp = x + (size_t)p * I * C;
+    const float* yp = y + (size_t)p * J * C;
+    const float* gp = gu ? gu + (size_t)p * (GU_OWN ? I : J) : nullptr;
+
+    for (int e = tid; e < DT * CW; e += DTHREADS) {
+        const int r = e / CW, c = e - r * CW, i = i0 + r;
+        xs[r][c] = (i < I && c < C) ? xp[(size_t)i * C + c] : 0.f;
+    }
+    for (int d0 = 0; d0 < D; d0 += DC) {
+        float av[16], acc[16];
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+            const int d = d0 + wv + 4 * jj, i = i0 + lane;
+            av[jj] = (d < D && i < I) ? ap[(size_t)d * I + i] : 0.f;
+            acc[jj] = 0.f;
+        }
+        for (int j0 = 0; j0 < J; j0 += DT) {
+            __syncthreads();                              // previous readers of ys / bsm / bt are done (and xs written)
+            for (int e = tid; e < DT * CW; e += DTHREADS) {
+                const int r = e / CW, c = e - r * CW, j = j0 + r;
+                ys[r][c] = (j < J && c < C) ? yp[(size_t)j * C + c] : 0.f;
+            }
+            for (int e = tid; e < DC * DT; e += DTHREADS) {
+                const int dd = e / DT, jl = e - dd * DT, d = d0 + dd, j = j0 + jl;
+                bsm[dd][jl] = (d < D && j < J) ? bp[(size_t)d * J + j] : 0.f;
+            }
+            __syncthreads();
+            float bb[4][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) bb[r][q] = 0.f;
+            for (int c = 0; c < C; ++c) {
+                float xv[4], yv[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) { xv[r] = xs[4 * ty + r][c]; yv[r] = ys[4 * tx + r][c]; }
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) bb[r][q] += xv[r] * yv[q];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int i = i0 + 4 * ty + r, j = j0 + 4 * tx + q;
+                    float g = 0.f;
+                    if (gp) g = GU_OWN ? (i < I ? gp[i] : 0.f) : (j < J ? gp[j] : 0.f);
+                    bt[4 * ty + r][4 * tx + q] = bb[r][q] + g;
+                }
+            __syncthreads();
+            const int nj = min(DT, J - j0);
+            for (int j = 0; j < nj; ++j) {
+                const float bv = bt[lane][j];
+#pragma unroll
+                for (int jj = 0; jj < 16; ++jj) {
+                    const float z = av[jj] - bsm[wv + 4 * jj][j];
+                    const float sg = z > 0.f ? 1.f : (z < 0.f ? -1.f : tie);
+                    acc[jj] += sg * bv;
+                }
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+            const int d = d0 + wv + 4 * jj, i = i0 + lane;
+            if (d < D && i < I) out[(size_t)p * D * I + (size_t)d * I + i] = scale * acc[jj];
+        }
+    }
+}
+
+int direct_sign(bool gu_own, const float* a, const float* b, const float* x, const float* y, const float* gu,
+                float* out, float tie, float scale, int P, int D, int I, int J, int C, hipStream_t st) {
+    const int itiles = (I + DT - 1) / DT;
+    const dim3 grid((unsigned)(P * itiles)), block(DTHREADS);
+    StageTimer t("direct_sign", st);
+#define QLKA_SIGN(OWN, CTV) \
+    hipLaunchKernelGGL((direct_sign_kernel<OWN, CTV>), grid, block, 0, st, a, b, x, y, gu, out, tie, scale, D, I, J, \
+                       C, itiles)
+    if (gu_own) { if (C <= 64) QLKA_SIGN(true, 4); else QLKA_SIGN(true, 8); }
+    else        { if (C <= 64) QLKA_SIGN(false, 4); else QLKA_SIGN(false, 8); }
+#undef QLKA_SIGN
+    return (int)hipGetLastError();
+}
+
+int direct_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+               float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, hipStream_t st) {
+    // grad_q[d, m] = sum_n s(q - k) (<g_w[m], v[n]> + g_u[m])
+    if (int e = direct_sign(true, q, k, g_w, v, g_u, grad_q, tie, 1.f, P, D, M, N, C, st)) return e;
+    // grad_k[d, n] = sum_m s(k - q) (<v[n], g_w[m]> + g_u[m])
+    if (int e = direct_sign(false, k, q, v, g_w, g_u, grad_k, tie, 1.f, P, D, N, M, C, st)) return e;
+    // grad_v[n, :] = sum_m A[m, n] g_w[m, :]: the dense abs sum with the roles of q and k swapped
+    return direct_fwd(0, k, q, g_w, grad_v, nullptr, P, D, M, N, C, st);
+}
+
 }  // namespace qlka

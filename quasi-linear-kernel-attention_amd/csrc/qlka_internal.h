@@ -106,6 +106,13 @@ int range_count(int Ns, int C);          // key ranges per segment
 // Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null
 int direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
                int P, int D, int N, int M, int C, hipStream_t st);
+// out[d, i] = scale * sum_j s(a[d,i] - b[d,j]) (<x[i], y[j]> + g_u[own ? i : j]), s(0) = tie; a (P, D, I), b (P, D, J),
+// x (P, I, C), y (P, J, C), g_u nullable
+int direct_sign(bool gu_own, const float* a, const float* b, const float* x, const float* y, const float* gu,
+                float* out, float tie, float scale, int P, int D, int I, int J, int C, hipStream_t st);
+// dense abs backward with sign(0) = tie (0: KeOps, -1: the walk's convention); g_u nullable
+int direct_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+               float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, hipStream_t st);
 
 // Fused attention-layer epilogues (layers.hip)
 enum LayerKind { LAYER_ADD_LAPLACE = 0, LAYER_ADD_RIESZ = 1, LAYER_ADD_BUMP = 2 };

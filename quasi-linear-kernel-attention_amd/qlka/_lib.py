@@ -29,6 +29,8 @@ _SIGNATURES = {
     "qlka_sgn_fwd_ws_bytes": (_c_size, [_c_int] * 5),
     "qlka_sgn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_direct_fwd": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr]),
+    "qlka_direct_bwd": (_c_int, [ctypes.c_float] + [_c_ptr] * 8 + [_c_int] * 5 + [_c_ptr]),
+    "qlka_direct_sgn": (_c_int, [ctypes.c_float] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr]),
     "qlka_layer_fwd_ws_bytes": (_c_size, [_c_int] * 6),
     "qlka_layer_fwd": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_seg_sort_ws_bytes": (_c_size, [_c_int] * 2),

@@ -97,6 +97,39 @@ def weighted_abs_sum_direct_forward(q, k, v, full):
     return out, out_u
 
 
+def weighted_abs_sum_direct_backward(q, k, v, g_w, g_u, tie):
+    """Dense backward (qlka_direct_bwd) with sign(0) = tie: tie 0 is the gradient of the KeOps forward
+    (keops_backend.py:40-41), tie -1 the walk's convention. g_u may be None. Not in the reference's pybind module."""
+    P, D, N, M, C = _check_qkv(q, k, v)
+    _check_grad("g_w", g_w, q, (P, M, C))
+    if g_u is not None:
+        _check_grad("g_u", g_u, q, (P, M))
+    lib = _lib.load()
+    dev = q.device
+    with torch.cuda.device(dev):
+        grad_q = torch.empty((P, D, M), dtype=q.dtype, device=dev)
+        grad_k = torch.empty((P, D, N), dtype=q.dtype, device=dev)
+        grad_v = torch.empty((P, N, C), dtype=q.dtype, device=dev)
+        _lib.check(lib.qlka_direct_bwd(float(tie), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g_w), _lib.ptr(g_u),
+                                       _lib.ptr(grad_q), _lib.ptr(grad_k), _lib.ptr(grad_v), P, D, N, M, C,
+                                       _lib.stream_of(dev)))
+    return grad_q, grad_k, grad_v
+
+
+def weighted_sgn_sum_direct(q, k, v, g, tie):
+    """Dense weighted_sgn_sum (qlka_direct_sgn) with sign(0) = tie (0: keops_backend.py:38-48). Not in the
+    reference's pybind module."""
+    P, D, N, M, C = _check_qkv(q, k, v)
+    _check_grad("g", g, q, (P, M, C))
+    lib = _lib.load()
+    dev = q.device
+    with torch.cuda.device(dev):
+        out = torch.empty((P, D, M), dtype=q.dtype, device=dev)
+        _lib.check(lib.qlka_direct_sgn(float(tie), _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(out),
+                                       P, D, N, M, C, _lib.stream_of(dev)))
+    return out
+
+
 def _backward(q, k, v, g_w, g_u):
     P, D, N, M, C = _check_qkv(q, k, v)
     _check_grad("g_w", g_w, q, (P, M, C))

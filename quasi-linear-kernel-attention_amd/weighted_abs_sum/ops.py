@@ -5,12 +5,10 @@ runs the native gfx950 kernels of libqlka.so:
 
 * "cuda" / "cuda-global" -> path -1 / 0, "cuda-fused" -> path 1 (which, as in the reference, raises for
   max(N, M) > 4096).
-* "keops" (passed by Experiments/kernel_attention/attention.py:63 for S < 256) has no pykeops behind it on ROCm. Its
-  forward runs the native dense evaluation (qlka_direct_fwd: A = sum_d |q_d - k_d| reduced against [v, 1], the
-  computation keops_backend.py:19-35 describes), on contiguous copies as KeOps makes them; its backward and
-  weighted_sgn_sum run the native walk. The only semantic difference from pykeops is the sign of an exact tie in
-  those gradients and in weighted_sgn_sum (pykeops: sign(0) = 0, keops_backend.py:40-41; the walk: the reference's
-  CUDA convention).
+* "keops" (passed by Experiments/kernel_attention/attention.py:63 for S < 256) has no pykeops behind it on ROCm. It
+  runs the native dense evaluation with KeOps' semantics: the forward (qlka_direct_fwd: A = sum_d |q_d - k_d| reduced
+  against [v, 1], keops_backend.py:19-35) on contiguous copies as KeOps makes them, its gradients (qlka_direct_bwd)
+  and weighted_sgn_sum (qlka_direct_sgn) with sign(0) = 0 (keops_backend.py:40-41).
 * "auto" behaves as in the reference: "keops" strictly below KEOPS_CUTOFF, else "cuda".
 """
 
@@ -52,14 +50,18 @@ class _WeightedAbsSum(torch.autograd.Function):
             q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         ctx.save_for_backward(q, k, v)
         ctx.set_materialize_grads(False)
-        if path == _DIRECT:
+        ctx.direct = path == _DIRECT
+        if ctx.direct:
             return _C.weighted_abs_sum_direct_forward(q, k, v, full=False)[0]
         return _C.weighted_abs_sum_forward(q, k, v, path)
 
     @staticmethod
     def backward(ctx, g_w):
         q, k, v = ctx.saved_tensors
-        grad_q, grad_k, grad_v = _C.weighted_abs_sum_backward(q, k, v, g_w.contiguous())
+        if ctx.direct:      # the KeOps gradient: sign(0) = 0
+            grad_q, grad_k, grad_v = _C.weighted_abs_sum_direct_backward(q, k, v, g_w.contiguous(), None, tie=0.0)
+        else:
+            grad_q, grad_k, grad_v = _C.weighted_abs_sum_backward(q, k, v, g_w.contiguous())
         return grad_q, grad_k, grad_v, None
 
 
@@ -70,18 +72,22 @@ class _WeightedAbsSumFull(torch.autograd.Function):
             q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         ctx.save_for_backward(q, k, v)
         ctx.set_materialize_grads(False)
-        if path == _DIRECT:
+        ctx.direct = path == _DIRECT
+        if ctx.direct:
             return _C.weighted_abs_sum_direct_forward(q, k, v, full=True)
         return _C.weighted_abs_sum_full_forward(q, k, v, path)
 
     @staticmethod
     def backward(ctx, g_w, g_u):
         q, k, v = ctx.saved_tensors
-        if g_u is None:     # out_u unused -> the cheaper plain backward
+        if g_w is None:
+            g_w = torch.zeros(q.shape[0], q.shape[2], v.shape[2], device=q.device, dtype=q.dtype)
+        if ctx.direct:      # the KeOps gradient: sign(0) = 0
+            grad_q, grad_k, grad_v = _C.weighted_abs_sum_direct_backward(
+                q, k, v, g_w.contiguous(), None if g_u is None else g_u.contiguous(), tie=0.0)
+        elif g_u is None:   # out_u unused -> the cheaper plain backward
             grad_q, grad_k, grad_v = _C.weighted_abs_sum_backward(q, k, v, g_w.contiguous())
         else:
-            if g_w is None:
-                g_w = torch.zeros(q.shape[0], q.shape[2], v.shape[2], device=q.device, dtype=q.dtype)
             grad_q, grad_k, grad_v = _C.weighted_abs_sum_full_backward(
                 q, k, v, g_w.contiguous(), g_u.contiguous())
         return grad_q, grad_k, grad_v, None
@@ -110,6 +116,8 @@ def weighted_sgn_sum(q, k, v, g, backend="auto"):
     (P, D, M). Not differentiable (it IS a gradient).
     """
     b = _resolve(backend, q, k, v)
+    if b == "keops":        # KeOps semantics: sign(0) = 0 (keops_backend.py:38-48)
+        return _C.weighted_sgn_sum_direct(q.contiguous(), k.contiguous(), v.contiguous(), g.contiguous(), tie=0.0)
     if b == "cuda-fused":
         raise ValueError("weighted_sgn_sum has no fused path; use 'cuda' or 'cuda-global'")
     return _C.weighted_sgn_sum_forward(q, k, v, g.contiguous())

@@ -361,3 +361,55 @@ def test_keops_route_forward_and_autograd(dev, full):
     _assert_rel(_np(tq.grad), wq, nq, "keops route grad_q")
     _assert_rel(_np(tk.grad), wk, nk, "keops route grad_k")
     _assert_rel(_np(tv.grad), wv, nv, "keops route grad_v")
+
+
+@pytest.mark.parametrize("shape", DIRECT_SHAPES[:6])
+@pytest.mark.parametrize("tie", [0.0, -1.0])
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_direct_backward(dev, shape, tie, kind):
+    from weighted_abs_sum import _ext
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 11, kind=kind)
+    rng = np.random.default_rng(8)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    for full in (False, True):
+        gq, gk, gv = _ext.weighted_abs_sum_direct_backward(_t(q, dev), _t(k, dev), _t(v, dev), _t(g_w, dev),
+                                                           _t(g_u, dev) if full else None, tie)
+        (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u if full else None, tie=tie)
+        _assert_rel(_np(gq), wq, nq, f"direct grad_q tie={tie} full={full}")
+        _assert_rel(_np(gk), wk, nk, f"direct grad_k tie={tie} full={full}")
+        _assert_rel(_np(gv), wv, nv, f"direct grad_v full={full}")
+
+
+@pytest.mark.parametrize("shape", DIRECT_SHAPES[:6])
+@pytest.mark.parametrize("tie", [0.0, 1.0])
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_direct_sgn(dev, shape, tie, kind):
+    from weighted_abs_sum import _ext
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 12, kind=kind)
+    g = np.random.default_rng(9).standard_normal((P, M, C)).astype(np.float32)
+    out = _ext.weighted_sgn_sum_direct(_t(q, dev), _t(k, dev), _t(v, dev), _t(g, dev), tie)
+    want, norm = brute.sgn_sum(q, k, v, g, tie=tie)
+    _assert_rel(_np(out), want, norm, f"direct sgn tie={tie}")
+
+
+def test_keops_route_tie_semantics(dev):
+    # exact q == k ties: the "keops" backend follows KeOps' sign(0) = 0 in its gradients and in weighted_sgn_sum
+    from weighted_abs_sum import weighted_abs_sum_full, weighted_sgn_sum
+    P, D, N, M, C = 2, 3, 90, 70, 8
+    q, k, v = _data(P, D, N, M, C, seed=41, kind="ties")
+    rng = np.random.default_rng(10)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+    w, u = weighted_abs_sum_full(tq, tk, tv, backend="keops")
+    ((w * _t(g_w, dev)).sum() + (u * _t(g_u, dev)).sum()).backward()
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u, tie=0.0)
+    _assert_rel(_np(tq.grad), wq, nq, "keops grad_q (tie 0)")
+    _assert_rel(_np(tk.grad), wk, nk, "keops grad_k (tie 0)")
+    _assert_rel(_np(tv.grad), wv, nv, "keops grad_v")
+    out = weighted_sgn_sum(_t(q, dev), _t(k, dev), _t(v, dev), _t(g_w, dev), backend="keops")
+    want, norm = brute.sgn_sum(q, k, v, g_w, tie=0.0)
+    _assert_rel(_np(out), want, norm, "keops sgn (tie 0)")

@@ -262,3 +262,34 @@ def test_backward_subsample_matches_full():
     np.testing.assert_allclose(sv, fv[:, kidx[0]], rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(nsq, nfq[:, :, qidx[0]], rtol=1e-12)
     np.testing.assert_allclose(nsv, nfv[:, kidx[0]], rtol=1e-12)
+
+
+def test_backward_tie_convention():
+    # s(0) = tie enters linearly: grad(tie) - grad(-1) = (tie + 1) * (sum of B' over the exact ties), with the tie mass
+    # counted here by explicit loops; the KeOps sgn sum is -grad_q at tie 0 (keops_backend.py:38-48)
+    rng = np.random.default_rng(21)
+    P, D, N, M, C = 2, 3, 9, 7, 4
+    q = (rng.integers(-2, 3, size=(P, D, M)) / 2).astype(np.float32)
+    k = (rng.integers(-2, 3, size=(P, D, N)) / 2).astype(np.float32)
+    v = rng.standard_normal((P, N, C)).astype(np.float32)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    (q1, k1, v1), _ = brute.abs_backward(q, k, v, g_w, g_u, tie=-1.0)
+    tq = np.zeros((P, D, M)); tk = np.zeros((P, D, N))
+    for p in range(P):
+        for d in range(D):
+            for m in range(M):
+                for n in range(N):
+                    if q[p, d, m] == k[p, d, n]:
+                        b = float(np.dot(g_w[p, m].astype(np.float64), v[p, n].astype(np.float64))) + float(g_u[p, m])
+                        tq[p, d, m] += b
+                        tk[p, d, n] += b
+    assert np.abs(tq).sum() > 0, "the inputs must contain ties"
+    for tie in (0.0, 0.5, 1.0):
+        (qt, kt, vt), _ = brute.abs_backward(q, k, v, g_w, g_u, tie=tie)
+        np.testing.assert_allclose(qt - q1, (tie + 1) * tq, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(kt - k1, (tie + 1) * tk, rtol=1e-12, atol=1e-12)
+        np.testing.assert_allclose(vt, v1, rtol=1e-12, atol=1e-12)     # grad_v has no sign
+    (q0, _, _), _ = brute.abs_backward(q, k, v, g_w, None, tie=0.0)
+    sg, _ = brute.sgn_sum(q, k, v, g_w, tie=0.0)
+    np.testing.assert_allclose(sg, -q0, rtol=1e-12, atol=1e-12)
