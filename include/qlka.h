@@ -115,6 +115,18 @@ int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, con
                    int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The same layers with the key mask applied inside the sums: q (P, D, M) and k (P, D, N) divided by tau, k and v NOT
+ * multiplied by the mask, keep (P, N) bytes (nonzero = real key, non-null). Masked keys weigh 0 in every sum, so w and
+ * u run over the real keys only and the n_pad corrections become exact (add_laplace: out = w / clamp(u, 1e-6), ...);
+ * no k * keep or v * keep is materialised. Same values as qlka_layer_fwd on k * keep, v * keep and n_pad = N - #kept,
+ * without the cancellation of the n_pad terms. Workspace: qlka_layer_fwd_ws_bytes.
+ * Replaces the keep branch of attention() (Experiments/kernel_attention/attention.py:122-124) around _add_laplace /
+ * _add_riesz / _add_bump, and the padded-key rule of Weighted_Laplace_Sum/weighted_laplace_sum/__init__.py:12.
+ */
+int qlka_layer_fwd_masked(int kind, const float* q, const float* k, const float* v, const uint8_t* keep, float* out,
+                          int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Test entry: stable ascending sort of num_segs contiguous segments of seg_len fp32 keys; perm[i] is the in-segment
  * index of the i-th smallest key (np.argsort(kind="stable"); -0.0 ties +0.0 and is written as +0.0).
  * Replaces launch_iota + launch_cub_sort (Weighted_Abs_Sum/csrc/sort_utils.cu:85-117).

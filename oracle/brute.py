@@ -6,6 +6,9 @@ Weighted_Abs_Sum/csrc/abs_kernels.cu:9-19) used only to pin the brute force in t
 
 Layouts are the reference's: q (P, D, M), k (P, D, N), v (P, N, C), g (P, M, C), g_u (P, M).
 `qidx` (optional, int array (P, Mq)) restricts the evaluation to a subsample of queries of each p.
+`keep` (optional, (P, N), nonzero = kept) drops the masked keys from every sum (the in-kernel key mask); it is pinned
+by the reference's own composition over zeroed keys: k * keep, v * keep and the n_pad correction of u
+(attention.py:122-124, weighted_laplace_sum/__init__.py:12), a different computation of the same value.
 
 Function                       reference                                                     pinned by (tests/test_oracle.py)
 abs_sum                        ops.py:107-126, keops_backend.py:19-36                          sorted-prefix closed form, N=1 / D=1 cases,
@@ -41,29 +44,33 @@ def _select(q, qidx):
     return np.stack([q[p][:, qidx[p]] for p in range(q.shape[0])]), qidx
 
 
-def abs_sum(q, k, v, qidx=None):
+def _kept(keep, p, N):
+    return np.ones(N, dtype=np.float64) if keep is None else (np.asarray(keep[p]) != 0).astype(np.float64)
+
+
+def abs_sum(q, k, v, qidx=None, keep=None):
     """(out_w, out_u, norm_w): out_w[p,m,c] = sum_{d,n} |k[p,d,n] - q[p,d,m]| v[p,n,c], out_u[p,m] = sum_{d,n} |k-q|,
-    norm_w[p,m,c] = sum_{d,n} |k - q| |v[p,n,c]| (the per-element error normaliser)."""
+    norm_w[p,m,c] = sum_{d,n} |k - q| |v[p,n,c]| (the per-element error normaliser); n over the kept keys."""
     qs, _ = _select(q, qidx)
     k, v = _f64(k), _f64(v)
     P = qs.shape[0]
     out_w, out_u, norm = [], [], []
     for p in range(P):
-        A = _pairwise(qs[p], k[p], np.abs)
+        A = _pairwise(qs[p], k[p], np.abs) * _kept(keep, p, k.shape[2])[None, :]
         out_w.append(A @ v[p])
         out_u.append(A.sum(axis=1))
         norm.append(A @ np.abs(v[p]))
     return np.stack(out_w), np.stack(out_u), np.stack(norm)
 
 
-def laplace_sum(q, k, v, qidx=None):
-    """(out_w, out_u, norm_w) with the Laplace kernel exp(-|k - q|) in place of |k - q|."""
+def laplace_sum(q, k, v, qidx=None, keep=None):
+    """(out_w, out_u, norm_w) with the Laplace kernel exp(-|k - q|) in place of |k - q|; n over the kept keys."""
     qs, _ = _select(q, qidx)
     k, v = _f64(k), _f64(v)
     P = qs.shape[0]
     out_w, out_u, norm = [], [], []
     for p in range(P):
-        A = _pairwise(qs[p], k[p], lambda x: np.exp(-np.abs(x)))
+        A = _pairwise(qs[p], k[p], lambda x: np.exp(-np.abs(x))) * _kept(keep, p, k.shape[2])[None, :]
         out_w.append(A @ v[p])
         out_u.append(A.sum(axis=1))
         norm.append(A @ np.abs(v[p]))

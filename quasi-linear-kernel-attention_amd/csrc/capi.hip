@@ -140,7 +140,7 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     const int S = P * D;
     SortedWs w = carve(ws, spec);
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
-    int e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+    int e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, nullptr, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
     if (e) return hip_status(e, "laplace walk");
     e = reduce_slabs(w.slab, w.uslab, w.qinv, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "laplace reduce");
@@ -341,9 +341,11 @@ size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C) {
     return layer_ws_bytes(kind, WsSpec{P, D, N, M, C, N, M, true});
 }
 
-int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad, float* out,
-                   int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
-    g_err.clear();
+// Both layer entry points: keep == null is the reference's composition over pre-masked k, v and n_pad; keep != null
+// applies the key mask inside the sums (k and v as given, no n_pad).
+static int layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad,
+                     const uint8_t* keep, float* out, int P, int D, int N, int M, int C, void* ws,
+                     size_t ws_bytes_given, void* stream) {
     if (kind < 0 || kind > 2) return fail(QLKA_EINVAL, "kind must be 0 (add_laplace), 1 (add_riesz) or 2 (add_bump)");
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !out) return fail(QLKA_EINVAL, "q, k, v and out must be non-null");
@@ -356,13 +358,13 @@ int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, con
     if (int e = sort_both(q, k, w, S, N, M, st)) return e;
     int e = 0;
     if (kind == LAYER_ADD_LAPLACE) {
-        e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+        e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, keep, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
         if (e) return hip_status(e, "laplace walk");
         e = reduce_slabs(w.slab, w.uslab, w.qinv, L.w[0], L.u[0], P, D, M, C, st);
         if (e) return hip_status(e, "laplace reduce");
     } else {
         AbsWalkArgs a{};
-        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
+        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr; a.keep = keep;
         a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
         a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
         a.out_dot = nullptr; a.out_rank = nullptr;
@@ -388,14 +390,28 @@ int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, con
             if (e) return hip_status(e, "abs reduce");
         }
         if (kind == LAYER_ADD_RIESZ) {
-            e = riesz_prefix(k, v, L.pre, P, D, N, C, st);
+            e = riesz_prefix(k, v, keep, L.pre, P, D, N, C, st);
             if (e) return hip_status(e, "riesz prefixes");
         }
     }
     const bool bump = kind == LAYER_ADD_BUMP;
-    e = layer_epilogue(kind, q, n_pad, L.w[0], L.u[0], bump ? L.w[1] : nullptr, bump ? L.u[1] : nullptr,
-                       bump ? L.w[2] : nullptr, bump ? L.u[2] : nullptr, L.pre, L.qt, out, P, D, N, M, C, st);
+    e = layer_epilogue(kind, keep != nullptr, q, n_pad, L.w[0], L.u[0], bump ? L.w[1] : nullptr,
+                       bump ? L.u[1] : nullptr, bump ? L.w[2] : nullptr, bump ? L.u[2] : nullptr, L.pre, L.qt, out,
+                       P, D, N, M, C, st);
     return hip_status(e, "layer epilogue");
+}
+
+int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad, float* out,
+                   int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
+    g_err.clear();
+    return layer_fwd(kind, q, k, v, n_pad, nullptr, out, P, D, N, M, C, ws, ws_bytes_given, stream);
+}
+
+int qlka_layer_fwd_masked(int kind, const float* q, const float* k, const float* v, const uint8_t* keep, float* out,
+                          int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
+    g_err.clear();
+    if (!keep) return fail(QLKA_EINVAL, "keep must be non-null (qlka_layer_fwd is the unmasked entry)");
+    return layer_fwd(kind, q, k, v, nullptr, keep, out, P, D, N, M, C, ws, ws_bytes_given, stream);
 }
 
 // ------------------------------------------------------------------------------------------------ test entries

@@ -12,6 +12,13 @@
 // with CLAMP = 1e-6 (attention.py:20), EPS = 1e-3 (kernels.py:9) and S = q.shape[2] (the number of queries, as the
 // reference writes it). Every expression keeps the reference's operation order in fp32. The per-query d-reductions
 // (sum_d e^{-|q_d|}, |q|_1, sum_d max(0, 1 - |q_d|)) are computed once per query before the per-channel pass.
+//
+// Masked form (key mask applied inside the sums, attention.py:122-124 without materialising k * keep, v * keep): w
+// and u then already run over the kept keys only, which is what the n_pad terms above remove from the reference's
+// sums over zeroed keys (a zeroed key adds e^{-|q_d|}, |q_d| or max(0, 1 - |q_d|) per feature to u). So add_laplace
+// and add_bump drop their n_pad term, and add_riesz, whose u lost n_pad |q|_1, keeps the reference's algebra as
+//   den = (|q|_1 + EPS) * S + sum_kept |k_n|_1 - u - n_pad (|q|_1 + EPS),  n_pad = N - #kept,
+// with sum_n v and sum_n |k_n|_1 v_n over the kept keys.
 #include "qlka_common.h"
 #include "qlka_internal.h"
 
@@ -24,30 +31,36 @@ constexpr int RZ_T = 256;          // threads per block of the layer kernels
 
 static inline size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// pre layout: vsum (P, C) | akv (P, C) | sak (P) | partials (P, RZ_NB, 2C + 1)
+// pre layout: vsum (P, C) | akv (P, C) | sak (P) | npad (P) | partials (P, RZ_NB, 2C + 2)
 size_t riesz_prefix_bytes(int P, int N, int C) {
     (void)N;
-    return 2 * al256((size_t)P * C * 4) + al256((size_t)P * 4) + al256((size_t)P * RZ_NB * (2 * C + 1) * 4);
+    return 2 * al256((size_t)P * C * 4) + 2 * al256((size_t)P * 4) + al256((size_t)P * RZ_NB * (2 * C + 2) * 4);
 }
 
-// One block per (p, key chunk): |k_n|_1 of the chunk's keys into LDS, then per channel the chunk's sum_n v and
-// sum_n |k_n|_1 v (G = RZ_T / C row groups per channel, combined in LDS), and the chunk's sum_n |k_n|_1.
+// One block per (p, key chunk): |k_n|_1 of the chunk's keys into LDS (0 for masked keys), then per channel the
+// chunk's sum_n v and sum_n |k_n|_1 v over its kept keys (G = RZ_T / C row groups per channel, combined in LDS), the
+// chunk's sum_n |k_n|_1 and its count of kept keys.
 __global__ __launch_bounds__(RZ_T)
-void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, float* __restrict__ part,
-                    const int D, const int N, const int C)
+void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, const uint8_t* __restrict__ keep,
+                    float* __restrict__ part, const int D, const int N, const int C)
 {
     __shared__ float aks[(131072 + RZ_NB - 1) / RZ_NB];
+    __shared__ uint8_t kept[(131072 + RZ_NB - 1) / RZ_NB];
     __shared__ float red[2][RZ_T];
     const int p = blockIdx.x / RZ_NB, b = blockIdx.x - p * RZ_NB, tid = threadIdx.x;
     const int chunk = (N + RZ_NB - 1) / RZ_NB;
     const int n0 = min(N, b * chunk), n1 = min(N, n0 + chunk);
     const float* kp = k + (size_t)p * D * N;
-    float sak = 0.f;
+    float sak = 0.f, cnt = 0.f;
     for (int n = n0 + tid; n < n1; n += RZ_T) {
+        const bool kn = !keep || keep[(size_t)p * N + n] != 0;
         float a = 0.f;
-        for (int d = 0; d < D; ++d) a += fabsf(kp[(size_t)d * N + n]);
+        if (kn)
+            for (int d = 0; d < D; ++d) a += fabsf(kp[(size_t)d * N + n]);
         aks[n - n0] = a;
+        kept[n - n0] = kn;
         sak += a;
+        cnt += kn ? 1.f : 0.f;
     }
     __syncthreads();
     const int G = RZ_T / C;                               // >= 2 for C <= 128
@@ -56,6 +69,7 @@ void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, fl
     if (rg < G) {
         const float* vp = v + (size_t)p * N * C;
         for (int n = n0 + rg; n < n1; n += G) {
+            if (!kept[n - n0]) continue;
             const float x = vp[(size_t)n * C + c];
             sv += x;
             skv += aks[n - n0] * x;
@@ -64,7 +78,7 @@ void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, fl
     red[0][tid] = sv;
     red[1][tid] = skv;
     __syncthreads();
-    float* out = part + ((size_t)p * RZ_NB + b) * (2 * C + 1);
+    float* out = part + ((size_t)p * RZ_NB + b) * (2 * C + 2);
     if (tid < C) {
         float a0 = 0.f, a1 = 0.f;
         for (int r = 0; r < G; ++r) { a0 += red[0][r * C + tid]; a1 += red[1][r * C + tid]; }
@@ -73,20 +87,21 @@ void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, fl
     }
     __syncthreads();
     red[0][tid] = sak;
+    red[1][tid] = cnt;
     __syncthreads();
     for (int off = RZ_T / 2; off >= 1; off >>= 1) {
-        if (tid < off) red[0][tid] += red[0][tid + off];
+        if (tid < off) { red[0][tid] += red[0][tid + off]; red[1][tid] += red[1][tid + off]; }
         __syncthreads();
     }
-    if (tid == 0) out[2 * C] = red[0][0];
+    if (tid == 0) { out[2 * C] = red[0][0]; out[2 * C + 1] = red[1][0]; }
 }
 
-// Chunk partials summed in chunk order (deterministic): one thread per (p, j), j < 2C + 1.
+// Chunk partials summed in chunk order (deterministic): one thread per (p, j), j < 2C + 2; npad = N - kept keys.
 __global__ __launch_bounds__(RZ_T)
 void riesz_finish(const float* __restrict__ part, float* __restrict__ vsum, float* __restrict__ akv,
-                  float* __restrict__ sak, const int P, const int C)
+                  float* __restrict__ sak, float* __restrict__ npad, const int P, const int N, const int C)
 {
-    const int W = 2 * C + 1;
+    const int W = 2 * C + 2;
     const int i = blockIdx.x * RZ_T + threadIdx.x;
     if (i >= P * W) return;
     const int p = i / W, j = i - p * W;
@@ -94,20 +109,23 @@ void riesz_finish(const float* __restrict__ part, float* __restrict__ vsum, floa
     for (int b = 0; b < RZ_NB; ++b) a += part[((size_t)p * RZ_NB + b) * W + j];
     if (j < C) vsum[(size_t)p * C + j] = a;
     else if (j < 2 * C) akv[(size_t)p * C + (j - C)] = a;
-    else sak[p] = a;
+    else if (j == 2 * C) sak[p] = a;
+    else npad[p] = (float)N - a;
 }
 
-int riesz_prefix(const float* k, const float* v, void* pre, int P, int D, int N, int C, hipStream_t st) {
+int riesz_prefix(const float* k, const float* v, const uint8_t* keep, void* pre, int P, int D, int N, int C,
+                 hipStream_t st) {
     char* b = (char*)pre;
     float* vsum = (float*)b;  b += al256((size_t)P * C * 4);
     float* akv = (float*)b;   b += al256((size_t)P * C * 4);
     float* sak = (float*)b;   b += al256((size_t)P * 4);
+    float* npad = (float*)b;  b += al256((size_t)P * 4);
     float* part = (float*)b;
     StageTimer t("riesz_prefix", st);
-    hipLaunchKernelGGL(riesz_partials, dim3((unsigned)(P * RZ_NB)), dim3(RZ_T), 0, st, k, v, part, D, N, C);
-    const int n = P * (2 * C + 1);
+    hipLaunchKernelGGL(riesz_partials, dim3((unsigned)(P * RZ_NB)), dim3(RZ_T), 0, st, k, v, keep, part, D, N, C);
+    const int n = P * (2 * C + 2);
     hipLaunchKernelGGL(riesz_finish, dim3((unsigned)((n + RZ_T - 1) / RZ_T)), dim3(RZ_T), 0, st, part, vsum, akv, sak,
-                       P, C);
+                       npad, P, N, C);
     return (int)hipGetLastError();
 }
 
@@ -131,8 +149,9 @@ void layer_query_terms(const float* __restrict__ q, float* __restrict__ qt, cons
     qt[i] = a;
 }
 
-// Every channel of the output rows: one thread per (p, m, c).
-template <int KIND>
+// Every channel of the output rows: one thread per (p, m, c). MASKED: w and u are sums over the kept keys (n_pad then
+// only enters add_riesz's count term).
+template <int KIND, bool MASKED>
 __global__ __launch_bounds__(RZ_T)
 void layer_epilogue_kernel(const float* __restrict__ qt, const float* __restrict__ n_pad,
                            const float* __restrict__ w0, const float* __restrict__ u0,
@@ -150,19 +169,20 @@ void layer_epilogue_kernel(const float* __restrict__ qt, const float* __restrict
     float num, den;
     if constexpr (KIND == LAYER_ADD_LAPLACE) {
         num = w0[i];
-        den = u0[pm] - np * qt[pm];
+        den = MASKED ? u0[pm] : u0[pm] - np * qt[pm];
     } else if constexpr (KIND == LAYER_ADD_RIESZ) {
         const float aqe = qt[pm] + LAYER_EPS;
         num = aqe * vsum[(size_t)p * C + c] + akv[(size_t)p * C + c] - w0[i];
-        den = aqe * (float)M + sak[p] - u0[pm] - LAYER_EPS * np;
+        den = MASKED ? aqe * (float)M + sak[p] - u0[pm] - np * aqe
+                     : aqe * (float)M + sak[p] - u0[pm] - LAYER_EPS * np;
     } else {
         num = (wp[i] + wm[i]) / 2.f - w0[i];
-        den = (up[pm] + um[pm]) / 2.f - u0[pm] - np * qt[pm];
+        den = MASKED ? (up[pm] + um[pm]) / 2.f - u0[pm] : (up[pm] + um[pm]) / 2.f - u0[pm] - np * qt[pm];
     }
     out[i] = num / fmaxf(den, LAYER_CLAMP);
 }
 
-int layer_epilogue(int kind, const float* q, const float* n_pad, const float* w0, const float* u0,
+int layer_epilogue(int kind, bool masked, const float* q, const float* n_pad, const float* w0, const float* u0,
                    const float* wp, const float* up, const float* wm, const float* um, const void* pre, float* qt,
                    float* out, int P, int D, int N, int M, int C, hipStream_t st) {
     const float *vsum = nullptr, *akv = nullptr, *sak = nullptr;
@@ -170,16 +190,22 @@ int layer_epilogue(int kind, const float* q, const float* n_pad, const float* w0
         const char* b = (const char*)pre;
         vsum = (const float*)b;  b += al256((size_t)P * C * 4);
         akv = (const float*)b;   b += al256((size_t)P * C * 4);
-        sak = (const float*)b;
+        sak = (const float*)b;   b += al256((size_t)P * 4);
+        if (masked) n_pad = (const float*)b;              // N - kept keys, from riesz_prefix
     }
+    if (masked && kind != LAYER_ADD_RIESZ) n_pad = nullptr;
     (void)N;
     const long nq = (long)P * M, n = nq * C;
     const unsigned qblocks = (unsigned)((nq + RZ_T - 1) / RZ_T), blocks = (unsigned)((n + RZ_T - 1) / RZ_T);
     StageTimer t("layer_epilogue", st);
 #define QLKA_LAYER_LAUNCH(K)                                                                                        \
     hipLaunchKernelGGL(layer_query_terms<K>, dim3(qblocks), dim3(RZ_T), 0, st, q, qt, P, D, M);                    \
-    hipLaunchKernelGGL(layer_epilogue_kernel<K>, dim3(blocks), dim3(RZ_T), 0, st, qt, n_pad, w0, u0, wp, up, wm, um, \
-                       vsum, akv, sak, out, P, M, C)
+    if (masked)                                                                                                     \
+        hipLaunchKernelGGL((layer_epilogue_kernel<K, true>), dim3(blocks), dim3(RZ_T), 0, st, qt, n_pad, w0, u0, wp,  \
+                           up, wm, um, vsum, akv, sak, out, P, M, C);                                               \
+    else                                                                                                            \
+        hipLaunchKernelGGL((layer_epilogue_kernel<K, false>), dim3(blocks), dim3(RZ_T), 0, st, qt, n_pad, w0, u0, wp, \
+                           up, wm, um, vsum, akv, sak, out, P, M, C)
     switch (kind) {
         case LAYER_ADD_LAPLACE: QLKA_LAYER_LAUNCH(LAYER_ADD_LAPLACE); break;
         case LAYER_ADD_RIESZ:   QLKA_LAYER_LAUNCH(LAYER_ADD_RIESZ); break;

@@ -56,9 +56,11 @@ int fill_zero(float* p, size_t n, hipStream_t st);
 __host__ __device__ inline int slab_stride(int C) { return (C + 31) / 32 * 32; }
 
 // Per feature d of p: slab[(p*D + d)*M + m][c] = sum_n exp(-|k_n - q_m|) v[p,n,c] (row stride slab_stride(C)),
-// uslab[(p*D + d)*M + i] = sum_n exp(-|k_n - q_(i)|) for the i-th smallest query of the feature.
+// uslab[(p*D + d)*M + i] = sum_n exp(-|k_n - q_(i)|) for the i-th smallest query of the feature. keep (P, N) bytes,
+// nonzero = kept, or null: the sums run over the kept keys only.
 int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st);
+                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
+                 hipStream_t st);
 
 // D-reduction of the slabs: out[p,m,c] = sum_d slab[(p*D+d)*M + m][c]; out_u[p,m] = sum_d uslab[(p*D+d)*M + qinv]
 // with qinv[(p*D+d)*M + m] the sorted position of query m in feature d. out_u / uslab / qinv may be null.
@@ -80,6 +82,7 @@ struct AbsWalkArgs {
     const float* ks; const uint32_t* kp; int Ns;
     const float* w;          // (P, Ns, C) weight rows, gathered by kp
     const float* u;          // (P, Ns) scalar weights (ABS_DOTX2) or null
+    const uint8_t* keep;     // (P, Ns) key mask, nonzero = kept, or null (all kept); masked keys weigh 0 in every sum
     // queries
     const float* qs; const uint32_t* qp; int Mq;
     const float* g;          // (P, Mq, C) rows dotted at emission (ABS_DOT) or null
@@ -117,12 +120,14 @@ int direct_bwd(float tie, const float* q, const float* k, const float* v, const 
 // Fused attention-layer epilogues (layers.hip)
 enum LayerKind { LAYER_ADD_LAPLACE = 0, LAYER_ADD_RIESZ = 1, LAYER_ADD_BUMP = 2 };
 size_t riesz_prefix_bytes(int P, int N, int C);
-// add_riesz per-p constants: vsum[p][c] = sum_n v, akv[p][c] = sum_n |k_n|_1 v_n, sak[p] = sum_n |k_n|_1 (pre must
-// hold riesz_prefix_bytes)
-int riesz_prefix(const float* k, const float* v, void* pre, int P, int D, int N, int C, hipStream_t st);
-// out[p][m][:] from the op outputs: w0/u0 (and, for add_bump, w+/u+ and w-/u- of q + 1 and q - 1)
-// qt: (P, M) scratch for the per-query d-reductions
-int layer_epilogue(int kind, const float* q, const float* n_pad, const float* w0, const float* u0,
+// add_riesz per-p constants over the kept keys (keep (P, N) bytes, nonzero = kept, or null): vsum[p][c] = sum_n v,
+// akv[p][c] = sum_n |k_n|_1 v_n, sak[p] = sum_n |k_n|_1, npad[p] = N - #kept (pre must hold riesz_prefix_bytes)
+int riesz_prefix(const float* k, const float* v, const uint8_t* keep, void* pre, int P, int D, int N, int C,
+                 hipStream_t st);
+// out[p][m][:] from the op outputs: w0/u0 (and, for add_bump, w+/u+ and w-/u- of q + 1 and q - 1). masked: the op
+// outputs are sums over the kept keys and n_pad is ignored (add_riesz takes its n_pad from pre); else n_pad (P) is
+// the reference's padded-key count (null: none). qt: (P, M) scratch for the per-query d-reductions
+int layer_epilogue(int kind, bool masked, const float* q, const float* n_pad, const float* w0, const float* u0,
                    const float* wp, const float* up, const float* wm, const float* um, const void* pre, float* qt,
                    float* out, int P, int D, int N, int M, int C, hipStream_t st);
 

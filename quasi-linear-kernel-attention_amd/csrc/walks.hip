@@ -94,6 +94,27 @@ __device__ __forceinline__ int range_rank(const float kl, const int nk, const fl
     return pos;
 }
 
+// Weight of a key in the sums: 0 for the pad lanes of a partial range and for keys masked out by keep (P, Ns bytes,
+// nonzero = kept, indexed by the key's original position n), else 1. A masked key keeps its value and its place in the
+// sorted order; weighing 0, it adds nothing to any sum, so no correction for padded keys is needed afterwards.
+__device__ __forceinline__ float key_weight(const uint8_t* keep, const int p, const int Ns, const uint32_t n,
+                                            const bool real) {
+    if (!real) return 0.f;
+    return (keep && keep[(size_t)p * Ns + n] == 0) ? 0.f : 1.f;
+}
+
+// Zero the gathered rows of masked keys (x[t] holds key t of the range; kw is lane t's key weight). A select, not a
+// product, so a masked key's row is dropped whatever it holds.
+template <int NV, int RK>
+__device__ __forceinline__ void mask_rows(float (&x)[RK][NV], const float kw) {
+#pragma unroll
+    for (int t = 0; t < RK; ++t) {
+        const bool kept = bcast(kw, t) != 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) x[t][j] = kept ? x[t][j] : 0.f;
+    }
+}
+
 // =================================================================================================================
 // Laplace
 // =================================================================================================================
@@ -103,7 +124,8 @@ __device__ __forceinline__ int range_rank(const float kl, const int nk, const fl
 template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
 void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
-                    const float* __restrict__ v, float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
+                    const float* __restrict__ v, const uint8_t* __restrict__ keep, float* __restrict__ ta,
+                    float* __restrict__ tb, int* __restrict__ qb,
                     const int S, const int D, const int N, const int M, const int C, const int G)  // ta/tb: summaries
 {
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
@@ -117,9 +139,9 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
     const float kl = kseg[li];
     const uint32_t pl = kp[(size_t)s * N + li];
     const float kfirst = kseg[base], klast = kseg[base + nk - 1];
-    const bool real = l < nk;
-    const float wl = real ? __expf(-(klast - kl)) : 0.f;
-    const float wr = real ? __expf(-(kl - kfirst)) : 0.f;
+    const float kw = key_weight(keep, p, N, pl, l < nk);
+    const float wl = kw * __expf(-(klast - kl));
+    const float wr = kw * __expf(-(kl - kfirst));
 
     const rsrc_t vr = make_rsrc(v + (size_t)p * N * C, (uint32_t)((size_t)N * C * 4));
     float sl[NV], sr[NV];
@@ -302,12 +324,36 @@ struct EmitLanes {
 };
 
 
+// The first two blocks of 64 owned queries of a range (sorted value and query index, lane = query; indices clamped
+// into [0, q1 - 1], as the emission loop clamps them), loaded at the start of the range so that their latency
+// overlaps the row gathers. settle() makes the wave wait for them there, before its first store: vmcnt counts loads
+// and stores in issue order, so a load issued after the emission stores, or first waited for after them, also waits
+// until those stores have reached L2. Blocks from the third on (ranges owning more than 128 queries) load in place.
+struct QueryBlocks {
+    float v0, v1;
+    uint32_t m0, m1;
+    __device__ __forceinline__ QueryBlocks(const float* qseg, const uint32_t* qpseg, const int q0, const int q1) {
+        const int l = lane_id(), hi = max(q1 - 1, 0);
+        const int i0 = min(q0 + l, hi), i1 = min(q0 + WAVE + l, hi);
+        v0 = qseg[i0]; m0 = qpseg[i0];
+        v1 = qseg[i1]; m1 = qpseg[i1];
+    }
+    __device__ __forceinline__ void settle() { asm volatile("" : "+v"(v0), "+v"(v1), "+v"(m0), "+v"(m1)); }
+    // block b of the range (queries from q0 + 64 b); qi = the lane's clamped query index in it
+    __device__ __forceinline__ void get(const int b, const float* qseg, const uint32_t* qpseg, const int qi,
+                                        float& qv, uint32_t& mq) const {
+        if (b == 0) { qv = v0; mq = m0; }
+        else if (b == 1) { qv = v1; mq = m1; }
+        else { qv = qseg[qi]; mq = qpseg[qi]; }
+    }
+};
+
 constexpr int RPW = 1;             // consecutive key ranges walked by one wave of a walk kernel
 
 template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
 void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
-                    const uint32_t* __restrict__ qp, const float* __restrict__ v,
+                    const uint32_t* __restrict__ qp, const float* __restrict__ v, const uint8_t* __restrict__ keep,
                     const float* __restrict__ ta, const float* __restrict__ tb, const int* __restrict__ qb,
                     float* __restrict__ slab, float* __restrict__ uslab,
                     const int S, const int D, const int N, const int M, const int C, const int CR, const int G)
@@ -340,6 +386,10 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
         const bool has_prev = g > 0, has_next = g < G - 1;
         const float kbefore = has_prev ? kseg[base - 1] : 0.f;
         const float kafter  = has_next ? kseg[base + RK] : 0.f;
+        const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+        const int q1 = has_next ? qb[(size_t)s * G + g] : M;
+        QueryBlocks qbk(qseg, qpseg, q0, q1);
+        const float kw = key_weight(keep, p, N, kpseg[li], real);
 
         // value rows of the range, lane = channel (pad keys and pad channels: zero). The row indices are read with
         // scalar loads straight into SGPRs (the buffer offset of each row gather).
@@ -368,6 +418,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
                 for (int j = 0; j < NV; ++j)
                     x[t][j] = (t < nk && l + WAVE * j < C) ? x[t][j] : 0.f;
         }
+        if (keep) mask_rows<NV, RK>(x, kw);
 
         const float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
         const float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
@@ -390,10 +441,10 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
         const float dnext = (l == RK - 1 && !has_next) ? 0.f : __expf(-(kaft - kl));
 
         // v == 1 channel: L1 after key t and R1 at key t, as lane-t values of two affine scans
-        float a1 = (l < RK) ? dprev : 1.f, b1 = real ? 1.f : 0.f;
+        float a1 = (l < RK) ? dprev : 1.f, b1 = kw;
         wave_affine_scan_fwd(a1, b1);
         const float l1 = a1 * L1in + b1;
-        float a2 = (l < RK) ? dnext : 1.f, b2 = real ? 1.f : 0.f;
+        float a2 = (l < RK) ? dnext : 1.f, b2 = kw;
         wave_affine_scan_bwd(a2, b2);
         const float r1 = a2 * R1out + b2;
 
@@ -421,14 +472,14 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
         // buffers, slab row offset, eL, eR) goes to LDS. Then the keys are walked in 4 chunks of CH: the chunk's rows
         // L_{t-1} (state before key t) and R_t go to LDS and the queries ranked in the chunk are emitted as
         // eL * L_{t-1} + eR * R_t, several query rows per store instruction.
-        const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
-        const int q1 = has_next ? qb[(size_t)s * G + g] : M;
-        for (int qb0 = q0; qb0 < q1; qb0 += WAVE) {
+        qbk.settle();
+        for (int qb0 = q0, bi = 0; qb0 < q1; qb0 += WAVE, ++bi) {
             const int nq = min(WAVE, q1 - qb0);
             const bool act = l < nq;
             const int qi = min(qb0 + l, q1 - 1);          // clamped: unconditional loads
-            const float qv = qseg[qi];
-            const uint32_t mq = qpseg[qi];
+            float qv;
+            uint32_t mq;
+            qbk.get(bi, qseg, qpseg, qi, qv, mq);
             const int t = range_rank<RK>(kl, nk, qv);
             const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
             const float knv = __shfl(kl, min(t, RK - 1), WAVE);
@@ -513,8 +564,8 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 
 template <int NV, int RK>
 static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                          float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
-                          hipStream_t st) {
+                          const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C,
+                          RangeArrays ra, hipStream_t st) {
     const int S = P * D;
     const int G = (N + RK - 1) / RK;
     const long waves = (long)S * G;
@@ -522,7 +573,7 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
     {
         StageTimer t("lap_range_sums", st);
         hipLaunchKernelGGL((lap_range_sums<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                           ks, kp, qs, v, ra.sa, ra.sb, ra.qb, S, D, N, M, C, G);
+                           ks, kp, qs, v, keep, ra.sa, ra.sb, ra.qb, S, D, N, M, C, G);
     }
     {
         StageTimer t("lap_range_scan", st);
@@ -534,27 +585,30 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
         const unsigned walk_blocks = (unsigned)((walk_waves + WPB - 1) / WPB);
         StageTimer t("lap_range_walk", st);
         hipLaunchKernelGGL((lap_range_walk<NV, RK>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
-                           ks, kp, qs, qp, v, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C), G);
+                           ks, kp, qs, qp, v, keep, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C),
+                           G);
     }
     return (int)hipGetLastError();
 }
 
 int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st) {
-    if (C <= WAVE) return laplace_walk_t<1, 64>(ks, kp, qs, qp, v, slab, uslab, P, D, N, M, C, ra, st);
-    return laplace_walk_t<2, 32>(ks, kp, qs, qp, v, slab, uslab, P, D, N, M, C, ra, st);
+                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
+                 hipStream_t st) {
+    if (C <= WAVE) return laplace_walk_t<1, 64>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
+    return laplace_walk_t<2, 32>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
 }
 
 // =================================================================================================================
 // Abs family
 // =================================================================================================================
 
-// Range summary: Wt = sum_t w_t, Bt = sum_t (k_last - k_t) w_t; slot C: Ut = sum_t u_t (ta), B1t = sum_t
-// (k_last - k_t) (tb).
+// Range summary: Wt = sum_t w_t, Bt = sum_t (k_last - k_t) w_t; slot C: Ut = sum_t u_t (ta; without u: the key
+// weight sum sum_t kw_t, i.e. the range's count of kept keys) and B1t = sum_t kw_t (k_last - k_t) (tb). kw_t is the key
+// weight (0 for masked keys); w_t and u_t are taken times kw_t.
 template <int NV, int RK, bool WANT_W, bool WANT_U>
 __global__ __launch_bounds__(WPB * WAVE)
 void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
-                    const float* __restrict__ w, const float* __restrict__ u,
+                    const float* __restrict__ w, const float* __restrict__ u, const uint8_t* __restrict__ keep,
                     float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
                     const int S, const int D, const int Ns, const int Mq, const int C, const int G,
                     const float qshift)
@@ -570,9 +624,8 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
     const float kl = kseg[li];
     const uint32_t pl = kp[(size_t)s * Ns + li];
     const float klast = kseg[base + nk - 1];
-    const bool real = l < nk;
-    const float kw = real ? 1.f : 0.f;                   // pad keys weigh 0
-    const float dl = real ? (klast - kl) : 0.f;
+    const float kw = key_weight(keep, p, Ns, pl, l < nk);   // pad and masked keys weigh 0
+    const float dl = kw * (klast - kl);
 
     float sw[NV], sb[NV];
 #pragma unroll
@@ -594,10 +647,12 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
         }
     }
     const float b1 = wave_sum(dl);
-    float u1 = 0.f;
+    float u1;
     if constexpr (WANT_U) {
         const float ur = u[(size_t)p * Ns + pl];
-        u1 = wave_sum(real ? ur : 0.f);
+        u1 = wave_sum(kw != 0.f ? ur : 0.f);
+    } else {
+        u1 = wave_sum(kw);
     }
 
     const int CS = range_stride(C);
@@ -636,10 +691,9 @@ void range_bounds_kernel(const float* __restrict__ ks, const float* __restrict__
     if (lane_id() == 0) qb[(size_t)s * G + g] = ub;
 }
 
-// Abs: entry prefix state of every range and the segment totals (row G). State (PW, B, cnt) with B relative to the
-// last key absorbed: at range g, B <- b_g + B + gap_g PW, PW <- PW + a_g, cnt <- cnt + n_g (slot C of B uses cnt in
-// place of PW; gap_g = klast_g - klast_{g-1}). A piece composes to  PW = PW_in + sum a,  B = B_in + B_local +
-// (sum of its gaps) PW_in.
+// Abs: entry prefix state of every range and the segment totals (row G). State (PW, B) with B relative to the last
+// key absorbed: at range g, B <- b_g + B + gap_g PW, PW <- PW + a_g for every slot, slot C included (gap_g = klast_g -
+// klast_{g-1}). A piece composes to  PW = PW_in + sum a,  B = B_in + B_local + (sum of its gaps) PW_in.
 template <int NV, int RK>
 __global__ __launch_bounds__(SCAN_W * WAVE)
 void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ ta,
@@ -658,8 +712,10 @@ void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
     auto hi_of = [&](int ww) { return min(G, ww * per + per); };
     const int glo = lo_of(w), ghi = hi_of(w);
 
-    // piece walk from (pw, bb, cnt); writes entry states when OUT; returns the sum of the piece's gaps
-    auto walk = [&](float (&pw)[NV + 1], float (&bb)[NV + 1], float& cnt, const bool out) {
+    // piece walk from (pw, bb); writes entry states when OUT; returns the sum of the piece's gaps. Slot NV (slot C
+    // of the rows) runs the same recurrence: its B state (the v == 1 channel) is weighted by its PW state, the count of
+    // kept keys so far (for the u-weighted walks that slot of B is not read).
+    auto walk = [&](float (&pw)[NV + 1], float (&bb)[NV + 1], const bool out) {
         float gsum = 0.f;
         for (int g0 = glo; g0 < ghi; g0 += SCAN_BATCH) {
             float a[SCAN_BATCH][NV + 1], b_[SCAN_BATCH][NV + 1], gap[SCAN_BATCH], unused;
@@ -678,20 +734,17 @@ void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
                     store_scan_row<NV>(B + (size_t)g * CS, C, bb);
                 }
 #pragma unroll
-                for (int j = 0; j < NV; ++j) { bb[j] = b_[b][j] + bb[j] + gap[b] * pw[j]; pw[j] += a[b][j]; }
-                bb[NV] = b_[b][NV] + bb[NV] + gap[b] * cnt;
-                pw[NV] += a[b][NV];
-                cnt += (float)min(RK, Ns - g * RK);
+                for (int j = 0; j <= NV; ++j) { bb[j] = b_[b][j] + bb[j] + gap[b] * pw[j]; pw[j] += a[b][j]; }
                 gsum += gap[b];
             }
         }
         return gsum;
     };
 
-    float pw[NV + 1], bb[NV + 1], cnt = 0.f;
+    float pw[NV + 1], bb[NV + 1];
 #pragma unroll
     for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
-    const float gs = walk(pw, bb, cnt, false);
+    const float gs = walk(pw, bb, false);
 #pragma unroll
     for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = pw[j]; agg[1][w][j][l] = bb[j]; }
     if (l == 0) span[w] = gs;
@@ -700,16 +753,12 @@ void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
     // incoming state: compose the aggregates of the pieces to the left (empty pieces: all zero)
 #pragma unroll
     for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
-    cnt = 0.f;
     for (int ww = 0; ww < w; ++ww) {
         const float sp = span[ww];
 #pragma unroll
-        for (int j = 0; j < NV; ++j) { bb[j] += agg[1][ww][j][l] + sp * pw[j]; pw[j] += agg[0][ww][j][l]; }
-        bb[NV] += agg[1][ww][NV][l] + sp * cnt;
-        pw[NV] += agg[0][ww][NV][l];
-        cnt += (float)(min(Ns, hi_of(ww) * RK) - min(Ns, lo_of(ww) * RK));
+        for (int j = 0; j <= NV; ++j) { bb[j] += agg[1][ww][j][l] + sp * pw[j]; pw[j] += agg[0][ww][j][l]; }
     }
-    walk(pw, bb, cnt, true);
+    walk(pw, bb, true);
     if (ghi == G && glo < G) {                            // the wave whose piece ends the segment writes the totals
         store_scan_row<NV>(A + (size_t)G * CS, C, pw);
         store_scan_row<NV>(B + (size_t)G * CS, C, bb);
@@ -748,6 +797,9 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     const bool has_prev = g > 0, has_next = g < G - 1;
     const float kbefore = has_prev ? kseg[base - 1] : 0.f;
     const float kmax = kseg[Ns - 1];
+    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+    const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
+    const float kw = (EMIT || ONES) ? key_weight(a.keep, p, Ns, kpseg[li], real) : 0.f;
 
     // weight rows of the range, lane = channel (pad keys and pad channels: zero); row indices by scalar loads
     float x[RK][NV];
@@ -777,6 +829,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
                 for (int j = 0; j < NV; ++j)
                     x[t][j] = (t < nk && l + WAVE * j < C) ? x[t][j] : 0.f;
         }
+        if (a.keep) mask_rows<NV, RK>(x, kw);
     }
     float ul = 0.f;
     if constexpr (X2) {
@@ -804,7 +857,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         Bt[j] = (ROW && ok) ? totB[cc] : 0.f;
     }
     float PU = 0.f, Ut = 0.f, B1 = 0.f, B1t = 0.f;
-    if constexpr (X2) { PU = rowA[C]; Ut = totA[C]; }
+    if constexpr (X2 || ONES) { PU = rowA[C]; Ut = totA[C]; }      // u sums (X2) / kept-key counts (ONES)
     if constexpr (ONES) { B1 = rowB[C]; B1t = totB[C]; }
     const float Nf = (float)Ns;
 
@@ -818,13 +871,15 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     const bool g_vec4 = DOT && (C % 4 == 0) && ((((uintptr_t)a.g) & 15) == 0);
 
     // Lane-parallel prefixes over the range's keys for the scalar emissions (exclusive prefix at rank t = inclusive
-    // value of lane t-1): b1 state  sum_{i<t} gap_i * (base + i)  and u prefix  sum_{i<t} u_i.
-    float gci = 0.f, uli = 0.f;
-    if constexpr (ONES) gci = wave_prefix_sum(gap * (float)(base + l));
+    // value of lane t-1): kept keys  sum_{i<t} kw_i,  b1 state  sum_{i<t} gap_i * (kept keys before key i)  and u
+    // prefix  sum_{i<t} u_i.
+    float kci = 0.f, gci = 0.f, uli = 0.f;
+    if constexpr (ONES) {
+        kci = wave_prefix_sum(kw);
+        gci = wave_prefix_sum(gap * (PU + (kci - kw)));
+    }
     if constexpr (X2) uli = wave_prefix_sum(ul);
 
-    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
-    const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
     const rsrc_t sr_ = ROW ? make_rsrc(a.slab + (size_t)s * Mq * a.CR, (uint32_t)((size_t)Mq * a.CR * 4))
                            : make_rsrc(nullptr, 0);
     const rsrc_t gr_ = DOT ? make_rsrc(a.g + (size_t)p * Mq * C, (uint32_t)((size_t)Mq * C * 4))
@@ -852,8 +907,10 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         }
         if constexpr (ONES) {
             const float gp = __shfl(gci, max(t - 1, 0), WAVE);
+            const float kp_ = __shfl(kci, max(t - 1, 0), WAVE);
             const float b1 = B1 + (t > 0 ? gp : 0.f);
-            if (act) useg[qb0 + l] = 2.f * (lq * cnt + b1) - B1t - qm * Nf;
+            const float wcnt = PU + (t > 0 ? kp_ : 0.f);  // kept keys below q
+            if (act) useg[qb0 + l] = 2.f * (lq * wcnt + b1) - B1t - qm * Ut;
         }
         if constexpr (EXTRA) {
             float e = 0.f;
@@ -973,13 +1030,16 @@ static int abs_prepare_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStre
         StageTimer t("abs_range_sums", st);
         if (mode & ABS_DOTX2)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, true>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G, a.qshift);
+                               a.ks, a.kp, a.qs, a.w, a.u, a.keep, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G,
+                               a.qshift);
         else if (mode == ABS_RANK)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, false, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G, a.qshift);
+                               a.ks, a.kp, a.qs, a.w, a.u, a.keep, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G,
+                               a.qshift);
         else
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G, a.qshift);
+                               a.ks, a.kp, a.qs, a.w, a.u, a.keep, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G,
+                               a.qshift);
     }
     {
         StageTimer t("abs_range_scan", st);

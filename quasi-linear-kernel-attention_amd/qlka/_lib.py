@@ -33,6 +33,7 @@ _SIGNATURES = {
     "qlka_direct_sgn": (_c_int, [ctypes.c_float] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr]),
     "qlka_layer_fwd_ws_bytes": (_c_size, [_c_int] * 6),
     "qlka_layer_fwd": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
+    "qlka_layer_fwd_masked": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_seg_sort_ws_bytes": (_c_size, [_c_int] * 2),
     "qlka_seg_sort": (_c_int, [_c_ptr] * 3 + [_c_int] * 2 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_merge_rank_ws_bytes": (_c_size, [_c_int] * 3),

@@ -6,6 +6,9 @@ Mirrors Experiments/kernel_attention/attention.py:
     n_pad the number of masked keys per p (0 or a (P,) / (P, 1) tensor); returns (P, S, C).
   * attention(q, k, v, kernel, tau, keep=None) is the additive-kernel branch of attention() (attention.py:95-126):
     (B, H, S, D) in and out, tau scaling, key mask.
+  * layer_forward(kernel, q, k, v, keep=...) applies a key mask inside the sums (qlka_layer_fwd_masked): k and v are
+    passed as they are, masked keys weigh 0, and no n_pad correction is needed. attention() takes this route for a
+    mask when no gradient is needed.
 
 Forward through one library call per layer: the op(s) and the normalising epilogue run on the GPU in one stream of
 kernels, and add_bump's three abs sums (q, q + 1, q - 1) share one sort of k and q and one set of key-range
@@ -46,23 +49,41 @@ def _n_pad(n_pad, P, device):
     return t.reshape(P).contiguous()
 
 
-def layer_forward(kernel, q, k, v, n_pad=0):
-    """One fused forward of `kernel` in ("add_laplace", "add_riesz", "add_bump"); returns (P, M, C). No autograd."""
+def _keep(keep, P, N, device):
+    """(P, N) key mask (bool or 0/1) as contiguous bytes, nonzero = kept."""
+    if keep.shape != (P, N):
+        raise RuntimeError(f"keep must be (P, N) = ({P}, {N}), got {tuple(keep.shape)}")
+    if keep.device != device:
+        raise RuntimeError("keep must be on the device of q, k and v")
+    return (keep != 0).to(torch.uint8).contiguous()
+
+
+def layer_forward(kernel, q, k, v, n_pad=0, keep=None):
+    """One fused forward of `kernel` in ("add_laplace", "add_riesz", "add_bump"); returns (P, M, C). No autograd.
+
+    keep=None: the reference's composition, k and v already multiplied by the key mask and n_pad the count of masked
+    keys per p. keep (P, N): the mask applied inside the sums (k and v unmasked, n_pad unused)."""
     if kernel not in KINDS:
         raise ValueError(f"unknown additive kernel {kernel!r}")
     _check(q, k, v)
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     P, D, M = q.shape
     N, C = k.shape[2], v.shape[2]
-    npad = _n_pad(n_pad, P, q.device)
     out = torch.empty(P, M, C, dtype=torch.float32, device=q.device)
     lib = _lib.load()
     kind = KINDS[kernel]
     with torch.cuda.device(q.device):
         nbytes = lib.qlka_layer_fwd_ws_bytes(kind, P, D, N, M, C)
         ws = _lib.workspace(nbytes, q.device)
-        _lib.check(lib.qlka_layer_fwd(kind, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(npad), _lib.ptr(out),
-                                      P, D, N, M, C, _lib.ptr(ws), nbytes, _lib.stream_of(q.device)))
+        if keep is None:
+            npad = _n_pad(n_pad, P, q.device)
+            rc = lib.qlka_layer_fwd(kind, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(npad), _lib.ptr(out),
+                                    P, D, N, M, C, _lib.ptr(ws), nbytes, _lib.stream_of(q.device))
+        else:
+            kb = _keep(keep, P, N, q.device)
+            rc = lib.qlka_layer_fwd_masked(kind, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(kb), _lib.ptr(out),
+                                           P, D, N, M, C, _lib.ptr(ws), nbytes, _lib.stream_of(q.device))
+        _lib.check(rc)
     return out
 
 
@@ -122,7 +143,8 @@ LAYERS = {"add_laplace": add_laplace, "add_riesz": add_riesz, "add_bump": add_bu
 def attention(q, k, v, kernel, tau, keep=None):
     """The additive-kernel branch of attention() (attention.py:95-126): q, k, v (B, H, S, D) fp32 -> (B, H, S, D).
 
-    keep (B, S) marks the real keys (bool or 0/1); masked keys become k = 0, v = 0 and are removed from the row sums.
+    keep (B, S) marks the real keys (bool or 0/1). Without a gradient the mask is applied inside the fused layer's
+    sums; with one, masked keys become k = 0, v = 0 and leave the row sums through n_pad, as in the reference.
     """
     if kernel not in LAYERS:
         raise ValueError(f"attention: kernel {kernel!r} is not one of {sorted(LAYERS)}")
@@ -134,6 +156,8 @@ def attention(q, k, v, kernel, tau, keep=None):
     v = v.reshape(P, S, D)
     keep = None if keep is None else keep.repeat_interleave(H, dim=0)       # (P, S)
     q, k, n_pad = q / tau, k / tau, 0
+    if keep is not None and not _needs_grad(q, k, v):
+        return layer_forward(kernel, q, k, v, keep=keep).view(B, H, S, D)
     if keep is not None:
         k, v = k * keep[:, None, :], v * keep[:, :, None]
         n_pad = S - keep.sum(dim=1, keepdim=True)

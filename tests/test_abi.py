@@ -102,3 +102,7 @@ def test_layer_workspace_and_validation(lib):
     assert rc == 2 and "workspace too small" in lib.qlka_last_error().decode()
     rc = lib.qlka_layer_fwd(1, dummy, dummy, dummy, None, None, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
     assert rc == 1 and "non-null" in lib.qlka_last_error().decode()
+    rc = lib.qlka_layer_fwd_masked(0, dummy, dummy, dummy, None, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
+    assert rc == 1 and "keep must be non-null" in lib.qlka_last_error().decode()
+    rc = lib.qlka_layer_fwd_masked(5, dummy, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
+    assert rc == 1 and "kind must be" in lib.qlka_last_error().decode()

@@ -6,6 +6,9 @@
   key mask (attention.py:119-124), at sizes where the matrix is cheap.
 * The gradient path of add_riesz / add_bump (the reference's formulas over the differentiable op) and the
   forward-only add_laplace.
+* The in-kernel key mask (qlka_layer_fwd_masked): against the reference's composition over zeroed keys with the
+  n_pad corrections, evaluated in float64 (attention.py:122-124); bit-equal to the unmasked layer when nothing is
+  masked; exactly zero rows for a p whose keys are all masked.
 """
 import numpy as np
 import pytest
@@ -126,3 +129,92 @@ def test_layer_validation(dev):
         layers.layer_forward("add_riesz", q.double(), k, v)
     with pytest.raises(RuntimeError, match="CUDA"):
         layers.layer_forward("add_riesz", q.cpu(), k, v)
+
+
+MASK_SHAPES = [  # P, D, N, M, C
+    (3, 3, 40, 40, 8),
+    (3, 4, 300, 400, 5),        # M != N, odd C, partial last key range. M >= N: add_riesz's den counts keys as
+                                # S = M (attention.py:78), so for M < N - n_pad it is a difference of large terms
+    (3, 4, 1000, 1000, 64),
+    (2, 2, 300, 300, 128),      # two channel slots per lane
+]
+
+
+def _mask(P, N, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    keep = torch.rand(P, N, generator=g) < 0.7
+    keep[0, N // 3: N // 3 + min(N // 2, 150)] = False     # a masked run over whole key ranges
+    if P > 2:
+        keep[2] = False                                    # every key masked
+    return keep.to(dev)
+
+
+def _reference_masked(kernel, q, k, v, keep):
+    """attention.py:122-124 then attention.py:67-92, in float64 on the CPU with dense ops (kernels.py:73,81)."""
+    q64, k64, v64 = (t.detach().cpu().double() for t in (q, k, v))
+    kp = keep.cpu().double()
+    k64, v64 = k64 * kp[:, None, :], v64 * kp[:, :, None]
+    n_pad = k.shape[2] - kp.sum(dim=1, keepdim=True)
+
+    def abs_full(a, b, c):
+        return dense.dense_abs_sum(a, b, c)
+
+    def lap(a, b, c):
+        return dense.dense_laplace_sum(a, b, c)
+
+    if kernel == "add_laplace":
+        return dense.add_laplace_layer(q64, k64, v64, n_pad, lap)
+    if kernel == "add_riesz":
+        return dense.add_riesz_layer(q64, k64, v64, n_pad, abs_full)
+    return dense.add_bump_layer(q64, k64, v64, n_pad, abs_full)
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+@pytest.mark.parametrize("shape", MASK_SHAPES)
+def test_masked_layer_matches_reference_composition(dev, kernel, shape):
+    from qlka import layers
+    P, D, N, M, C = shape
+    print(f"masked {kernel} {shape}", flush=True)
+    q, k, v = _inputs(P, D, N, M, C, seed=sum(shape) + 3, dev=dev, scale=0.7)
+    keep = _mask(P, N, seed=sum(shape), dev=dev)
+    got = layers.layer_forward(kernel, q, k, v, keep=keep).cpu().double()
+    want = _reference_masked(kernel, q, k, v, keep)
+    assert got.shape == (P, M, C)
+    np.testing.assert_allclose(got.numpy(), want.numpy(), rtol=1e-4, atol=1e-5, err_msg=f"{kernel} {shape}")
+    if P > 2:
+        assert torch.all(got[2] == 0), "a p with every key masked gives zero rows"
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_masked_layer_without_masked_keys_is_the_unmasked_layer(dev, kernel):
+    from qlka import layers
+    P, D, N, M, C = 2, 3, 500, 400, 16
+    q, k, v = _inputs(P, D, N, M, C, seed=77, dev=dev, scale=0.7)
+    keep = torch.ones(P, N, dtype=torch.bool, device=dev)
+    got = layers.layer_forward(kernel, q, k, v, keep=keep)
+    want = layers.layer_forward(kernel, q, k, v)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("kernel", KERNELS)
+def test_masked_layer_vs_reference_route_on_gpu(dev, kernel):
+    # the reference's own GPU route (zeroed keys through the ops, n_pad epilogue) agrees with the in-kernel mask
+    from qlka import layers
+    P, D, N, M, C = 3, 4, 700, 700, 32
+    q, k, v = _inputs(P, D, N, M, C, seed=5, dev=dev, scale=0.7)
+    keep = _mask(P, N, seed=6, dev=dev)
+    keep[2, :5] = True                                     # keep the all-masked p off this comparison's den clamp
+    kf = keep.float()
+    n_pad = N - kf.sum(dim=1, keepdim=True)
+    route = layers.layer_forward(kernel, q, k * kf[:, None, :], v * kf[:, :, None], n_pad)
+    got = layers.layer_forward(kernel, q, k, v, keep=keep)
+    want = _reference_masked(kernel, q, k, v, keep)
+    np.testing.assert_allclose(got.cpu().double().numpy(), want.numpy(), rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(route.cpu().double().numpy(), want.numpy(), rtol=1e-3, atol=1e-4)
+
+
+def test_masked_layer_validation(dev):
+    from qlka import layers
+    q, k, v = _inputs(2, 2, 16, 16, 4, seed=1, dev=dev)
+    with pytest.raises(RuntimeError, match="keep must be"):
+        layers.layer_forward("add_riesz", q, k, v, keep=torch.ones(2, 15, dtype=torch.bool, device=dev))

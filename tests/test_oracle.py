@@ -293,3 +293,30 @@ def test_backward_tie_convention():
     (q0, _, _), _ = brute.abs_backward(q, k, v, g_w, None, tie=0.0)
     sg, _ = brute.sgn_sum(q, k, v, g_w, tie=0.0)
     np.testing.assert_allclose(sg, -q0, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------------------------------------------- key mask
+@pytest.mark.parametrize("op", ["abs", "laplace"])
+def test_key_mask_matches_reference_composition(op):
+    # The in-kernel mask (masked keys dropped from every sum) against the reference's own route to the same value
+    # (attention.py:122-124, weighted_laplace_sum/__init__.py:12): zero k and v at masked keys, sum over all keys, then
+    # remove from u what each zeroed key adds, n_pad * sum_d f(q_d - 0). A mask applied to the wrong axis, a dropped
+    # n_pad term or a mask that also touched v == 1 sums differently fails here.
+    P, D, N, M, C = 3, 4, 23, 11, 5
+    q, k, v = _rand(P, D, N, M, C, seed=31)
+    keep = np.random.default_rng(32).random((P, N)) < 0.6
+    keep[1] = False                       # a p with every key masked
+    keep[2] = True                        # a p with none masked
+    fn = brute.abs_sum if op == "abs" else brute.laplace_sum
+    f = np.abs if op == "abs" else (lambda x: np.exp(-np.abs(x)))
+    w, u, _ = fn(q, k, v, keep=keep)
+    kz = k * keep[:, None, :]
+    vz = v * keep[:, :, None]
+    wz, uz, _ = fn(q, kz, vz)
+    n_pad = (N - keep.sum(axis=1)).astype(np.float64)
+    np.testing.assert_allclose(w, wz, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(u, uz - n_pad[:, None] * f(q.astype(np.float64)).sum(axis=1), rtol=1e-12, atol=1e-9)
+    assert np.all(w[1] == 0) and np.all(u[1] == 0)
+    w2, u2, _ = fn(q, k, v)
+    np.testing.assert_array_equal(w[2], w2[2])
+    np.testing.assert_array_equal(u[2], u2[2])
