@@ -200,11 +200,23 @@ def main():
     # composition (separate op calls + torch epilogue, attention.py:67-92).
     from qlka import layers
     layer_ms = {}
+    # Padded batch: the last 10% of the keys of every p masked (attention.py:122-124). In-kernel mask (one masked
+    # layer call on the raw k, v) vs the reference's route (k * keep, v * keep, the ops, the n_pad epilogue).
+    keep = torch.ones(P, N, dtype=torch.bool, device=dev)
+    keep[:, N - N // 10:] = False
+    kf = keep.float()
+    n_pad = N - kf.sum(dim=1, keepdim=True)
+
+    def reference_masked(kern):
+        return layers.unfused(kern, q, k * kf[:, None, :], v * kf[:, :, None], n_pad)
+
     with torch.no_grad():
         for kern in layers.KINDS:
             layer_ms[kern] = {
                 "fused": round(op_time(lambda: layers.layer_forward(kern, q, k, v)), 4),
                 "unfused": round(op_time(lambda: layers.unfused(kern, q, k, v)), 4),
+                "masked_in_kernel": round(op_time(lambda: layers.layer_forward(kern, q, k, v, keep=keep)), 4),
+                "masked_reference_route": round(op_time(lambda: reference_masked(kern)), 4),
             }
 
     out = {

@@ -369,7 +369,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
         a.out_dot = nullptr; a.out_rank = nullptr;
         a.sign = 1.f; a.P = P; a.D = D; a.C = C; a.qshift = 0.f;
-        const int mode = ABS_ROW | ABS_ONES;
+        const int mode = ABS_ROW | ABS_ONES | (keep ? ABS_KEEP : 0);
         // one sort of k and q, one set of range summaries and one scan serve every query shift: q + s has the sorted
         // order of q, and the key side does not depend on the queries
         e = abs_prepare(a, mode, w.ra, st);

@@ -75,6 +75,7 @@ enum AbsMode : int {
     ABS_DOTX1 = 8,    //   ... + uq[p, m] * (2 rank - Ns)
     ABS_DOTX2 = 16,   //   ... + sum_n s(q_m - k_n) u_n
     ABS_RANK  = 32,   // out_rank[s, m]    = #{n : k_n < q_m}                 (store)
+    ABS_KEEP  = 64,   // with ABS_ROW | ABS_ONES: keys masked by a.keep weigh 0 (a.keep non-null exactly with this bit)
 };
 
 struct AbsWalkArgs {

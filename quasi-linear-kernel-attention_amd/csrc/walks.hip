@@ -350,7 +350,7 @@ struct QueryBlocks {
 
 constexpr int RPW = 1;             // consecutive key ranges walked by one wave of a walk kernel
 
-template <int NV, int RK>
+template <int NV, int RK, bool KEEP>
 __global__ __launch_bounds__(WPB * WAVE)
 void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
                     const uint32_t* __restrict__ qp, const float* __restrict__ v, const uint8_t* __restrict__ keep,
@@ -386,10 +386,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
         const bool has_prev = g > 0, has_next = g < G - 1;
         const float kbefore = has_prev ? kseg[base - 1] : 0.f;
         const float kafter  = has_next ? kseg[base + RK] : 0.f;
-        const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
-        const int q1 = has_next ? qb[(size_t)s * G + g] : M;
-        QueryBlocks qbk(qseg, qpseg, q0, q1);
-        const float kw = key_weight(keep, p, N, kpseg[li], real);
+        const float kw = KEEP ? key_weight(keep, p, N, kpseg[li], real) : (real ? 1.f : 0.f);
 
         // value rows of the range, lane = channel (pad keys and pad channels: zero). The row indices are read with
         // scalar loads straight into SGPRs (the buffer offset of each row gather).
@@ -411,6 +408,11 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
                     x[t][j] = buf_load(vr, min(l + WAVE * j, C - 1) * 4, rowoff);
             }
         }
+        // owned queries [q0, q1): their bounds are scalar loads issued after the gathers (an earlier scalar load would
+        // hold back the gathers, which wait for the row offsets' scalar loads), then the first two query blocks
+        const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+        const int q1 = has_next ? qb[(size_t)s * G + g] : M;
+        QueryBlocks qbk(qseg, qpseg, q0, q1);
         if (nk < RK || C < RS) {                          // partial last range or pad channels (uniform branch)
 #pragma unroll
             for (int t = 0; t < RK; ++t)
@@ -418,7 +420,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
                 for (int j = 0; j < NV; ++j)
                     x[t][j] = (t < nk && l + WAVE * j < C) ? x[t][j] : 0.f;
         }
-        if (keep) mask_rows<NV, RK>(x, kw);
+        if constexpr (KEEP) mask_rows<NV, RK>(x, kw);
 
         const float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
         const float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
@@ -584,9 +586,14 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
         const long walk_waves = (long)S * ((G + RPW - 1) / RPW);
         const unsigned walk_blocks = (unsigned)((walk_waves + WPB - 1) / WPB);
         StageTimer t("lap_range_walk", st);
-        hipLaunchKernelGGL((lap_range_walk<NV, RK>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
-                           ks, kp, qs, qp, v, keep, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C),
-                           G);
+        if (keep)
+            hipLaunchKernelGGL((lap_range_walk<NV, RK, true>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
+                               ks, kp, qs, qp, v, keep, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C),
+                               G);
+        else
+            hipLaunchKernelGGL((lap_range_walk<NV, RK, false>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
+                               ks, kp, qs, qp, v, nullptr, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C,
+                               slab_stride(C), G);
     }
     return (int)hipGetLastError();
 }
@@ -771,7 +778,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
                     const int* __restrict__ qb, const int G)
 {
     constexpr bool ROW = MODE & ABS_ROW, ONES = MODE & ABS_ONES, DOT = MODE & ABS_DOT;
-    constexpr bool X1 = MODE & ABS_DOTX1, X2 = MODE & ABS_DOTX2, RANK = MODE & ABS_RANK;
+    constexpr bool X1 = MODE & ABS_DOTX1, X2 = MODE & ABS_DOTX2, RANK = MODE & ABS_RANK, KEEP = MODE & ABS_KEEP;
     constexpr bool EMIT = ROW || DOT;                     // rows gathered, states staged in LDS, emission
     constexpr bool EXTRA = X1 || X2;
     using Lds = WalkLds<NV, RK>;
@@ -797,9 +804,8 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     const bool has_prev = g > 0, has_next = g < G - 1;
     const float kbefore = has_prev ? kseg[base - 1] : 0.f;
     const float kmax = kseg[Ns - 1];
-    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
-    const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
-    const float kw = (EMIT || ONES) ? key_weight(a.keep, p, Ns, kpseg[li], real) : 0.f;
+    float kw = real ? 1.f : 0.f;                         // key weight (KEEP: 0 for masked keys)
+    if constexpr (KEEP) kw = key_weight(a.keep, p, Ns, kpseg[li], real);
 
     // weight rows of the range, lane = channel (pad keys and pad channels: zero); row indices by scalar loads
     float x[RK][NV];
@@ -829,7 +835,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
                 for (int j = 0; j < NV; ++j)
                     x[t][j] = (t < nk && l + WAVE * j < C) ? x[t][j] : 0.f;
         }
-        if (a.keep) mask_rows<NV, RK>(x, kw);
+        if constexpr (KEEP) mask_rows<NV, RK>(x, kw);
     }
     float ul = 0.f;
     if constexpr (X2) {
@@ -857,7 +863,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         Bt[j] = (ROW && ok) ? totB[cc] : 0.f;
     }
     float PU = 0.f, Ut = 0.f, B1 = 0.f, B1t = 0.f;
-    if constexpr (X2 || ONES) { PU = rowA[C]; Ut = totA[C]; }      // u sums (X2) / kept-key counts (ONES)
+    if constexpr (X2 || (ONES && KEEP)) { PU = rowA[C]; Ut = totA[C]; }   // u sums (X2) / kept-key counts (KEEP)
     if constexpr (ONES) { B1 = rowB[C]; B1t = totB[C]; }
     const float Nf = (float)Ns;
 
@@ -871,15 +877,19 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     const bool g_vec4 = DOT && (C % 4 == 0) && ((((uintptr_t)a.g) & 15) == 0);
 
     // Lane-parallel prefixes over the range's keys for the scalar emissions (exclusive prefix at rank t = inclusive
-    // value of lane t-1): kept keys  sum_{i<t} kw_i,  b1 state  sum_{i<t} gap_i * (kept keys before key i)  and u
-    // prefix  sum_{i<t} u_i.
+    // value of lane t-1): b1 state  sum_{i<t} gap_i * (keys before key i), u prefix  sum_{i<t} u_i and, with a key
+    // mask, kept keys  sum_{i<t} kw_i  (the key counts then count kept keys only, from the scan's count PU).
     float kci = 0.f, gci = 0.f, uli = 0.f;
-    if constexpr (ONES) {
+    if constexpr (ONES && KEEP) {
         kci = wave_prefix_sum(kw);
         gci = wave_prefix_sum(gap * (PU + (kci - kw)));
+    } else if constexpr (ONES) {
+        gci = wave_prefix_sum(gap * (float)(base + l));
     }
     if constexpr (X2) uli = wave_prefix_sum(ul);
 
+    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+    const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
     const rsrc_t sr_ = ROW ? make_rsrc(a.slab + (size_t)s * Mq * a.CR, (uint32_t)((size_t)Mq * a.CR * 4))
                            : make_rsrc(nullptr, 0);
     const rsrc_t gr_ = DOT ? make_rsrc(a.g + (size_t)p * Mq * C, (uint32_t)((size_t)Mq * C * 4))
@@ -907,10 +917,14 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         }
         if constexpr (ONES) {
             const float gp = __shfl(gci, max(t - 1, 0), WAVE);
-            const float kp_ = __shfl(kci, max(t - 1, 0), WAVE);
             const float b1 = B1 + (t > 0 ? gp : 0.f);
-            const float wcnt = PU + (t > 0 ? kp_ : 0.f);  // kept keys below q
-            if (act) useg[qb0 + l] = 2.f * (lq * wcnt + b1) - B1t - qm * Ut;
+            float below = cnt, all = Nf;                  // (kept) keys below q, all (kept) keys
+            if constexpr (KEEP) {
+                const float kp_ = __shfl(kci, max(t - 1, 0), WAVE);
+                below = PU + (t > 0 ? kp_ : 0.f);
+                all = Ut;
+            }
+            if (act) useg[qb0 + l] = 2.f * (lq * below + b1) - B1t - qm * all;
         }
         if constexpr (EXTRA) {
             float e = 0.f;
@@ -1052,9 +1066,12 @@ static int abs_prepare_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStre
 template <int NV, int RK>
 static int abs_emit_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
     const int G = (a.Ns + RK - 1) / RK;
+    if (((mode & ABS_KEEP) != 0) != (a.keep != nullptr)) return (int)hipErrorInvalidValue;   // sums and walk agree
     switch (mode) {
         case ABS_ROW:                         launch_abs_walk<NV, RK, ABS_ROW>(a, ra, G, st); break;
         case ABS_ROW | ABS_ONES:              launch_abs_walk<NV, RK, ABS_ROW | ABS_ONES>(a, ra, G, st); break;
+        case ABS_ROW | ABS_ONES | ABS_KEEP:   launch_abs_walk<NV, RK, ABS_ROW | ABS_ONES | ABS_KEEP>(a, ra, G, st);
+                                              break;
         case ABS_DOT:                         launch_abs_walk<NV, RK, ABS_DOT>(a, ra, G, st); break;
         case ABS_DOT | ABS_DOTX1:             launch_abs_walk<NV, RK, ABS_DOT | ABS_DOTX1>(a, ra, G, st); break;
         case ABS_ROW | ABS_DOT:               launch_abs_walk<NV, RK, ABS_ROW | ABS_DOT>(a, ra, G, st); break;
