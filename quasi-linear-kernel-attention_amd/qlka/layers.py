@@ -23,6 +23,7 @@ from . import _lib
 
 CLAMP = 1e-6    # attention.py:20
 EPS = 1e-3      # kernels.py:9
+KEOPS_BELOW = 256   # attention.py:22: the reference's abs sums take backend "keops" below this many queries
 KINDS = {"add_laplace": 0, "add_riesz": 1, "add_bump": 2}
 
 
@@ -100,9 +101,14 @@ def add_laplace(q, k, v, n_pad=0):
 
 def unfused(kernel, q, k, v, n_pad=0):
     """The reference's own composition (attention.py:67-92): separate op calls and a torch epilogue. Differentiable
-    for add_riesz / add_bump through weighted_abs_sum_full's autograd."""
-    from weighted_abs_sum import weighted_abs_sum_full
+    for add_riesz / add_bump through weighted_abs_sum_full's autograd, on the backend the reference's _abs_sum picks
+    (attention.py:60-63: "keops" below KEOPS_BELOW queries, so a gradient tie counts 0 there, else "cuda")."""
+    from weighted_abs_sum import weighted_abs_sum_full as _full
     from weighted_laplace_sum import weighted_laplace_sum
+
+    def weighted_abs_sum_full(a, b, c):
+        return _full(a, b, c, backend="keops" if a.shape[2] < KEOPS_BELOW else "cuda")
+
     if kernel == "add_laplace":
         out_w, out_u = weighted_laplace_sum(q.contiguous(), k.contiguous(), v.contiguous())
         den = out_u - n_pad * (-q.abs()).exp().sum(dim=1)
