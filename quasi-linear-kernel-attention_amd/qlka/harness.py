@@ -4,7 +4,8 @@ The synthetic stand-in for the timing of Experiments/text_transformer/pareto.py:
 padded to seq_len, CUDA events around the model forward, GPU milliseconds summed over the batches, divided by the
 number of documents, pareto.py:101). The LoCo documents and the trained nomic weights need downloads, so the encoder
 is NomicBertModel at its default configuration (hidden 768, 12 heads of 64, 12 layers, SwiGLU 3072, rotary) with
-random weights, fed random token ids. Each document's real length is drawn in [seq_len / 2, seq_len]; the padding
+max_position_embeddings raised to the sequence length (nomic-embed-text-v1 itself has 8192) and random weights, fed
+random token ids. Each document's real length is drawn in [seq_len / 2, seq_len]; the padding
 becomes the key mask of every attention layer (inside the sums for the additive kernels, qlka_layer_fwd_masked).
 pareto.py's per-sequence RoPE base (an embedding-quality fix) does not change the work and is left out.
 
@@ -21,12 +22,13 @@ import torch
 from . import modules
 
 
-def build_encoder(layers, kernel, device, hidden=768, heads=12, intermediate=3072, seed=0):
-    """NomicBertModel (SDPA masks) with random weights and every attention layer swapped for `kernel`."""
+def build_encoder(layers, kernel, device, hidden=768, heads=12, intermediate=3072, seed=0, max_positions=2048):
+    """NomicBertModel (SDPA masks) with random weights and every attention layer swapped for `kernel`. The model
+    gathers its token-type buffer at the position ids, so it takes at most max_positions tokens."""
     from transformers import NomicBertConfig, NomicBertModel
     torch.manual_seed(seed)
     cfg = NomicBertConfig(num_hidden_layers=layers, hidden_size=hidden, num_attention_heads=heads,
-                          intermediate_size=intermediate)
+                          intermediate_size=intermediate, max_position_embeddings=max(2048, max_positions))
     model = NomicBertModel._from_config(cfg, attn_implementation="sdpa").to(device).eval()
     return modules.use_kernel_attention(model, kernel)
 
@@ -61,7 +63,9 @@ def encode_time(model, batches):
 
 def run(kernel="add_bump", seq_len=8192, batch_size=16, docs=32, layers=12, device="cuda:0", **model_kw):
     device = torch.device(device)
-    model = build_encoder(layers, kernel, device, **model_kw)
+    model = build_encoder(layers, kernel, device, max_positions=seq_len, **model_kw)
+    if seq_len > model.config.max_position_embeddings:
+        raise ValueError(f"seq_len {seq_len} exceeds the encoder's {model.config.max_position_embeddings} positions")
     vocab = model.config.vocab_size
     # one warmup batch at the timed shape (allocator and workspace sizes settle)
     encode_time(model, synthetic_batches(min(docs, batch_size), batch_size, seq_len, vocab, device, seed=1))

@@ -66,3 +66,20 @@ def test_unsupported_kernels_and_impl():
         modules.attention(q, q, q, "add_bump", 1.5, impl="naive")
     with pytest.raises(AssertionError):
         modules.attention(q, q, q, "add_bump", 1.5, impl="fast")
+
+
+def test_harness_encoder_takes_its_sequence_length():
+    # The encoder gathers its token-type buffer at the position ids (NomicBertEmbeddings), so a sequence longer than
+    # max_position_embeddings indexes past that buffer: on the CPU torch raises, on the GPU the gather reads out of
+    # bounds. The harness sizes the encoder to its seq_len.
+    from qlka import harness
+    S = 2100
+    ids = torch.randint(1, 1000, (1, S))
+    short = harness.build_encoder(1, "softmax", "cpu", hidden=32, heads=2, intermediate=64)
+    with pytest.raises((IndexError, RuntimeError)):
+        with torch.no_grad():
+            short(input_ids=ids)
+    model = harness.build_encoder(1, "softmax", "cpu", hidden=32, heads=2, intermediate=64, max_positions=S)
+    assert model.config.max_position_embeddings == S
+    with torch.no_grad():
+        assert model(input_ids=ids).last_hidden_state.shape == (1, S, 32)
