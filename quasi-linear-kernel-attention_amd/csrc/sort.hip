@@ -61,16 +61,15 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
         for (int i = lane; i < 256; i += WAVE) hist[wave * 256 + i] = 0u;
         __syncthreads();                                  // every scatter done, every row cleared
 
-        uint32_t key[ITEMS], pk[ITEMS];                   // pk = run index << 16 | offset within the wave's digit
+        // pk = run index << 16 | offset within the wave's digit. The keys are read again after the ranking (skey is
+        // not written until the scatter), so the ranking holds only pk and one key at a time in registers.
+        uint32_t key[ITEMS], pk[ITEMS];
         const int wbase = wave * WAVE * ITEMS;
 #pragma unroll
-        for (int r = 0; r < ITEMS; ++r) {                 // item (wave, r, lane) sits at wbase + r*64 + lane
-            key[r] = skey[wbase + r * WAVE + lane];
-            pk[r]  = sidx[wbase + r * WAVE + lane] << 16;
-        }
+        for (int r = 0; r < ITEMS; ++r) pk[r] = sidx[wbase + r * WAVE + lane] << 16;   // item (wave, r, lane)
 #pragma unroll
         for (int r = 0; r < ITEMS; ++r) {
-            const uint32_t dig = (key[r] >> shift) & 255u;
+            const uint32_t dig = (skey[wbase + r * WAVE + lane] >> shift) & 255u;
             uint64_t peers = ~0ull;
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
@@ -84,7 +83,9 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
             if (below == 0) hist[wave * 256 + dig] = old + cnt;
             pk[r] |= old + below;
         }
-        __syncthreads();                                  // all per-wave digit counts final; all items in regs
+        __syncthreads();                                  // all per-wave digit counts final
+#pragma unroll
+        for (int r = 0; r < ITEMS; ++r) key[r] = skey[wbase + r * WAVE + lane];
 
         for (int d = tid; d < 256; d += THREADS) {        // exclusive over waves (digit-major order)
             uint32_t run_sum = 0;
