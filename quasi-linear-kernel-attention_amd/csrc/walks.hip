@@ -351,7 +351,7 @@ struct QueryBlocks {
 constexpr int RPW = 1;             // consecutive key ranges walked by one wave of a walk kernel
 
 template <int NV, int RK, bool KEEP>
-__global__ __launch_bounds__(WPB * WAVE)
+__global__ __launch_bounds__(WPB * WAVE) __attribute__((amdgpu_waves_per_eu(KEEP && NV == 1 ? 4 : 1)))
 void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
                     const uint32_t* __restrict__ qp, const float* __restrict__ v, const uint8_t* __restrict__ keep,
                     const float* __restrict__ ta, const float* __restrict__ tb, const int* __restrict__ qb,
