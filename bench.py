@@ -149,8 +149,8 @@ def main():
     torch.cuda.synchronize()
     ms_total = start.elapsed_time(stop)
     stages = {}
-    for name in ("lds_radix_sort", "merge_runs", "fill_zero", "lap_range_sums", "lap_range_scan", "lap_range_walk",
-                 "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_gather", "slab_reduce"):
+    for name in ("lds_radix_sort", "merge_runs", "query_bounds", "fill_zero", "lap_range_sums", "lap_range_scan",
+                 "lap_range_walk", "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_gather", "slab_reduce"):
         ms, cnt = _lib.stage_time(name)
         if cnt:
             stages[name] = {"ms_total": ms, "launches": cnt, "ms_per_launch": ms / cnt}

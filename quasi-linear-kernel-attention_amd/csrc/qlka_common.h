@@ -91,57 +91,6 @@ __device__ __forceinline__ float wave_prefix_sum(float x) {
     return x;
 }
 
-// Number of elements of the ascending array a[0, n) that are <= x (std::upper_bound), found by the whole wave with a
-// 64-ary search: every round each lane probes one of 64 evenly spaced split points, so n = 2^17 needs 3 rounds of
-// dependent loads instead of 17. The predicate a[i] <= x is monotone, so the probes that pass form a lane prefix.
-// Must be called by all 64 lanes with the same (a, n, x).
-// With a shift, the array searched is a[i] + shift (fp32 addition is monotone, so it is still ascending).
-__device__ __forceinline__ int wave_upper_bound_from(const float* __restrict__ a, int lo, int hi, float x,
-                                                     float shift = 0.f) {
-    const int l = lane_id();
-    while (lo < hi) {                                     // answer in [lo, hi]
-        const int span   = hi - lo;
-        const int stride = (span + WAVE - 1) / WAVE;      // >= 1
-        const int idx    = lo + (l + 1) * stride - 1;     // last element of lane l's block
-        const bool ok    = (idx < hi) && (a[idx] + shift <= x);
-        const int c      = __popcll(__ballot(ok));        // blocks entirely <= x
-        const int nlo    = lo + c * stride;
-        const int nhi    = min(hi, nlo + stride - 1);
-        if (stride == 1) { lo = hi = nlo; break; }
-        lo = nlo; hi = nhi;
-    }
-    return lo;
-}
-__device__ __forceinline__ int wave_upper_bound(const float* __restrict__ a, int n, float x) {
-    return wave_upper_bound_from(a, 0, n, x);
-}
-
-// The first round of an upper bound split in two so that a caller can issue other loads between them: probe()
-// loads the last element of each of 256 blocks of stride ceil(n / 256) (4 per lane), finish() counts the blocks
-// entirely <= x and continues with the 64-ary rounds inside the first block that is not.
-struct UpperBoundProbe {
-    int stride;
-    float v[4];
-    bool in[4];
-    __device__ __forceinline__ void probe(const float* __restrict__ a, int n) {
-        stride = (n + 4 * WAVE - 1) / (4 * WAVE);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int idx = (lane_id() + WAVE * r + 1) * stride - 1;
-            in[r] = idx < n;
-            v[r] = (n > 0) ? a[min(idx, n - 1)] : 0.f;    // clamped, unconditional for n > 0: all four in flight
-        }
-    }
-    __device__ __forceinline__ int finish(const float* __restrict__ a, int n, float x, float shift = 0.f) const {
-        if (n <= 0) return 0;
-        int c = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) c += __popcll(__ballot(in[r] && v[r] + shift <= x));   // monotone in block
-        const int lo = c * stride;
-        return wave_upper_bound_from(a, lo, min(n, lo + stride - 1), x, shift);
-    }
-};
-
 // Workgroups are dispatched to the 8 XCDs round-robin (block b runs on XCD b % 8), each XCD with its own L2. This
 // maps the hardware block id to a logical work id such that every XCD processes one contiguous slice of the logical
 // order, so work items that share data (the segments of one p share its v rows) run on the same XCD and L2.

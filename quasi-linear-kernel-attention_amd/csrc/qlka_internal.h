@@ -105,6 +105,10 @@ int abs_prepare(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
 int abs_emit(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
 // query boundaries of every key range for queries shifted by qshift (what abs_prepare writes to ra.qb for a.qshift)
 int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st);
+// qb[s, g] = #{i : qs[s, i] + qshift <= largest key of range g} over the sorted keys ks (S segments of Ns) and sorted
+// queries qs (S segments of Mq), ranges of range_keys(C) keys
+int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S, int Ns, int Mq, int C,
+                 hipStream_t st);
 int range_count(int Ns, int C);          // key ranges per segment
 
 // Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null

@@ -1,10 +1,12 @@
 // Stages 2-4 of the hot path: merge rank, prefix/suffix scans and emission, for both operators.
 //
 // Per segment s = (p, d) the keys are sorted (sort.hip) and cut into key ranges of RK keys; one wave owns one range
-// and the queries whose merge rank r = #{keys < q} falls in it (the last range also owns r = N). Three kernels:
+// and the queries whose merge rank r = #{keys < q} falls in it (the last range also owns r = N). Four kernels:
 //
+//   query_bounds   one thread per sorted query: the query bounds of every range (a binary search over the range
+//                  boundaries in LDS per query; the bounds fall between consecutive queries).
 //   *_range_sums   one wave per range: the range's summary, computed directly (every term has its own weight,
-//                  no recurrence), and the range's query boundary by a 64-ary search in the sorted queries.
+//                  no recurrence).
 //   *_range_scan   one wave per segment: turns the summaries into each range's entry state (exclusive prefix over
 //                  the ranges to the left) and, for the Laplace sum, exit state (exclusive suffix to the right).
 //   *_range_walk   one wave per range: gathers the range's RK value rows into registers (lane = channel), runs the
@@ -123,10 +125,9 @@ __device__ __forceinline__ void mask_rows(float (&x)[RK][NV], const float kw) {
 // Rt = sum_t e^{-(k_t - k_first)} v_t (the R state at its first key, zero beyond the range). Slot C: the v == 1 sums.
 template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
-void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
+void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp,
                     const float* __restrict__ v, const uint8_t* __restrict__ keep, float* __restrict__ ta,
-                    float* __restrict__ tb, int* __restrict__ qb,
-                    const int S, const int D, const int N, const int M, const int C, const int G)  // ta/tb: summaries
+                    float* __restrict__ tb, const int S, const int D, const int N, const int C, const int G)
 {
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
@@ -178,8 +179,6 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
         rb[C + 1] = (g < G - 1) ? __expf(-(kseg[base + RK] - kfirst)) : 0.f;
     }
 
-    const int ub = wave_upper_bound(qs + (size_t)s * M, M, klast);
-    if (l == 0) qb[(size_t)s * G + g] = ub;
 }
 
 // The range scans run one workgroup of SCAN_W waves per segment. Each wave owns a contiguous piece of the segment's
@@ -572,10 +571,11 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
     const int G = (N + RK - 1) / RK;
     const long waves = (long)S * G;
     const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
+    if (int e = query_bounds(ks, qs, ra.qb, 0.f, S, N, M, C, st)) return e;
     {
         StageTimer t("lap_range_sums", st);
         hipLaunchKernelGGL((lap_range_sums<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                           ks, kp, qs, v, keep, ra.sa, ra.sb, ra.qb, S, D, N, M, C, G);
+                           ks, kp, v, keep, ra.sa, ra.sb, S, D, N, C, G);
     }
     {
         StageTimer t("lap_range_scan", st);
@@ -614,11 +614,10 @@ int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uin
 // weight (0 for masked keys); w_t and u_t are taken times kw_t.
 template <int NV, int RK, bool WANT_W, bool WANT_U>
 __global__ __launch_bounds__(WPB * WAVE)
-void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
+void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp,
                     const float* __restrict__ w, const float* __restrict__ u, const uint8_t* __restrict__ keep,
-                    float* __restrict__ ta, float* __restrict__ tb, int* __restrict__ qb,
-                    const int S, const int D, const int Ns, const int Mq, const int C, const int G,
-                    const float qshift)
+                    float* __restrict__ ta, float* __restrict__ tb, const int S, const int D, const int Ns,
+                    const int C, const int G)
 {
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
@@ -676,26 +675,70 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
         ra[C + 1] = (g > 0) ? (klast - kseg[base - 1]) : 0.f;   // slot C+1: the scan's key gap into this range
     }
 
-    const float* qseg = qs + (size_t)s * Mq;
-    const int ub = wave_upper_bound_from(qseg, 0, Mq, klast, qshift);
-    if (l == 0) qb[(size_t)s * G + g] = ub;
 }
 
-// Query boundaries alone (what the sums kernels write to qb), for queries shifted by qshift: one wave per range.
+// Query bounds of every key range, from the sorted queries in one pass: qb[s, g] = #{i : q_i + qshift <= klast_g},
+// klast_g the largest key of range g. A workgroup (segment, RB_T * RB_Q queries) stages the segment's G range
+// boundaries in LDS; query i finds its bucket b_i = #{g : klast_g < q_i + qshift} by binary search there. The b_i do not decrease with i,
+// so qb[g] = i + 1 for every g in [b_i, b_{i+1}) (b_M = G), and qb[g] = 0 below b_0: every bound is written exactly
+// once, by the query it follows. (One search per query instead of a dependent search chain per range.)
+constexpr int RB_T = 1024;         // threads per workgroup
+constexpr int RB_Q = 4;            // consecutive queries per thread
+constexpr int RB_MAXG = 4096;      // ranges per segment: N <= 131072 keys in ranges of >= 32
+
 template <int RK>
-__global__ __launch_bounds__(WPB * WAVE)
-void range_bounds_kernel(const float* __restrict__ ks, const float* __restrict__ qs, int* __restrict__ qb,
-                         const float qshift, const int S, const int Ns, const int Mq, const int G)
+__global__ __launch_bounds__(RB_T)
+void query_bounds_kernel(const float* __restrict__ ks, const float* __restrict__ qs, int* __restrict__ qb,
+                         const float qshift, const int Ns, const int Mq, const int G, const int chunks)
 {
-    const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
-    if (wv >= (long)S * G) return;
-    const int s = (int)(wv / G), g = (int)(wv - (long)s * G);
-    const float klast = ks[(size_t)s * Ns + min(Ns, (g + 1) * RK) - 1];
+    __shared__ float bnd[RB_MAXG];
+    const int s = blockIdx.x / chunks, ch = blockIdx.x - s * chunks;
+    const float* kseg = ks + (size_t)s * Ns;
+    for (int g = threadIdx.x; g < G; g += RB_T) bnd[g] = kseg[min(Ns, (g + 1) * RK) - 1];
+    __syncthreads();
+    auto bucket = [&](const float x) {
+        int lo = 0, hi = G;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (bnd[mid] < x) lo = mid + 1;
+            else hi = mid;
+        }
+        return lo;
+    };
+    // thread t: queries i0 .. i0 + RB_Q - 1 and, for the bounds after the last of them, the query that follows
+    const int i0 = (ch * RB_T + (int)threadIdx.x) * RB_Q;
+    if (i0 >= Mq) return;
     const float* qseg = qs + (size_t)s * Mq;
-    UpperBoundProbe ubp;
-    ubp.probe(qseg, Mq);
-    const int ub = ubp.finish(qseg, Mq, klast, qshift);
-    if (lane_id() == 0) qb[(size_t)s * G + g] = ub;
+    float x[RB_Q + 1];
+#pragma unroll
+    for (int j = 0; j <= RB_Q; ++j) x[j] = qseg[min(i0 + j, Mq - 1)];   // clamped: all loads in flight
+    int* qbs = qb + (size_t)s * G;
+    int b = bucket(x[0] + qshift);
+    if (i0 == 0)
+        for (int g = 0; g < b; ++g) qbs[g] = 0;
+#pragma unroll
+    for (int j = 0; j < RB_Q; ++j) {
+        const int i = i0 + j;
+        if (i >= Mq) break;
+        const int bn = (i + 1 < Mq) ? bucket(x[j + 1] + qshift) : G;
+        for (int g = b; g < bn; ++g) qbs[g] = i + 1;
+        b = bn;
+    }
+}
+
+int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S, int Ns, int Mq, int C,
+                 hipStream_t st) {
+    const int RK = range_keys(C);
+    const int G = (Ns + RK - 1) / RK;
+    if (G > RB_MAXG) return (int)hipErrorInvalidValue;
+    const int chunks = (Mq + RB_T * RB_Q - 1) / (RB_T * RB_Q);
+    const dim3 grid((unsigned)((long)S * chunks));
+    StageTimer t("query_bounds", st);
+    if (RK == 64)
+        hipLaunchKernelGGL((query_bounds_kernel<64>), grid, dim3(RB_T), 0, st, ks, qs, qb, qshift, Ns, Mq, G, chunks);
+    else
+        hipLaunchKernelGGL((query_bounds_kernel<32>), grid, dim3(RB_T), 0, st, ks, qs, qb, qshift, Ns, Mq, G, chunks);
+    return (int)hipGetLastError();
 }
 
 // Abs: entry prefix state of every range and the segment totals (row G). State (PW, B) with B relative to the last
@@ -1040,20 +1083,18 @@ static int abs_prepare_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStre
     const int G = (a.Ns + RK - 1) / RK;
     const long waves = (long)S * G;
     const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
+    if (int e = query_bounds(a.ks, a.qs, ra.qb, a.qshift, S, a.Ns, a.Mq, a.C, st)) return e;
     {
         StageTimer t("abs_range_sums", st);
         if (mode & ABS_DOTX2)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, true>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, a.keep, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G,
-                               a.qshift);
+                               a.ks, a.kp, a.w, a.u, a.keep, ra.sa, ra.sb, S, a.D, a.Ns, a.C, G);
         else if (mode == ABS_RANK)
             hipLaunchKernelGGL((abs_range_sums<NV, RK, false, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, a.keep, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G,
-                               a.qshift);
+                               a.ks, a.kp, a.w, a.u, a.keep, ra.sa, ra.sb, S, a.D, a.Ns, a.C, G);
         else
             hipLaunchKernelGGL((abs_range_sums<NV, RK, true, false>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                               a.ks, a.kp, a.qs, a.w, a.u, a.keep, ra.sa, ra.sb, ra.qb, S, a.D, a.Ns, a.Mq, a.C, G,
-                               a.qshift);
+                               a.ks, a.kp, a.w, a.u, a.keep, ra.sa, ra.sb, S, a.D, a.Ns, a.C, G);
     }
     {
         StageTimer t("abs_range_scan", st);
@@ -1104,18 +1145,7 @@ int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
 }
 
 int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st) {
-    const int S = a.P * a.D;
-    const int G = range_count(a.Ns, a.C);
-    const long waves = (long)S * G;
-    const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
-    StageTimer t("range_bounds", st);
-    if (a.C <= WAVE)
-        hipLaunchKernelGGL((range_bounds_kernel<64>), dim3(blocks), dim3(WPB * WAVE), 0, st, a.ks, a.qs, qb, a.qshift,
-                           S, a.Ns, a.Mq, G);
-    else
-        hipLaunchKernelGGL((range_bounds_kernel<32>), dim3(blocks), dim3(WPB * WAVE), 0, st, a.ks, a.qs, qb, a.qshift,
-                           S, a.Ns, a.Mq, G);
-    return (int)hipGetLastError();
+    return query_bounds(a.ks, a.qs, qb, a.qshift, a.P * a.D, a.Ns, a.Mq, a.C, st);
 }
 
 }  // namespace qlka
