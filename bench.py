@@ -9,7 +9,7 @@ step). `roofline` is for the dominant kernel, timed with hipEvents recorded by l
 inside the timed region. `cpu_baseline` times the reference's dense PyTorch path (restated in oracle/dense.py) on the
 host CPU on a bounded query sample of the same workload.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-layers]
 """
 
 import argparse
@@ -103,6 +103,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-layers", action="store_true",
+                    help="skip the attention-layer timings (layer_ms), e.g. to profile the two ops alone")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -200,6 +202,7 @@ def main():
     # composition (separate op calls + torch epilogue, attention.py:67-92).
     from qlka import layers
     layer_ms = {}
+    kinds = () if args.no_layers else layers.KINDS
     # Padded batch: the last 10% of the keys of every p masked (attention.py:122-124). In-kernel mask (one masked
     # layer call on the raw k, v) vs the reference's route (k * keep, v * keep, the ops, the n_pad epilogue).
     keep = torch.ones(P, N, dtype=torch.bool, device=dev)
@@ -211,7 +214,7 @@ def main():
         return layers.unfused(kern, q, k * kf[:, None, :], v * kf[:, :, None], n_pad)
 
     with torch.no_grad():
-        for kern in layers.KINDS:
+        for kern in kinds:
             layer_ms[kern] = {
                 "fused": round(op_time(lambda: layers.layer_forward(kern, q, k, v)), 4),
                 "unfused": round(op_time(lambda: layers.unfused(kern, q, k, v)), 4),
