@@ -311,7 +311,14 @@ DIRECT_SHAPES = [  # P, D, N, M, C: tiles of 64 queries / keys and 32 features, 
     (1, 2, 257, 300, 128),
     (4, 32, 65, 65, 32),      # the ViT segment shape of BASELINE configs[1]
     (2, 4, 1500, 900, 16),    # long segments: the dense route is valid at any size
+    # Segments of at most 128 (padded) keys and queries have one-workgroup-per-p kernels (whole segment in LDS)
+    # besides the tiled ones; the shapes above cover both, these add several 64-feature chunks with ragged sizes,
+    # the largest segment the small kernels take, and C = 128 (small forward, tiled sign sums).
+    (2, 70, 61, 50, 19),
+    (1, 8, 108, 112, 8),
+    (2, 3, 40, 30, 128),
 ]
+DIRECT_SIGN_SHAPES = [s for s in DIRECT_SHAPES if s[2] * s[3] < 1_000_000]
 
 
 @pytest.mark.parametrize("shape", DIRECT_SHAPES)
@@ -363,8 +370,8 @@ def test_keops_route_forward_and_autograd(dev, full):
     _assert_rel(_np(tv.grad), wv, nv, "keops route grad_v")
 
 
-@pytest.mark.parametrize("shape", DIRECT_SHAPES[:6])
-@pytest.mark.parametrize("tie", [0.0, -1.0])
+@pytest.mark.parametrize("shape", DIRECT_SIGN_SHAPES)
+@pytest.mark.parametrize("tie", [0.0, -1.0, 1.0])      # s(0) = +-1 have their own compare-select sign step
 @pytest.mark.parametrize("kind", ["normal", "ties"])
 def test_direct_backward(dev, shape, tie, kind):
     from weighted_abs_sum import _ext
@@ -382,8 +389,8 @@ def test_direct_backward(dev, shape, tie, kind):
         _assert_rel(_np(gv), wv, nv, f"direct grad_v full={full}")
 
 
-@pytest.mark.parametrize("shape", DIRECT_SHAPES[:6])
-@pytest.mark.parametrize("tie", [0.0, 1.0])
+@pytest.mark.parametrize("shape", DIRECT_SIGN_SHAPES)
+@pytest.mark.parametrize("tie", [0.0, 1.0, -1.0, 0.5])
 @pytest.mark.parametrize("kind", ["normal", "ties"])
 def test_direct_sgn(dev, shape, tie, kind):
     from weighted_abs_sum import _ext
