@@ -554,10 +554,16 @@ static void launch_sign_small(const float* a, const float* b, const float* x, co
                            x, y, gu, out, tie, scale, D, I, J, C);
 }
 
+static bool sign_small_fits(int D, int I, int J, int C) {
+    return pad4(I) <= DS_MAX && pad4(J) <= DS_MAX && pad4(C) <= DS_CMAX && direct_sign_small_lds(D, I, J, C) <= DS_LDS_MAX;
+}
+
+bool direct_sign_fast(int D, int N, int M, int C) { return sign_small_fits(D, M, N, C) && sign_small_fits(D, N, M, C); }
+
 int direct_sign(bool gu_own, const float* a, const float* b, const float* x, const float* y, const float* gu,
                 float* out, float tie, float scale, int P, int D, int I, int J, int C, hipStream_t st) {
-    const size_t lds = direct_sign_small_lds(D, I, J, C);
-    if (pad4(I) <= DS_MAX && pad4(J) <= DS_MAX && pad4(C) <= DS_CMAX && lds <= DS_LDS_MAX) {
+    if (sign_small_fits(D, I, J, C)) {
+        const size_t lds = direct_sign_small_lds(D, I, J, C);
         StageTimer t("direct_sign", st);
         if (gu_own) launch_sign_small<true>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, lds, st);
         else launch_sign_small<false>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, lds, st);

@@ -106,3 +106,15 @@ def test_layer_workspace_and_validation(lib):
     assert rc == 1 and "keep must be non-null" in lib.qlka_last_error().decode()
     rc = lib.qlka_layer_fwd_masked(5, dummy, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
     assert rc == 1 and "kind must be" in lib.qlka_last_error().decode()
+
+
+def test_direct_cutoff_setter(lib):
+    prev = lib.qlka_set_direct_max(0)
+    try:
+        assert prev == 256                       # the default
+        assert lib.qlka_set_direct_max(100) == 0
+        assert lib.qlka_set_direct_max(-1) < 0
+        assert b"must be >= 0" in lib.qlka_last_error()
+        assert lib.qlka_set_direct_max(prev) == 100   # a rejected value leaves the cutoff alone
+    finally:
+        lib.qlka_set_direct_max(prev)

@@ -64,6 +64,27 @@ SHAPES = [
 ]
 
 
+@pytest.fixture(params=["auto", "walk"])
+def route(request):
+    """auto: the library's size routing (dense kernels for short segments); walk: sort + walk at every size
+    (qlka_set_direct_max(0)), so the walks stay covered on the short segments the routing sends elsewhere."""
+    from qlka import _lib
+    lib = _lib.load()
+    if request.param == "auto":
+        yield "auto"
+        return
+    prev = lib.qlka_set_direct_max(0)
+    try:
+        yield "walk"
+    finally:
+        lib.qlka_set_direct_max(prev)
+
+
+def _same_route(route, N, M):
+    if route == "walk" and max(N, M) > 256:
+        pytest.skip("above the dense cutoff both routes walk")
+
+
 # ------------------------------------------------------------------------------------------------ sort / rank
 @pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 100, 257, 1000, 2049, 5000, 8192, 16384, 16385, 40000])
 @pytest.mark.parametrize("kind", ["normal", "ties", "zeros"])
@@ -98,9 +119,10 @@ def test_merge_rank_bit_exact(dev, N, M, kind):
 # --------------------------------------------------------------------------------------------------- forward ops
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("kind", ["normal", "ties"])
-def test_laplace_forward(dev, shape, kind):
+def test_laplace_forward(dev, shape, kind, route):
     from weighted_laplace_sum import weighted_laplace_sum
     P, D, N, M, C = shape
+    _same_route(route, N, M)
     q, k, v = _data(P, D, N, M, C, seed=sum(shape), kind=kind)
     w, u = weighted_laplace_sum(_t(q, dev), _t(k, dev), _t(v, dev))
     ow, ou, nw = brute.laplace_sum(q, k, v)
@@ -119,9 +141,10 @@ def test_laplace_wide_spread_underflow(dev):
 
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("kind", ["normal", "ties"])
-def test_abs_forward_full(dev, shape, kind):
+def test_abs_forward_full(dev, shape, kind, route):
     from weighted_abs_sum import weighted_abs_sum, weighted_abs_sum_full
     P, D, N, M, C = shape
+    _same_route(route, N, M)
     q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 1, kind=kind)
     tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
     w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
@@ -146,9 +169,10 @@ def test_abs_translation_far_from_zero(dev):
 
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("kind", ["normal", "ties"])
-def test_sgn_sum(dev, shape, kind):
+def test_sgn_sum(dev, shape, kind, route):
     from weighted_abs_sum import weighted_sgn_sum
     P, D, N, M, C = shape
+    _same_route(route, N, M)
     q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 2, kind=kind)
     g = np.random.default_rng(3).standard_normal((P, M, C)).astype(np.float32)
     out = weighted_sgn_sum(_t(q, dev), _t(k, dev), _t(v, dev), _t(g, dev), backend="cuda")
@@ -160,9 +184,10 @@ def test_sgn_sum(dev, shape, kind):
 @pytest.mark.parametrize("shape", SHAPES)
 @pytest.mark.parametrize("full", [False, True])
 @pytest.mark.parametrize("kind", ["normal", "ties"])
-def test_abs_backward(dev, shape, full, kind):
+def test_abs_backward(dev, shape, full, kind, route):
     from weighted_abs_sum import _ext
     P, D, N, M, C = shape
+    _same_route(route, N, M)
     q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 3, kind=kind)
     rng = np.random.default_rng(4)
     g_w = rng.standard_normal((P, M, C)).astype(np.float32)
