@@ -115,6 +115,59 @@ int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, 
     return QLKA_OK;
 }
 
+// ---- overlap of the query side (q sort, range boundaries) with the key side (range summaries, scan)
+// The two sides read and write disjoint parts of the workspace and both need only the sorted keys. The key side runs
+// on the caller's stream, the query side on a side stream of the calling thread (one per device, created on first
+// use, default priority, non-blocking). Events order the side stream after the work already on the caller's stream,
+// and the caller's stream after the side stream's work. A host thread issues its calls in order, so reusing its two
+// events is safe; a fork / join through events is also how work on a captured stream reaches another stream.
+struct SideStream { hipStream_t s = nullptr; hipEvent_t fork = nullptr, join = nullptr; };
+
+hipError_t side_stream(hipStream_t st, SideStream** out) {
+    *out = nullptr;
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return e;
+    if (st != nullptr) {
+        hipDevice_t dev = cur;
+        if ((e = hipStreamGetDevice(st, &dev)) != hipSuccess) return e;
+        if (dev != cur) return hipSuccess;              // stream of another device: run in order on it
+    }
+    constexpr int MAX_DEVICES = 64;
+    thread_local SideStream sides[MAX_DEVICES];
+    if (cur >= MAX_DEVICES) return hipSuccess;
+    SideStream& sd = sides[cur];
+    if (sd.s == nullptr) {
+        SideStream n;
+        if ((e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&n.join, hipEventDisableTiming)) != hipSuccess) return e;
+        sd = n;
+    }
+    *out = &sd;
+    return hipSuccess;
+}
+
+template <class KeySide, class QuerySide>
+int fork_join(hipStream_t st, KeySide key_side, QuerySide query_side) {
+    SideStream* sd = nullptr;
+    if (hipError_t e = side_stream(st, &sd)) return hip_status((int)e, "side stream");
+    if (sd == nullptr) {
+        if (int e = query_side(st)) return e;
+        return key_side(st);
+    }
+    if (hipError_t e = hipEventRecord(sd->fork, st)) return hip_status((int)e, "fork");
+    if (hipError_t e = hipStreamWaitEvent(sd->s, sd->fork, 0)) return hip_status((int)e, "fork");
+    const int eq = query_side(sd->s);
+    const int ek = key_side(st);
+    // join whatever happened, so that nothing later on st can overtake work issued on the side stream
+    const hipError_t r = hipEventRecord(sd->join, sd->s);
+    const hipError_t w = r == hipSuccess ? hipStreamWaitEvent(st, sd->join, 0) : r;
+    if (eq) return eq;
+    if (ek) return ek;
+    return w == hipSuccess ? QLKA_OK : hip_status((int)w, "join");
+}
+
 }  // namespace
 
 extern "C" {
@@ -149,8 +202,16 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
         return hip_status(direct_fwd(1, q, k, v, out_w, out_u, P, D, N, M, C, st), "laplace direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
-    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
-    int e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, nullptr, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    int e = fork_join(st,
+        [&](hipStream_t s) {
+            return hip_status(laplace_prepare(w.ks, w.kp, v, nullptr, P, D, N, C, w.ra, s), "laplace ranges"); },
+        [&](hipStream_t s) {
+            if (int r = seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, s))
+                return hip_status(r, "segmented sort of q");
+            return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, 0.f, S, N, M, C, s), "query bounds"); });
+    if (e) return e;
+    e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, nullptr, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
     if (e) return hip_status(e, "laplace walk");
     e = reduce_slabs(w.slab, w.uslab, w.qinv, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "laplace reduce");
@@ -182,14 +243,22 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
         return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
-    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
     AbsWalkArgs a{};
     a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
     a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
     a.slab = w.slab; a.uslab = out_u ? w.uslab : nullptr; a.CR = slab_stride(C);
     a.out_dot = nullptr; a.out_rank = nullptr;
     a.sign = 1.f; a.P = P; a.D = D; a.C = C;
-    int e = abs_walk(a, out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW, w.ra, st);
+    const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    int e = fork_join(st,
+        [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); },
+        [&](hipStream_t s) {
+            if (int r = seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, s))
+                return hip_status(r, "segmented sort of q");
+            return hip_status(range_bounds(a, w.ra.qb, s), "query bounds"); });
+    if (e) return e;
+    e = abs_emit(a, mode, w.ra, st);
     if (e) return hip_status(e, "abs walk");
     e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qinv, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "abs reduce");
@@ -370,10 +439,20 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
     const int S = P * D;
     LayerWs L = carve_layer(kind, ws, spec);
     SortedWs& w = L.op;
-    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    auto sort_q = [&](hipStream_t s) {
+        return hip_status(seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, s), "segmented sort of q");
+    };
     int e = 0;
     if (kind == LAYER_ADD_LAPLACE) {
-        e = laplace_walk(w.ks, w.kp, w.qs, w.qp, v, keep, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+        e = fork_join(st,
+            [&](hipStream_t s) {
+                return hip_status(laplace_prepare(w.ks, w.kp, v, keep, P, D, N, C, w.ra, s), "laplace ranges"); },
+            [&](hipStream_t s) {
+                if (int r = sort_q(s)) return r;
+                return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, 0.f, S, N, M, C, s), "query bounds"); });
+        if (e) return e;
+        e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, keep, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
         if (e) return hip_status(e, "laplace walk");
         e = reduce_slabs(w.slab, w.uslab, w.qinv, L.w[0], L.u[0], P, D, M, C, st);
         if (e) return hip_status(e, "laplace reduce");
@@ -387,26 +466,32 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         const int mode = ABS_ROW | ABS_ONES | (keep ? ABS_KEEP : 0);
         // one sort of k and q, one set of range summaries and one scan serve every query shift: q + s has the sorted
         // order of q, and the key side does not depend on the queries
-        e = abs_prepare(a, mode, w.ra, st);
-        if (e) return hip_status(e, "abs ranges");
         const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
         const float shift[3] = {0.f, 1.f, -1.f};
+        int* qbs[3] = {w.ra.qb, L.qb[0], L.qb[1]};
+        e = fork_join(st,
+            [&](hipStream_t s) {
+                if (int r = abs_prepare(a, mode, w.ra, s)) return hip_status(r, "abs ranges");
+                if (kind == LAYER_ADD_RIESZ)
+                    return hip_status(riesz_prefix(k, v, keep, L.pre, P, D, N, C, s), "riesz prefixes");
+                return QLKA_OK; },
+            [&](hipStream_t s) {
+                if (int r = sort_q(s)) return r;
+                for (int ev = 0; ev < nev; ++ev) {
+                    AbsWalkArgs b = a;
+                    b.qshift = shift[ev];
+                    if (int r = range_bounds(b, qbs[ev], s)) return hip_status(r, "query bounds");
+                }
+                return QLKA_OK; });
+        if (e) return e;
         for (int ev = 0; ev < nev; ++ev) {
             RangeArrays ra = w.ra;
             a.qshift = shift[ev];
-            if (ev > 0) {
-                ra.qb = L.qb[ev - 1];
-                e = range_bounds(a, ra.qb, st);
-                if (e) return hip_status(e, "query bounds");
-            }
+            ra.qb = qbs[ev];
             e = abs_emit(a, mode, ra, st);
             if (e) return hip_status(e, "abs walk");
             e = reduce_slabs(w.slab, w.uslab, w.qinv, L.w[ev], L.u[ev], P, D, M, C, st);
             if (e) return hip_status(e, "abs reduce");
-        }
-        if (kind == LAYER_ADD_RIESZ) {
-            e = riesz_prefix(k, v, keep, L.pre, P, D, N, C, st);
-            if (e) return hip_status(e, "riesz prefixes");
         }
     }
     const bool bump = kind == LAYER_ADD_BUMP;

@@ -61,6 +61,13 @@ __host__ __device__ inline int slab_stride(int C) { return (C + 31) / 32 * 32; }
 int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
                  const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
                  hipStream_t st);
+// The parts of laplace_walk: the key side (range summaries and scan into ra.ta / ra.tb), which needs only the sorted
+// keys, and the walk, which also needs the sorted queries and their range boundaries (query_bounds into ra.qb).
+int laplace_prepare(const float* ks, const uint32_t* kp, const float* v, const uint8_t* keep, int P, int D, int N,
+                    int C, RangeArrays ra, hipStream_t st);
+int laplace_emit(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
+                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
+                 hipStream_t st);
 
 // D-reduction of the slabs: out[p,m,c] = sum_d slab[(p*D+d)*M + m][c]; out_u[p,m] = sum_d uslab[(p*D+d)*M + qinv]
 // with qinv[(p*D+d)*M + m] the sorted position of query m in feature d. out_u / uslab / qinv may be null.
@@ -97,10 +104,11 @@ struct AbsWalkArgs {
     int P, D, C;
     float qshift;            // added to every query value (0: the queries as given); the sorted order is unchanged
 };
-// sums + scan + walk
+// query boundaries + sums + scan + walk
 int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
-// the two halves of abs_walk: range summaries, query boundaries (for a.qshift) and scan; then the walk alone, which
-// may run several times over one prepared ra with different qshift / ra.qb
+// the parts of abs_walk: the key side (range summaries and scan, from the sorted keys alone); the query boundaries
+// (range_bounds, for a.qshift, from the sorted keys and queries); then the walk, which may run several times over one
+// prepared ra with different qshift / ra.qb
 int abs_prepare(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
 int abs_emit(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
 // query boundaries of every key range for queries shifted by qshift (what abs_prepare writes to ra.qb for a.qshift)

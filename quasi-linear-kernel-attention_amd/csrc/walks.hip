@@ -564,14 +564,12 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 }
 
 template <int NV, int RK>
-static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                          const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C,
-                          RangeArrays ra, hipStream_t st) {
+static int laplace_prepare_t(const float* ks, const uint32_t* kp, const float* v, const uint8_t* keep, int P, int D,
+                             int N, int C, RangeArrays ra, hipStream_t st) {
     const int S = P * D;
     const int G = (N + RK - 1) / RK;
     const long waves = (long)S * G;
     const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
-    if (int e = query_bounds(ks, qs, ra.qb, 0.f, S, N, M, C, st)) return e;
     {
         StageTimer t("lap_range_sums", st);
         hipLaunchKernelGGL((lap_range_sums<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
@@ -582,6 +580,15 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
         hipLaunchKernelGGL((lap_range_scan<NV, RK>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
                            ra.sa, ra.sb, ra.ta, ra.tb, S, C, G);
     }
+    return (int)hipGetLastError();
+}
+
+template <int NV, int RK>
+static int laplace_emit_t(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
+                          const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C,
+                          RangeArrays ra, hipStream_t st) {
+    const int S = P * D;
+    const int G = (N + RK - 1) / RK;
     {
         const long walk_waves = (long)S * ((G + RPW - 1) / RPW);
         const unsigned walk_blocks = (unsigned)((walk_waves + WPB - 1) / WPB);
@@ -598,11 +605,25 @@ static int laplace_walk_t(const float* ks, const uint32_t* kp, const float* qs, 
     return (int)hipGetLastError();
 }
 
+int laplace_prepare(const float* ks, const uint32_t* kp, const float* v, const uint8_t* keep, int P, int D, int N,
+                    int C, RangeArrays ra, hipStream_t st) {
+    if (C <= WAVE) return laplace_prepare_t<1, 64>(ks, kp, v, keep, P, D, N, C, ra, st);
+    return laplace_prepare_t<2, 32>(ks, kp, v, keep, P, D, N, C, ra, st);
+}
+
+int laplace_emit(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
+                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
+                 hipStream_t st) {
+    if (C <= WAVE) return laplace_emit_t<1, 64>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
+    return laplace_emit_t<2, 32>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
+}
+
 int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
                  const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
                  hipStream_t st) {
-    if (C <= WAVE) return laplace_walk_t<1, 64>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
-    return laplace_walk_t<2, 32>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
+    if (int e = query_bounds(ks, qs, ra.qb, 0.f, P * D, N, M, C, st)) return e;
+    if (int e = laplace_prepare(ks, kp, v, keep, P, D, N, C, ra, st)) return e;
+    return laplace_emit(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
 }
 
 // =================================================================================================================
@@ -1083,7 +1104,6 @@ static int abs_prepare_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStre
     const int G = (a.Ns + RK - 1) / RK;
     const long waves = (long)S * G;
     const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
-    if (int e = query_bounds(a.ks, a.qs, ra.qb, a.qshift, S, a.Ns, a.Mq, a.C, st)) return e;
     {
         StageTimer t("abs_range_sums", st);
         if (mode & ABS_DOTX2)
@@ -1140,6 +1160,7 @@ int abs_emit(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
 }
 
 int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
+    if (int e = range_bounds(a, ra.qb, st)) return e;
     if (int e = abs_prepare(a, mode, ra, st)) return e;
     return abs_emit(a, mode, ra, st);
 }
