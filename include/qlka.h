@@ -32,11 +32,10 @@ const char* qlka_last_error(void);
 int qlka_version(void);
 /*
  * Largest max(N, M) for which qlka_laplace_fwd, qlka_abs_fwd (path -1), qlka_abs_bwd and qlka_sgn_fwd use the dense
- * evaluation (the qlka_direct_* kernels, same results to fp32 rounding, same tie conventions) instead of sort + walk;
- * the backward and the sgn sum only where the segment also fits the one-workgroup dense sign kernel (max(N, M) <= 128,
- * C <= 64). Default 256; 0 always sorts and walks. Process-wide; returns the previous value (or -QLKA_EINVAL for
- * n < 0). The C-level counterpart of the reference's set_keops_cutoff (Weighted_Abs_Sum/weighted_abs_sum/ops.py:21-25),
- * which picks the KeOps backend in Python.
+ * evaluation (the qlka_direct_* kernels, same results to fp32 rounding, same tie conventions) instead of sort + walk.
+ * Default 512; 0 always sorts and walks. Process-wide; returns the previous value (or -QLKA_EINVAL for n < 0). The
+ * C-level counterpart of the reference's set_keops_cutoff (Weighted_Abs_Sum/weighted_abs_sum/ops.py:21-25), which
+ * picks the KeOps backend in Python.
  */
 int qlka_set_direct_max(int n);
 

@@ -34,12 +34,11 @@ int hip_status(int e, const char* where) {
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Up to this max(N, M) the dense evaluation (direct.hip) beats sort + scans + walk + reduce, whose cost there is
-// launch and per-segment overhead (measured on MI355X, forward: 4-5x at N = 65, 2-2.6x at N = 256, break-even near
-// 600). The backward and the sgn sum take it where the one-workgroup dense sign kernel applies (max(N, M) <= 128,
-// C <= 64). qlka_set_direct_max changes it (0: always sort + walk).
-std::atomic<int> g_direct_max{256};
+// launch and per-segment overhead. Measured on MI355X (P = 48, D = C = 64 and P = 512, D = C = 32), dense / walk:
+// abs forward 0.30 / 0.39 at N = 512 and still faster at 1024; Laplace forward 0.51 / 0.67 at 512, about even at 768;
+// backward 0.50 / 0.75 at 512, even at 768. qlka_set_direct_max changes it (0: always sort + walk).
+std::atomic<int> g_direct_max{512};
 inline bool use_direct(int N, int M) { return std::max(N, M) <= g_direct_max.load(std::memory_order_relaxed); }
-inline bool use_direct_sign(int D, int N, int M, int C) { return use_direct(N, M) && direct_sign_fast(D, N, M, C); }
 
 // Same limits and wording as check_qkv (Weighted_Abs_Sum/csrc/binding.cpp:79-83).
 int check_dims(int P, int D, int N, int M, int C) {
@@ -284,7 +283,7 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
     const WsSpec spec = abs_bwd_spec(P, D, N, M, C);
     if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
-    if (use_direct_sign(D, N, M, C))     // the walks' convention: a tie counts -1 in both gradients
+    if (use_direct(N, M))     // the walks' convention: a tie counts -1 in both gradients
         return hip_status(direct_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st),
                           "dense backward");
     const int S = P * D;
@@ -324,7 +323,7 @@ int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g,
     if (!q || !k || !v || !g || !out) return fail(QLKA_EINVAL, "q, k, v, g and out must be non-null");
     if (int e = check_ws(ws, ws_bytes_given, qlka_sgn_fwd_ws_bytes(P, D, N, M, C))) return e;
     hipStream_t st = (hipStream_t)stream;
-    if (use_direct_sign(D, N, M, C))     // sgn(k - q) with a tie counted +1 == -(s(q - k) with a tie counted -1)
+    if (use_direct(N, M))     // sgn(k - q) with a tie counted +1 == -(s(q - k) with a tie counted -1)
         return hip_status(direct_sign(true, q, k, g, v, nullptr, out, -1.f, -1.f, P, D, M, N, C, st), "dense sgn sum");
     const int S = P * D;
     SortedWs w = carve(ws, WsSpec{P, D, N, M, C, N, 0, false});

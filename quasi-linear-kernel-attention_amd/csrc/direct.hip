@@ -5,20 +5,19 @@
 //   A[m, n] = sum_d f(q[d, m] - k[d, n]),  f = |x| (abs) or e^{-|x|} (Laplace)
 //   out_w[m, :] = sum_n A[m, n] v[n, :],   out_u[m] = sum_n A[m, n]
 //
-// One workgroup per (p, tile of 64 queries) walks the keys in tiles of 64. Per key tile, q and k columns and the v
-// rows are staged in LDS; each of the 256 threads accumulates a 4 x 4 block of A over d (q and k values read as
-// 16-byte broadcasts), the A tile goes to LDS, and each thread then accumulates a 4-query x CT-channel block of
-// A v and the row sums. Nothing is sorted, so no workspace: below a few hundred keys this beats the sort + scan
-// pipeline, whose cost there is launch and per-segment overhead. All arithmetic is fp32, as in the dense and KeOps
-// paths of the reference.
+// and the sign sums of their gradients (further below). Segments of up to 128 keys and queries run one workgroup per
+// p with the whole segment in LDS; longer ones run one workgroup per (p, tile of outputs) that walks the other side
+// in tiles of 64. Nothing is sorted, so no workspace: below a few hundred keys this beats the sort + scan pipeline,
+// whose cost there is launch and per-segment overhead. All arithmetic is fp32, as in the dense and KeOps paths of
+// the reference.
 #include "qlka_common.h"
 #include "qlka_internal.h"
 
 namespace qlka {
 
-constexpr int DT = 64;             // queries and keys per tile
-constexpr int DTHREADS = 256;      // 16 x 16 threads
-constexpr int DDK = 32;            // features staged per LDS round
+// ---- tiled kernels (longer segments)
+constexpr int ST_T = 256;          // threads per workgroup
+constexpr int ST_JT = 64;          // keys (forward) / j (sign sums) per tile
 
 // ---- shared by the small-segment kernels (one workgroup per p, the whole segment in LDS)
 constexpr int DS_MAXT = 1024;      // threads per workgroup at most
@@ -29,7 +28,7 @@ constexpr size_t DS_LDS_MAX = 64 * 1024;
 
 static inline int pad4(int x) { return (x + 3) & ~3; }
 
-// One round of a zero-padded copy of the row-major [R][K] block at src into LDS: the thread's SU elements
+// One round of a zero-padded copy of the row-major [R][K] block at src (row stride K) into LDS: the thread's SU elements
 // e = e0 + u * nt of the padded [Rp][Kp] index space (row e / Kp, column e % Kp, e < n = Rp * Kp). All loads of a
 // round are issued before any LDS store, so a round costs one global-memory latency, not SU of them.
 template <int SU>
@@ -59,113 +58,11 @@ struct StageRound {
         }
     }
 };
-constexpr int DS_SU = 8;           // elements per thread per staging round
+constexpr int DS_SU = 8;
+// Size of a raw buffer descriptor used for staging, and the offset that reads past its end (the load returns 0).
+constexpr uint32_t STAGE_OOB = 0x7ffffff0u;           // elements per thread per staging round
 
 typedef float f2_t __attribute__((ext_vector_type(2)));
-
-template <int KIND, int CT>        // KIND 0: abs, 1: Laplace; CT channels per thread (4: C <= 64, 8: C <= 128)
-__global__ __launch_bounds__(DTHREADS)
-void direct_fwd_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-                       float* __restrict__ out_w, float* __restrict__ out_u,
-                       const int D, const int N, const int M, const int C, const int mtiles)
-{
-    constexpr int CW = 16 * CT;                           // channels covered by the 16 thread columns
-    __shared__ f4_t qs[DDK][DT / 4];                      // q[d][m0 .. m0+63]
-    __shared__ f4_t ks[DDK][DT / 4];                      // k[d][n0 .. n0+63]
-    __shared__ float at[DT][DT + 4];                      // A tile [m][n] (+4: no bank conflicts on columns)
-    __shared__ float vs[DT][CW];                          // v rows of the key tile
-
-    const int p = blockIdx.x / mtiles, mt = blockIdx.x - p * mtiles;
-    const int m0 = mt * DT, tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
-    const float* qp = q + (size_t)p * D * M;
-    const float* kp = k + (size_t)p * D * N;
-    const float* vp = v + (size_t)p * N * C;
-
-    float acc[4][CT], usum[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        usum[i] = 0.f;
-#pragma unroll
-        for (int j = 0; j < CT; ++j) acc[i][j] = 0.f;
-    }
-
-    for (int n0 = 0; n0 < N; n0 += DT) {
-        // ---- A tile: thread (ty, tx) owns queries m0 + 4 ty .. +3 and keys n0 + 4 tx .. +3
-        float a[4][4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) a[i][j] = 0.f;
-        for (int d0 = 0; d0 < D; d0 += DDK) {
-            __syncthreads();                              // previous readers of qs / ks are done
-            for (int e = tid; e < DDK * DT; e += DTHREADS) {
-                const int dd = e / DT, x = e - dd * DT, d = d0 + dd;
-                const int m = m0 + x, n = n0 + x;
-                // pads (past D, M or N) are never emitted: queries past M are not stored, keys past N weigh 0 below
-                reinterpret_cast<float*>(qs[dd])[x] = (d < D && m < M) ? qp[(size_t)d * M + m] : 0.f;
-                reinterpret_cast<float*>(ks[dd])[x] = (d < D && n < N) ? kp[(size_t)d * N + n] : 0.f;
-            }
-            __syncthreads();
-            const int dn = min(DDK, D - d0);
-            for (int dd = 0; dd < dn; ++dd) {
-                const f4_t qv = qs[dd][ty], kv = ks[dd][tx];
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float x = fabsf(qv[i] - kv[j]);
-                        if constexpr (KIND == 0) a[i][j] += x;
-                        else a[i][j] += __expf(-x);
-                    }
-            }
-        }
-        // keys past N contribute nothing
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (n0 + 4 * tx + j >= N) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) a[i][j] = 0.f;
-            }
-        __syncthreads();                                  // previous readers of at / vs are done
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) at[4 * ty + i][4 * tx + j] = a[i][j];
-        for (int e = tid; e < DT * CW; e += DTHREADS) {
-            const int r = e / CW, c = e - r * CW, n = n0 + r;
-            vs[r][c] = (n < N && c < C) ? vp[(size_t)n * C + c] : 0.f;
-        }
-        __syncthreads();
-        // ---- A v and row sums: thread (ty, tx) owns queries 4 ty .. +3 and channels CT tx .. +CT-1
-        const int nn = min(DT, N - n0);
-        for (int r = 0; r < nn; ++r) {
-            float av[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) av[i] = at[4 * ty + i][r];
-            float vv[CT];
-#pragma unroll
-            for (int j = 0; j < CT; ++j) vv[j] = vs[r][CT * tx + j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                usum[i] += av[i];
-#pragma unroll
-                for (int j = 0; j < CT; ++j) acc[i][j] += av[i] * vv[j];
-            }
-        }
-    }
-
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 4 * ty + i;
-        if (m >= M) continue;
-#pragma unroll
-        for (int j = 0; j < CT; ++j) {
-            const int c = CT * tx + j;
-            if (c < C) out_w[((size_t)p * M + m) * C + c] = acc[i][j];
-        }
-        if (out_u != nullptr && tx == 0) out_u[(size_t)p * M + m] = usum[i];
-    }
-}
 
 // Small segments (padded M, N <= 128, the working set within 64 KB of LDS): one workgroup per p. q and k go to LDS
 // in chunks of 64 features ([d][m], [d][n], zero-padded) and each thread accumulates a 4-key x 4-query block of
@@ -273,6 +170,163 @@ void direct_fwd_small_kernel(const float* __restrict__ q, const float* __restric
     }
 }
 
+// Longer segments: one workgroup of 256 threads per (p, tile of IT queries) walks the keys in tiles of 64. Per key
+// tile and 64-feature chunk the k values ([d][n]) come from registers loaded during the previous step, and each thread
+// adds the chunk to its 4-key x (IT / 16)-query block of A; after the last chunk the A tile goes to LDS ([n][m], zero
+// at keys past N) and each thread adds A^T v to its 2-query x 4-channel blocks (and the row sums), with the tile's v
+// rows, loaded while A was formed, in LDS ([n][c]). IT = 64 for C <= 32 (CM = 32), else 32 (CM = 64 or 128), so that
+// the blocks of A and of A^T v are (a multiple of) one per thread. Staging as in the tiled sign sums: raw buffer
+// descriptors that end at the segment's end (rows past it read 0), fixed LDS row strides; columns past the tile (keys
+// past N, queries past M, channels past C) may read the next row and never reach an output or A.
+template <int KIND, int IT, int CM>
+__global__ __launch_bounds__(ST_T)
+void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+                             float* __restrict__ out_w, float* __restrict__ out_u,
+                             const int D, const int N, const int M, const int C, const int mtiles)
+{
+    constexpr int DCK = 64;                               // features per chunk
+    constexpr int QM = IT / 16;                           // queries per thread in the A phase (4 keys x QM)
+    constexpr int KS = ST_JT + 4, VS = CM + 4;            // LDS row strides
+    constexpr int KK = ST_JT / 4, KV = CM / 4, KQ = IT / 4;   // staged elements per thread (4 threads per row)
+    constexpr int NAV = (IT / 2) * (CM / 4) / ST_T;       // A^T v blocks per thread (1 or 2)
+    __shared__ float qs[DCK * IT];                        // [d][m]
+    __shared__ float ks[DCK * KS];                        // [d][n]
+    __shared__ float vs[ST_JT * VS];                      // [n][c]
+    __shared__ float At[ST_JT * IT];                      // [n][m]
+
+    const int p = blockIdx.x / mtiles, mb = (blockIdx.x - p * mtiles) * IT, tid = threadIdx.x;
+    const int Ml = min(IT, M - mb);
+    const int sr = tid / 4, sc = tid - sr * 4;            // staging: row, first column
+    const int ktiles = (N + ST_JT - 1) / ST_JT, chunks = (D + DCK - 1) / DCK, steps = ktiles * chunks;
+    float kv[KK], vv[KV];
+    auto load_k = [&](int s) {
+        const int n0 = (s / chunks) * ST_JT, d0 = (s % chunks) * DCK;
+        const rsrc_t rk = make_rsrc(k + ((size_t)p * D + d0) * N + n0, (uint32_t)(((D - d0) * N - n0) * 4));
+#pragma unroll
+        for (int e = 0; e < KK; ++e) kv[e] = buf_load(rk, (sr * N + sc + 4 * e) * 4, 0);
+    };
+    auto load_v = [&](int t) {
+        const int n0 = t * ST_JT;
+        const rsrc_t rv = make_rsrc(v + ((size_t)p * N + n0) * C, (uint32_t)((N - n0) * C * 4));
+#pragma unroll
+        for (int e = 0; e < KV; ++e) vv[e] = buf_load(rv, (sr * C + sc + 4 * e) * 4, 0);
+    };
+    auto stage_q = [&](int d0) {                          // q rows d0 .. d0 + 63 of the query tile
+        const rsrc_t rq = make_rsrc(q + ((size_t)p * D + d0) * M + mb, (uint32_t)(((D - d0) * M - mb) * 4));
+        float qv[KQ];
+#pragma unroll
+        for (int e = 0; e < KQ; ++e) qv[e] = buf_load(rq, (sr * M + sc + 4 * e) * 4, 0);
+#pragma unroll
+        for (int e = 0; e < KQ; ++e) qs[sr * IT + sc + 4 * e] = qv[e];
+    };
+    load_k(0);
+    load_v(0);
+    if (chunks == 1) stage_q(0);
+    const int an = (tid / (IT / QM)) * 4, am = (tid - (tid / (IT / QM)) * (IT / QM)) * QM;   // A block
+    float a[4][QM], acc[NAV][2][4], us[2] = {0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int u = 0; u < QM; ++u) a[r][u] = 0.f;
+#pragma unroll
+    for (int w = 0; w < NAV; ++w)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[w][u][c] = 0.f;
+    for (int s = 0; s < steps; ++s) {
+        const int t = s / chunks, h = s - t * chunks, n0 = t * ST_JT, d0 = h * DCK;
+        __syncthreads();                                  // readers of ks (and of vs / At / qs) are done
+#pragma unroll
+        for (int e = 0; e < KK; ++e) ks[sr * KS + sc + 4 * e] = kv[e];
+        if (h == 0)
+#pragma unroll
+            for (int e = 0; e < KV; ++e) vs[sr * VS + sc + 4 * e] = vv[e];
+        if (s + 1 < steps) {
+            load_k(s + 1);
+            if ((s + 1) % chunks == 0) load_v(t + 1);
+        }
+        if (chunks > 1) stage_q(d0);
+        __syncthreads();
+        const int rows = min(DCK, D - d0);
+        for (int dd = 0; dd < rows; ++dd) {               // features past D are not summed (e^0 would count)
+            const f4_t kr = *reinterpret_cast<const f4_t*>(ks + dd * KS + an);
+            float qr[QM];
+            if constexpr (QM == 4) {
+                const f4_t x4 = *reinterpret_cast<const f4_t*>(qs + dd * IT + am);
+                qr[0] = x4[0]; qr[1] = x4[1]; qr[2] = x4[2]; qr[3] = x4[3];
+            } else {
+                const f2_t x2 = *reinterpret_cast<const f2_t*>(qs + dd * IT + am);
+                qr[0] = x2[0]; qr[1] = x2[1];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int u = 0; u < QM; ++u) {
+                    const float x = fabsf(qr[u] - kr[r]);
+                    if constexpr (KIND == 0) a[r][u] += x;
+                    else a[r][u] += __expf(-x);
+                }
+        }
+        if (h + 1 < chunks) continue;
+        // the A tile is complete: keys past N weigh 0 (v reads 0 there, out_u would not)
+        const int Nl = min(ST_JT, N - n0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int u = 0; u < QM; ++u) {
+                At[(an + r) * IT + am + u] = an + r < Nl ? a[r][u] : 0.f;
+                a[r][u] = 0.f;
+            }
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < NAV; ++w) {
+            const int tv = tid + w * ST_T, c0 = (tv / (IT / 2)) * 4, m0 = (tv - (tv / (IT / 2)) * (IT / 2)) * 2;
+#pragma unroll 4
+            for (int n = 0; n < Nl; ++n) {
+                const f2_t ar = *reinterpret_cast<const f2_t*>(At + n * IT + m0);
+                const f4_t vr = *reinterpret_cast<const f4_t*>(vs + n * VS + c0);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    if (w == 0) us[u] += ar[u];
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) acc[w][u][c] += ar[u] * vr[c];
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < NAV; ++w) {
+        const int tv = tid + w * ST_T, c0 = (tv / (IT / 2)) * 4, m0 = (tv - (tv / (IT / 2)) * (IT / 2)) * 2;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int m = m0 + u;
+            if (m >= Ml) continue;
+            float* o = out_w + ((size_t)p * M + mb + m) * C;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (c0 + c < C) o[c0 + c] = acc[w][u][c];
+            if (w == 0 && c0 == 0 && out_u != nullptr) out_u[(size_t)p * M + mb + m] = us[u];
+        }
+    }
+}
+
+template <int KIND, int IT, int CM>
+static void launch_fwd_tiled(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P,
+                             int D, int N, int M, int C, hipStream_t st) {
+    const int mtiles = (M + IT - 1) / IT;
+    hipLaunchKernelGGL((direct_fwd_tiled_kernel<KIND, IT, CM>), dim3((unsigned)(P * mtiles)), dim3(ST_T), 0, st, q, k,
+                       v, out_w, out_u, D, N, M, C, mtiles);
+}
+
+template <int KIND>
+static void launch_fwd_tiled(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P,
+                             int D, int N, int M, int C, hipStream_t st) {
+    if (pad4(C) <= 32) launch_fwd_tiled<KIND, 64, 32>(q, k, v, out_w, out_u, P, D, N, M, C, st);
+    else if (pad4(C) <= 64) launch_fwd_tiled<KIND, 32, 64>(q, k, v, out_w, out_u, P, D, N, M, C, st);
+    else launch_fwd_tiled<KIND, 32, 128>(q, k, v, out_w, out_u, P, D, N, M, C, st);
+}
+
 int direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
                int P, int D, int N, int M, int C, hipStream_t st) {
     const size_t lds = direct_fwd_small_lds(D, N, M, C);
@@ -288,14 +342,9 @@ int direct_fwd(int kind, const float* q, const float* k, const float* v, float* 
                                out_u, D, N, M, C);
         return (int)hipGetLastError();
     }
-    const int mtiles = (M + DT - 1) / DT;
-    const dim3 grid((unsigned)(P * mtiles)), block(DTHREADS);
     StageTimer t("direct_fwd", st);
-#define QLKA_DIRECT(K, CTV) \
-    hipLaunchKernelGGL((direct_fwd_kernel<K, CTV>), grid, block, 0, st, q, k, v, out_w, out_u, D, N, M, C, mtiles)
-    if (kind == 0) { if (C <= 64) QLKA_DIRECT(0, 4); else QLKA_DIRECT(0, 8); }
-    else           { if (C <= 64) QLKA_DIRECT(1, 4); else QLKA_DIRECT(1, 8); }
-#undef QLKA_DIRECT
+    if (kind == 0) launch_fwd_tiled<0>(q, k, v, out_w, out_u, P, D, N, M, C, st);
+    else launch_fwd_tiled<1>(q, k, v, out_w, out_u, P, D, N, M, C, st);
     return (int)hipGetLastError();
 }
 
@@ -308,97 +357,6 @@ int direct_fwd(int kind, const float* q, const float* k, const float* v, float* 
 //   grad_k:  a = k, b = q, x = v, y = g_w, gu = g_u[m]  (other)
 //   weighted_sgn_sum (KeOps convention): grad_q with g for g_w, no g_u, tie 0, scale -1 (keops_backend.py:38-48).
 // tie = 0 is KeOps' sign(0) (keops_backend.py:40-41); tie = -1 is the reference CUDA walk's convention.
-// One workgroup per (p, tile of 64 outputs i) walks the j in tiles of 64: the 64 x 64 tile of <x_i, y_j> + gu is
-// formed 4 x 4 per thread from LDS rows into LDS, then lane i of wave w accumulates features d = w, w + 4, ... (16
-// per pass over 64 features) against b values read as LDS broadcasts.
-template <bool GU_OWN, int CT>
-__global__ __launch_bounds__(DTHREADS)
-void direct_sign_kernel(const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ x,
-                        const float* __restrict__ y, const float* __restrict__ gu, float* __restrict__ out,
-                        const float tie, const float scale, const int D, const int I, const int J, const int C,
-                        const int itiles)
-{
-    constexpr int CW = 16 * CT;
-    constexpr int DC = 64;                                // features per pass
-    __shared__ float xs[DT][CW];
-    __shared__ float ys[DT][CW];
-    __shared__ float bt[DT][DT + 1];                      // [i][j], stride 65: conflict-free column reads
-    __shared__ float bsm[DC][DT];                         // b[d0 + dd][j0 + j]
-
-    const int p = blockIdx.x / itiles, it = blockIdx.x - p * itiles;
-    const int i0 = it * DT, tid = threadIdx.x, ty = tid / 16, tx = tid % 16;
-    const int lane = tid % DT, wv = tid / DT;             // sign-sum mapping: output i = i0 + lane, d = d0 + wv + 4 jj
-    const float* ap = a + (size_t)p * D * I;
-    const float* bp = b + (size_t)p * D * J;
-    const float* xp = x + (size_t)p * I * C;
-    const float* yp = y + (size_t)p * J * C;
-    const float* gp = gu ? gu + (size_t)p * (GU_OWN ? I : J) : nullptr;
-
-    for (int e = tid; e < DT * CW; e += DTHREADS) {
-        const int r = e / CW, c = e - r * CW, i = i0 + r;
-        xs[r][c] = (i < I && c < C) ? xp[(size_t)i * C + c] : 0.f;
-    }
-    for (int d0 = 0; d0 < D; d0 += DC) {
-        float av[16], acc[16];
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-            const int d = d0 + wv + 4 * jj, i = i0 + lane;
-            av[jj] = (d < D && i < I) ? ap[(size_t)d * I + i] : 0.f;
-            acc[jj] = 0.f;
-        }
-        for (int j0 = 0; j0 < J; j0 += DT) {
-            __syncthreads();                              // previous readers of ys / bsm / bt are done (and xs written)
-            for (int e = tid; e < DT * CW; e += DTHREADS) {
-                const int r = e / CW, c = e - r * CW, j = j0 + r;
-                ys[r][c] = (j < J && c < C) ? yp[(size_t)j * C + c] : 0.f;
-            }
-            for (int e = tid; e < DC * DT; e += DTHREADS) {
-                const int dd = e / DT, jl = e - dd * DT, d = d0 + dd, j = j0 + jl;
-                bsm[dd][jl] = (d < D && j < J) ? bp[(size_t)d * J + j] : 0.f;
-            }
-            __syncthreads();
-            float bb[4][4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) bb[r][q] = 0.f;
-            for (int c = 0; c < C; ++c) {
-                float xv[4], yv[4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) { xv[r] = xs[4 * ty + r][c]; yv[r] = ys[4 * tx + r][c]; }
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) bb[r][q] += xv[r] * yv[q];
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int i = i0 + 4 * ty + r, j = j0 + 4 * tx + q;
-                    float g = 0.f;
-                    if (gp) g = GU_OWN ? (i < I ? gp[i] : 0.f) : (j < J ? gp[j] : 0.f);
-                    bt[4 * ty + r][4 * tx + q] = bb[r][q] + g;
-                }
-            __syncthreads();
-            const int nj = min(DT, J - j0);
-            for (int j = 0; j < nj; ++j) {
-                const float bv = bt[lane][j];
-#pragma unroll
-                for (int jj = 0; jj < 16; ++jj) {
-                    const float z = av[jj] - bsm[wv + 4 * jj][j];
-                    const float sg = z > 0.f ? 1.f : (z < 0.f ? -1.f : tie);
-                    acc[jj] += sg * bv;
-                }
-            }
-        }
-#pragma unroll
-        for (int jj = 0; jj < 16; ++jj) {
-            const int d = d0 + wv + 4 * jj, i = i0 + lane;
-            if (d < D && i < I) out[(size_t)p * D * I + (size_t)d * I + i] = scale * acc[jj];
-        }
-    }
-}
 
 // Small segments (padded I, J <= 128, C <= 64, the whole working set within 64 KB of LDS): one workgroup per p holds
 // everything in LDS, sized to the shape, with as many threads as the sign sums have 4-feature x 2-output blocks
@@ -558,7 +516,181 @@ static bool sign_small_fits(int D, int I, int J, int C) {
     return pad4(I) <= DS_MAX && pad4(J) <= DS_MAX && pad4(C) <= DS_CMAX && direct_sign_small_lds(D, I, J, C) <= DS_LDS_MAX;
 }
 
-bool direct_sign_fast(int D, int N, int M, int C) { return sign_small_fits(D, M, N, C) && sign_small_fits(D, N, M, C); }
+// Longer segments: one workgroup of 256 threads per (p, tile of IT outputs) walks the j in tiles of 64. The x rows
+// of the tile sit in LDS feature-major for the whole walk; per j tile the y rows ([j][c]), the b values of a chunk of
+// DCM features ([d][j]) and g_u come from registers loaded during the previous tile, G[j][i] (zero at padded i, j) is
+// formed 4 j x 2 i per thread from four-float reads, and each thread adds 64 j to its block of 4 features x 2 outputs
+// with the same sign step as the small kernel. IT = 32 (DCM = 64) in general, IT = 64 (DCM = 32) for D <= 32, so that
+// the 256 blocks of a feature chunk are one per thread; more features take further chunks (G formed again per chunk).
+// Staging: each thread owns one row of a tile and loads its columns part, part + TPR, ... through a raw buffer
+// descriptor that ends at the segment's end, so rows past the segment read 0 and every load is one base register plus
+// an immediate offset; LDS rows have a fixed stride (CM + 4 / 64 + 4 floats: no bank conflicts on the four-float reads)
+// so stores need no bounds. Columns of b past J read the next row: harmless, as G is 0 there and the sign step selects
+// rather than multiplies.
+template <bool GU_OWN, int TIE, int IT, int CM>      // CM: padded C at most (64 or 128)
+__global__ __launch_bounds__(ST_T)
+void direct_sign_tiled_kernel(const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ x,
+                              const float* __restrict__ y, const float* __restrict__ gu, float* __restrict__ out,
+                              const float tie, const float scale, const int D, const int I, const int J, const int C,
+                              const int itiles)
+{
+    constexpr int DCM = 2048 / IT;                        // features per chunk
+    constexpr int NI2 = IT / 2;                           // output pairs per tile
+    constexpr int YS = CM + 4, BS = ST_JT + 4;            // LDS row strides of y and b
+    constexpr int TPX = ST_T / IT, KX = CM / TPX;         // x tile: threads per row, columns per thread
+    constexpr int TPY = ST_T / ST_JT, KY = CM / TPY;      // y tile
+    constexpr int TPB = ST_T / DCM, KB = ST_JT / TPB;     // b chunk
+    __shared__ float xs[CM * IT];                         // [c][i]
+    __shared__ float ys[ST_JT * YS];                      // [j][c]
+    __shared__ float G[ST_JT * IT];                       // [j][i]
+    __shared__ float bs[DCM * BS];                        // [d][j]
+    __shared__ float gj[ST_JT], gi[IT];                   // g_u of the j tile / of the outputs
+
+    const int p = blockIdx.x / itiles, ib = (blockIdx.x - p * itiles) * IT, tid = threadIdx.x;
+    const int Il = min(IT, I - ib);
+    const float* gp = gu ? gu + (size_t)p * (GU_OWN ? I : J) : nullptr;
+    {
+        const int i = tid / TPX, c0 = tid - i * TPX;
+        const rsrc_t rx = make_rsrc(x + ((size_t)p * I + ib) * C, (uint32_t)(Il * C * 4));
+        float xv[KX];
+#pragma unroll
+        for (int k = 0; k < KX; ++k) {
+            const int c = c0 + TPX * k;
+            xv[k] = buf_load(rx, c < C ? (i * C + c) * 4 : (int)STAGE_OOB, 0);
+        }
+        if (GU_OWN && tid < IT) gi[tid] = (gp && tid < Il) ? gp[ib + tid] : 0.f;
+#pragma unroll
+        for (int k = 0; k < KX; ++k) xs[(c0 + TPX * k) * IT + i] = xv[k];
+    }
+    const int yj = tid / TPY, yc0 = tid - yj * TPY;
+    const int bd = tid / TPB, bj0 = tid - bd * TPB;
+    const int jtiles = (J + ST_JT - 1) / ST_JT, steps = jtiles * ((D + DCM - 1) / DCM);
+    float yv[KY], bv[KB], gn = 0.f;
+    auto load_step = [&](int s) {                         // step s: feature chunk s / jtiles, j tile s % jtiles
+        const int j0 = (s % jtiles) * ST_JT, d0 = (s / jtiles) * DCM;
+        const rsrc_t ry = make_rsrc(y + ((size_t)p * J + j0) * C, (uint32_t)(min(ST_JT, J - j0) * C * 4));
+#pragma unroll
+        for (int k = 0; k < KY; ++k) {
+            const int c = yc0 + TPY * k;
+            yv[k] = buf_load(ry, c < C ? (yj * C + c) * 4 : (int)STAGE_OOB, 0);
+        }
+        const rsrc_t rb = make_rsrc(b + ((size_t)p * D + d0) * J + j0, (uint32_t)(((D - d0) * J - j0) * 4));
+#pragma unroll
+        for (int k = 0; k < KB; ++k) bv[k] = buf_load(rb, (bd * J + bj0 + TPB * k) * 4, 0);
+        if (!GU_OWN) gn = (gp && tid < ST_JT && j0 + tid < J) ? gp[j0 + tid] : 0.f;
+    };
+    load_step(0);
+    const int dd0 = (tid / NI2) * 4, i0 = (tid - (tid / NI2) * NI2) * 2;
+    const int Cp = (C + 3) & ~3;
+    const float* ap = a + (size_t)p * D * I + ib;
+    float* op = out + (size_t)p * D * I + ib;
+    float av[4][2], acc[4][2];
+    for (int s = 0; s < steps; ++s) {
+        const int j0 = (s % jtiles) * ST_JT, d0 = (s / jtiles) * DCM;
+        if (j0 == 0)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int d = d0 + dd0 + r, i = i0 + q;
+                    av[r][q] = (d < D && i < Il) ? ap[(size_t)d * I + i] : 0.f;
+                    acc[r][q] = 0.f;
+                }
+        __syncthreads();                                  // the previous step's readers are done (and xs is written)
+#pragma unroll
+        for (int k = 0; k < KY; ++k) ys[yj * YS + yc0 + TPY * k] = yv[k];
+#pragma unroll
+        for (int k = 0; k < KB; ++k) bs[bd * BS + bj0 + TPB * k] = bv[k];
+        if (!GU_OWN && tid < ST_JT) gj[tid] = gn;
+        if (s + 1 < steps) load_step(s + 1);
+        __syncthreads();
+        const int Jl = min(ST_JT, J - j0);
+        for (int t = tid; t < (ST_JT / 4) * NI2; t += ST_T) {
+            const int jq = (t / NI2) * 4, ip = (t - (t / NI2) * NI2) * 2;
+            float g[4][2];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) { g[u][0] = 0.f; g[u][1] = 0.f; }
+            for (int c = 0; c < Cp; c += 4) {             // columns C .. Cp-1 of xs are 0
+                f4_t yr[4];
+                f2_t xr[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) yr[u] = *reinterpret_cast<const f4_t*>(ys + (jq + u) * YS + c);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) xr[k] = *reinterpret_cast<const f2_t*>(xs + (c + k) * IT + ip);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) { g[u][0] += yr[u][k] * xr[k][0]; g[u][1] += yr[u][k] * xr[k][1]; }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int j = jq + u;
+                f2_t row;
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int i = ip + q;
+                    row[q] = (i < Il && j < Jl) ? g[u][q] + (GU_OWN ? gi[i] : gj[j]) : 0.f;
+                }
+                *reinterpret_cast<f2_t*>(G + j * IT + ip) = row;
+            }
+        }
+        __syncthreads();
+#pragma unroll 2
+        for (int j = 0; j < ST_JT; j += 4) {              // padded j: G = 0, no contribution
+            f2_t gv[4];
+            f4_t bq[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) gv[u] = *reinterpret_cast<const f2_t*>(G + (j + u) * IT + i0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bq[r] = *reinterpret_cast<const f4_t*>(bs + (dd0 + r) * BS + j);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                float tg[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) tg[q] = TIE == 0 ? tie * gv[u][q] : 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int q = 0; q < 2; ++q) acc[r][q] += signed_term<TIE>(av[r][q], bq[r][u], gv[u][q], tg[q]);
+            }
+        }
+        if (j0 + ST_JT >= J)                              // last j tile of the chunk
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const int d = d0 + dd0 + r, i = i0 + q;
+                    if (d < D && i < Il) op[(size_t)d * I + i] = scale * acc[r][q];
+                }
+    }
+}
+
+template <bool GU_OWN, int IT, int CM>
+static void launch_sign_tiled(const float* a, const float* b, const float* x, const float* y, const float* gu,
+                              float* out, float tie, float scale, int P, int D, int I, int J, int C, hipStream_t st) {
+    const int itiles = (I + IT - 1) / IT;
+    const dim3 grid((unsigned)(P * itiles)), block(ST_T);
+    if (tie == -1.f)
+        hipLaunchKernelGGL((direct_sign_tiled_kernel<GU_OWN, -1, IT, CM>), grid, block, 0, st, a, b, x, y, gu, out,
+                           tie, scale, D, I, J, C, itiles);
+    else if (tie == 1.f)
+        hipLaunchKernelGGL((direct_sign_tiled_kernel<GU_OWN, 1, IT, CM>), grid, block, 0, st, a, b, x, y, gu, out,
+                           tie, scale, D, I, J, C, itiles);
+    else
+        hipLaunchKernelGGL((direct_sign_tiled_kernel<GU_OWN, 0, IT, CM>), grid, block, 0, st, a, b, x, y, gu, out,
+                           tie, scale, D, I, J, C, itiles);
+}
+
+template <bool GU_OWN>
+static void launch_sign_tiled(const float* a, const float* b, const float* x, const float* y, const float* gu,
+                              float* out, float tie, float scale, int P, int D, int I, int J, int C, hipStream_t st) {
+    const bool wide = pad4(D) <= 32;                      // 64-output tiles: the 8 feature quads x 32 pairs fill 256
+    const bool c64 = pad4(C) <= 64;
+    if (wide && c64) launch_sign_tiled<GU_OWN, 64, 64>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, st);
+    else if (wide) launch_sign_tiled<GU_OWN, 64, 128>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, st);
+    else if (c64) launch_sign_tiled<GU_OWN, 32, 64>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, st);
+    else launch_sign_tiled<GU_OWN, 32, 128>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, st);
+}
 
 int direct_sign(bool gu_own, const float* a, const float* b, const float* x, const float* y, const float* gu,
                 float* out, float tie, float scale, int P, int D, int I, int J, int C, hipStream_t st) {
@@ -569,15 +701,9 @@ int direct_sign(bool gu_own, const float* a, const float* b, const float* x, con
         else launch_sign_small<false>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, lds, st);
         return (int)hipGetLastError();
     }
-    const int itiles = (I + DT - 1) / DT;
-    const dim3 grid((unsigned)(P * itiles)), block(DTHREADS);
     StageTimer t("direct_sign", st);
-#define QLKA_SIGN(OWN, CTV) \
-    hipLaunchKernelGGL((direct_sign_kernel<OWN, CTV>), grid, block, 0, st, a, b, x, y, gu, out, tie, scale, D, I, J, \
-                       C, itiles)
-    if (gu_own) { if (C <= 64) QLKA_SIGN(true, 4); else QLKA_SIGN(true, 8); }
-    else        { if (C <= 64) QLKA_SIGN(false, 4); else QLKA_SIGN(false, 8); }
-#undef QLKA_SIGN
+    if (gu_own) launch_sign_tiled<true>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, st);
+    else launch_sign_tiled<false>(a, b, x, y, gu, out, tie, scale, P, D, I, J, C, st);
     return (int)hipGetLastError();
 }
 

@@ -111,7 +111,7 @@ def test_layer_workspace_and_validation(lib):
 def test_direct_cutoff_setter(lib):
     prev = lib.qlka_set_direct_max(0)
     try:
-        assert prev == 256                       # the default
+        assert prev == 512                       # the default
         assert lib.qlka_set_direct_max(100) == 0
         assert lib.qlka_set_direct_max(-1) < 0
         assert b"must be >= 0" in lib.qlka_last_error()
