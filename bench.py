@@ -9,7 +9,7 @@ step). `roofline` is for the dominant kernel, timed with hipEvents recorded by l
 inside the timed region. `cpu_baseline` times the reference's dense PyTorch path (restated in oracle/dense.py) on the
 host CPU on a bounded query sample of the same workload.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-layers]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-layers] [--no-configs]
 """
 
 import argparse
@@ -44,6 +44,86 @@ def make_inputs(dev, seed=0):
     k = rng.standard_normal((P, D, N), dtype=np.float32)
     v = rng.standard_normal((P, N, C), dtype=np.float32)
     return [torch.from_numpy(a).to(dev) for a in (q, k, v)]
+
+
+# The other BASELINE.json configurations, timed as extra fields of the JSON line (their workloads as BASELINE.json
+# states them; `value` stays the headline). Inputs are drawn on the GPU with a seeded torch generator in the same
+# distributions as the parity tests: N(0,1) * scale, or for configs[4] a per-element 50/50 mixture of 8 * N(0,1) and
+# 256 exact levels (heavy ties) with v ~ Student-t(3).
+CONFIGS = {
+    0: dict(P=32, D=64, N=600, C=64, kind="normal", scale=1.0, work="weighted_abs_sum_full fwd+bwd (autograd)"),
+    1: dict(P=512, D=32, N=65, C=32, kind="normal", scale=1.0, work="weighted_laplace_sum + weighted_abs_sum_full fwd"),
+    2: dict(P=12, D=64, N=8192, C=64, kind="normal", scale=2.0, work="weighted_laplace_sum fwd"),
+    4: dict(P=12, D=64, N=131072, C=64, kind="mixture", scale=1.0,
+            work="weighted_abs_sum_full fwd+bwd + weighted_laplace_sum fwd"),
+}
+
+
+def config_inputs(c, dev, seed=0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    P, D, N, C = c["P"], c["D"], c["N"], c["C"]
+
+    def side(shape):
+        if c["kind"] == "normal":
+            return torch.randn(shape, generator=g, device=dev) * c["scale"]
+        pick = torch.rand(shape, generator=g, device=dev) < 0.5
+        wide = torch.randn(shape, generator=g, device=dev) * 8.0
+        lvl = (torch.randint(0, 256, shape, generator=g, device=dev) - 128).float() / 16
+        return torch.where(pick, wide, lvl)
+
+    q, k = side((P, D, N)), side((P, D, N))
+    if c["kind"] == "normal":
+        v = torch.randn((P, N, C), generator=g, device=dev)
+    else:   # Student-t(3) = N(0,1) / sqrt(chi2(3) / 3)
+        z = torch.randn((P, N, C), generator=g, device=dev)
+        chi2 = torch.randn((3, P, N, C), generator=g, device=dev).square().sum(0)
+        v = z / torch.sqrt(chi2 / 3)
+    g_w = torch.randn((P, N, C), generator=g, device=dev)
+    g_u = torch.randn((P, N), generator=g, device=dev)
+    return q, k, v, g_w, g_u
+
+
+def config_timings(dev, reps=3):
+    """ms per call of each configuration's workload (median of reps after one warmup)."""
+    from weighted_abs_sum import weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+    out = {}
+    for i, c in CONFIGS.items():
+        q, k, v, g_w, g_u = config_inputs(c, dev)
+
+        def fwd_bwd():
+            tq, tk, tv = (t.detach().requires_grad_(True) for t in (q, k, v))
+            w, u = weighted_abs_sum_full(tq, tk, tv)
+            torch.autograd.backward([w, u], [g_w, g_u])
+
+        if i == 0:
+            fn = fwd_bwd
+        elif i == 1:
+            def fn():
+                weighted_laplace_sum(q, k, v)
+                weighted_abs_sum_full(q, k, v)
+        elif i == 2:
+            def fn():
+                weighted_laplace_sum(q, k, v)
+        else:
+            def fn():
+                fwd_bwd()
+                weighted_laplace_sum(q, k, v)
+        fn()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        out[f"configs[{i}]"] = {"ms": round(statistics.median(ts), 4), "work": c["work"],
+                                "shape": f"P={c['P']} D={c['D']} N=M={c['N']} C={c['C']}"}
+        del q, k, v, g_w, g_u
+        torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(seed=0, mq=256, reps=3):
@@ -105,6 +185,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-layers", action="store_true",
                     help="skip the attention-layer timings (layer_ms), e.g. to profile the two ops alone")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the timings of the other BASELINE configurations (config_ms)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -245,6 +327,10 @@ def main():
         "stages": {kk: round(vv["ms_per_launch"], 4) for kk, vv in stages.items()},
         "device": torch.cuda.get_device_name(dev),
     }
+    if not args.no_configs:
+        del q, k, v
+        torch.cuda.empty_cache()
+        out["config_ms"] = config_timings(dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

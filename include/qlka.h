@@ -31,11 +31,12 @@ const char* qlka_last_error(void);
 /* ABI version of this library. */
 int qlka_version(void);
 /*
- * Largest max(N, M) for which qlka_laplace_fwd, qlka_abs_fwd (path -1), qlka_abs_bwd and qlka_sgn_fwd use the dense
- * evaluation (the qlka_direct_* kernels, same results to fp32 rounding, same tie conventions) instead of sort + walk.
- * Default 512; 0 always sorts and walks. Process-wide; returns the previous value (or -QLKA_EINVAL for n < 0). The
- * C-level counterpart of the reference's set_keops_cutoff (Weighted_Abs_Sum/weighted_abs_sum/ops.py:21-25), which
- * picks the KeOps backend in Python.
+ * Base cutoff B of the dense evaluation (the qlka_direct_* kernels: same results to fp32 rounding, same tie
+ * conventions) in qlka_laplace_fwd, qlka_abs_fwd (path -1), qlka_abs_bwd and qlka_sgn_fwd, with L = max(N, M): the
+ * abs forward goes dense for L <= 2B, the Laplace forward for L <= B, the backward and the sgn sum for L <= B or for
+ * L <= 5B/4 when P * ceil(L / 32) >= 512. Default 512; 0 always sorts and walks. Process-wide; returns the previous
+ * value (or -QLKA_EINVAL for n < 0). The C-level counterpart of the reference's set_keops_cutoff
+ * (Weighted_Abs_Sum/weighted_abs_sum/ops.py:21-25), which picks the KeOps backend in Python.
  */
 int qlka_set_direct_max(int n);
 

@@ -33,12 +33,21 @@ int hip_status(int e, const char* where) {
 
 inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Up to this max(N, M) the dense evaluation (direct.hip) beats sort + scans + walk + reduce, whose cost there is
-// launch and per-segment overhead. Measured on MI355X (P = 48, D = C = 64 and P = 512, D = C = 32), dense / walk:
-// abs forward 0.30 / 0.39 at N = 512 and still faster at 1024; Laplace forward 0.51 / 0.67 at 512, about even at 768;
-// backward 0.50 / 0.75 at 512, even at 768. qlka_set_direct_max changes it (0: always sort + walk).
+// Where the dense evaluation (direct.hip) beats sort + scans + walk + reduce, whose cost at short segments is launch
+// and per-segment overhead. With B = the base cutoff (qlka_set_direct_max, default 512; 0: always sort + walk) and
+// L = max(N, M), measured on MI355X (P = 12, 32, 48, 512; D, C = 32, 64):
+//   abs forward      L <= 2B   (dense 0.28 vs walk 0.51 ms at L = 1024, P = 48)
+//   Laplace forward  L <= B    (its exp per term: about even at L = 700 for P = 12)
+//   backward, sgn    L <= B, or L <= 5B/4 when P * ceil(L / 32) >= 512 workgroups fill the GPU (at L = 600: dense
+//                    0.30 vs 0.44 ms at P = 32, but 0.22 vs 0.20 at P = 12)
 std::atomic<int> g_direct_max{512};
-inline bool use_direct(int N, int M) { return std::max(N, M) <= g_direct_max.load(std::memory_order_relaxed); }
+inline int64_t direct_base() { return g_direct_max.load(std::memory_order_relaxed); }
+inline bool dense_abs_fwd(int N, int M) { return std::max(N, M) <= 2 * direct_base(); }
+inline bool dense_laplace_fwd(int N, int M) { return std::max(N, M) <= direct_base(); }
+inline bool dense_sign(int P, int N, int M) {
+    const int64_t L = std::max(N, M), B = direct_base();
+    return L <= B || (4 * L <= 5 * B && (int64_t)P * ((L + 31) / 32) >= 512);
+}
 
 // Same limits and wording as check_qkv (Weighted_Abs_Sum/csrc/binding.cpp:79-83).
 int check_dims(int P, int D, int N, int M, int C) {
@@ -197,7 +206,7 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     const WsSpec spec = laplace_spec(P, D, N, M, C);
     if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
-    if (use_direct(N, M))
+    if (dense_laplace_fwd(N, M))
         return hip_status(direct_fwd(1, q, k, v, out_w, out_u, P, D, N, M, C, st), "laplace direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
@@ -238,7 +247,7 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
     const WsSpec spec = abs_fwd_spec(P, D, N, M, C, true);
     if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
-    if (path == -1 && use_direct(N, M))
+    if (path == -1 && dense_abs_fwd(N, M))
         return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
@@ -283,7 +292,7 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
     const WsSpec spec = abs_bwd_spec(P, D, N, M, C);
     if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
-    if (use_direct(N, M))     // the walks' convention: a tie counts -1 in both gradients
+    if (dense_sign(P, N, M))     // the walks' convention: a tie counts -1 in both gradients
         return hip_status(direct_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st),
                           "dense backward");
     const int S = P * D;
@@ -323,7 +332,7 @@ int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g,
     if (!q || !k || !v || !g || !out) return fail(QLKA_EINVAL, "q, k, v, g and out must be non-null");
     if (int e = check_ws(ws, ws_bytes_given, qlka_sgn_fwd_ws_bytes(P, D, N, M, C))) return e;
     hipStream_t st = (hipStream_t)stream;
-    if (use_direct(N, M))     // sgn(k - q) with a tie counted +1 == -(s(q - k) with a tie counted -1)
+    if (dense_sign(P, N, M))     // sgn(k - q) with a tie counted +1 == -(s(q - k) with a tie counted -1)
         return hip_status(direct_sign(true, q, k, g, v, nullptr, out, -1.f, -1.f, P, D, M, N, C, st), "dense sgn sum");
     const int S = P * D;
     SortedWs w = carve(ws, WsSpec{P, D, N, M, C, N, 0, false});

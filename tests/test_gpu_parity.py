@@ -81,8 +81,8 @@ def route(request):
 
 
 def _same_route(route, N, M):
-    if route == "walk" and max(N, M) > 512:
-        pytest.skip("above the dense cutoff both routes walk")
+    if route == "walk" and max(N, M) > 1024:
+        pytest.skip("above the dense cutoffs both routes walk")
 
 
 # ------------------------------------------------------------------------------------------------ sort / rank
