@@ -142,10 +142,35 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
     }
 }
 
-// One stable merge pass: runs of `width` become runs of 2*width. Each thread emits ITEMS consecutive outputs of one
-// pair after a merge-path search for its first output (A = left run wins ties).
+// One stable merge pass: runs of `width` become runs of 2*width (A = the left run wins ties). A workgroup owns
+// MERGE_TILE consecutive outputs of one pair of runs:
+//  1. two waves find where the tile starts and ends on the merge path (the number of A elements before each
+//     boundary) with a 64-way search per round (3 rounds for 64K-key runs instead of 16 dependent steps);
+//  2. the tile's A and B slices (MERGE_TILE keys + indices in total) are loaded into LDS, coalesced;
+//  3. each thread finds its MERGE_ITEMS outputs' start on the merge path inside LDS and merges them;
+//  4. the merged tile goes back through LDS and out coalesced (the final pass writes floats, perm and the inverse).
 constexpr int MERGE_ITEMS   = 8;
 constexpr int MERGE_THREADS = 256;
+constexpr int MERGE_TILE    = MERGE_ITEMS * MERGE_THREADS;
+
+// Smallest i in [lo, hi] with A[i] > B[o - i - 1] (true at i = hi by convention): the number of A elements among the
+// first o outputs of the stable merge. Runs in one wave, 64 candidates per round.
+__device__ int merge_path_wave(const uint32_t* __restrict__ A, const uint32_t* __restrict__ B, int o, int lo, int hi) {
+    const int lane = lane_id();
+    while (lo < hi) {
+        const int step = (hi - lo + WAVE - 1) / WAVE;
+        const int i = lo + lane * step;
+        const bool p = i >= hi || A[i] > B[o - i - 1];
+        const uint64_t m = __ballot(p);
+        if (m == 0) { lo = lo + (WAVE - 1) * step + 1; continue; }
+        const int f = __builtin_ctzll(m);
+        if (f == 0) { hi = lo; break; }
+        const int nlo = lo + (f - 1) * step + 1;
+        hi = min(hi, lo + f * step);
+        lo = nlo;
+    }
+    return lo;
+}
 
 __global__ __launch_bounds__(MERGE_THREADS)
 void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__ src_i,
@@ -153,41 +178,74 @@ void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__
                 float* __restrict__ out_keys, uint32_t* __restrict__ out_perm, uint32_t* __restrict__ out_inv,
                 const int seg_len, const int width, const int final_pass, const int blocks_per_seg)
 {
+    __shared__ uint32_t sk[MERGE_TILE];
+    __shared__ uint32_t si[MERGE_TILE];
+    __shared__ int split[2];
     const int seg = blockIdx.x / blocks_per_seg;
     const int blk = blockIdx.x - seg * blocks_per_seg;
-    const int o0  = (blk * MERGE_THREADS + threadIdx.x) * MERGE_ITEMS;          // position within the segment
-    if (o0 >= seg_len) return;
+    const int o0  = blk * MERGE_TILE;                     // tile start within the segment
+    if (o0 >= seg_len) return;                            // whole workgroup
+    const int tid = threadIdx.x;
     const size_t so = (size_t)seg * seg_len;
-
     const int pair0 = (o0 / (2 * width)) * (2 * width);
-    const int a0    = pair0;
-    const int la    = min(width, seg_len - a0);
-    const int b0    = a0 + la;
+    const int la    = min(width, seg_len - pair0);
+    const int b0    = pair0 + la;
     const int lb    = max(0, min(width, seg_len - b0));
-    const uint32_t* A  = src_k + so + a0;
+    const uint32_t* A  = src_k + so + pair0;
     const uint32_t* B  = src_k + so + b0;
-    const uint32_t* Ai = src_i + so + a0;
+    const uint32_t* Ai = src_i + so + pair0;
     const uint32_t* Bi = src_i + so + b0;
-
-    const int o = o0 - pair0;                              // output offset inside the pair
-    int lo = max(0, o - lb), hi = min(o, la);
-    while (lo < hi) {                                      // smallest i with A[i] > B[o - i - 1]
-        const int mid = (lo + hi) >> 1;
-        if (A[mid] <= B[o - mid - 1]) lo = mid + 1; else hi = mid;
+    const int ob = o0 - pair0, oe = min(ob + MERGE_TILE, la + lb);   // tile outputs [ob, oe) of the pair
+    const int w = tid / WAVE;
+    if (w < 2) {
+        const int o = w == 0 ? ob : oe;
+        const int i = merge_path_wave(A, B, o, max(0, o - lb), min(o, la));
+        if (lane_id() == 0) split[w] = i;
     }
-    int i = lo, j = o - lo;
-    const int n_out = min(MERGE_ITEMS, la + lb - o);
-    for (int t = 0; t < n_out; ++t) {
-        uint32_t key, idx;
-        if (i < la && (j >= lb || A[i] <= B[j])) { key = A[i]; idx = Ai[i]; ++i; }
-        else                                       { key = B[j]; idx = Bi[j]; ++j; }
-        const size_t dpos = so + o0 + t;
-        if (final_pass) {
-            out_keys[dpos] = ordered_to_float(key);
-            out_perm[dpos] = idx;
-            if (out_inv != nullptr) out_inv[so + idx] = (uint32_t)(o0 + t);
+    __syncthreads();
+    const int ia = split[0], na = split[1] - split[0];
+    const int jb = ob - ia, nb = (oe - split[1]) - jb;
+    const int n = na + nb;                                // == oe - ob
+    for (int e = tid; e < n; e += MERGE_THREADS) {
+        const bool fa = e < na;
+        sk[e] = fa ? A[ia + e] : B[jb + e - na];
+        si[e] = fa ? Ai[ia + e] : Bi[jb + e - na];
+    }
+    __syncthreads();
+    // this thread's outputs d .. d + MERGE_ITEMS - 1 of the tile: A part sk[0, na), B part sk[na, n)
+    const int d = min(tid * MERGE_ITEMS, n);
+    int lo = max(0, d - nb), hi = min(d, na);
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sk[mid] <= sk[na + d - mid - 1]) lo = mid + 1; else hi = mid;
+    }
+    int i = lo, j = d - lo;
+    uint32_t rk[MERGE_ITEMS], ri[MERGE_ITEMS];
+#pragma unroll
+    for (int t = 0; t < MERGE_ITEMS; ++t) {
+        const bool takea = i < na && (j >= nb || sk[i] <= sk[na + j]);
+        const int at = takea ? i : na + j;
+        rk[t] = sk[at];
+        ri[t] = si[at];
+        i += takea;
+        j += !takea;
+    }
+    __syncthreads();                                      // every read of the inputs in LDS is done
+#pragma unroll
+    for (int t = 0; t < MERGE_ITEMS; ++t)
+        if (d + t < n) { sk[d + t] = rk[t]; si[d + t] = ri[t]; }
+    __syncthreads();
+    if (final_pass) {
+        for (int e = tid; e < n; e += MERGE_THREADS) {
+            out_keys[so + o0 + e] = ordered_to_float(sk[e]);
+            out_perm[so + o0 + e] = si[e];
+            if (out_inv != nullptr) out_inv[so + si[e]] = (uint32_t)(o0 + e);
         }
-        else            { dst_k[dpos] = key; dst_i[dpos] = idx; }
+    } else {
+        for (int e = tid; e < n; e += MERGE_THREADS) {
+            dst_k[so + o0 + e] = sk[e];
+            dst_i[so + o0 + e] = si[e];
+        }
     }
 }
 
@@ -229,8 +287,7 @@ int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, uint32_t* out
     launch_lds<16, 16>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, nullptr, k0, i0, st);
     int err = (int)hipGetLastError();
     if (err) return err;
-    const int per_block = MERGE_THREADS * MERGE_ITEMS;
-    const int bps = (L + per_block - 1) / per_block;
+    const int bps = (L + MERGE_TILE - 1) / MERGE_TILE;
     dim3 grid((unsigned)((long)bps * S));
     for (int width = LDS_SORT_MAX; width < L; width *= 2) {
         const int fin = (2 * width >= L);
