@@ -10,6 +10,7 @@ inside the timed region. `cpu_baseline` times the reference's dense PyTorch path
 host CPU on a bounded query sample of the same workload.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-layers] [--no-configs]
+    python bench.py --profile-config I [--steps K]     (one other configuration alone, e.g. under rocprofv3)
 """
 
 import argparse
@@ -83,12 +84,14 @@ def config_inputs(c, dev, seed=0):
     return q, k, v, g_w, g_u
 
 
-def config_timings(dev, reps=3):
-    """ms per call of each configuration's workload (median of reps after one warmup)."""
+def config_timings(dev, reps=3, only=None):
+    """ms per call of each configuration's workload (median of reps after one warmup); only: one config index."""
     from weighted_abs_sum import weighted_abs_sum_full
     from weighted_laplace_sum import weighted_laplace_sum
     out = {}
     for i, c in CONFIGS.items():
+        if only is not None and i != only:
+            continue
         q, k, v, g_w, g_u = config_inputs(c, dev)
 
         def fwd_bwd():
@@ -187,6 +190,9 @@ def main():
                     help="skip the attention-layer timings (layer_ms), e.g. to profile the two ops alone")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the timings of the other BASELINE configurations (config_ms)")
+    ap.add_argument("--profile-config", type=int, default=None, choices=sorted(CONFIGS),
+                    help="only time this configuration's workload (--steps calls) and print its config_ms entry, "
+                         "e.g. under rocprofv3")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -199,6 +205,10 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 3}), flush=True)
+        return
+    if args.profile_config is not None:
+        dev = torch.device("cuda", 0)
+        print(json.dumps(config_timings(dev, reps=args.steps, only=args.profile_config)), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); this build has no multi-GPU path "
