@@ -83,7 +83,7 @@ size_t ws_part(const WsSpec& w, int i) {
         case 2: case 3: return align256(S * w.M * 4);
         case 4: return align256(std::max(seg_sort_scratch_bytes((int)S, w.N), seg_sort_scratch_bytes((int)S, w.M)));
         case 5: return align256(range_arrays_bytes((int)S, w.range_stream_max, w.C));
-        case 6: return w.slab_rows ? align256(S * w.slab_rows * (size_t)slab_stride(w.C) * 4) : 0;
+        case 6: return w.slab_rows ? align256(S * slab_rows(w.slab_rows) * (size_t)slab_stride(w.C) * 4) : 0;
         case 7: return (w.slab_rows && w.want_u) ? align256(S * w.slab_rows * 4) : 0;
         case 8: return (w.slab_rows && w.want_u) ? align256(S * w.M * 4) : 0;   // inverse perm of the q sort
     }

@@ -55,6 +55,36 @@ int fill_zero(float* p, size_t n, hipStream_t st);
 // Row stride (floats) of the per-feature contribution slab: C rounded up to whole 128-byte lines.
 __host__ __device__ inline int slab_stride(int C) { return (C + 31) / 32 * 32; }
 
+// Slab layout. One row of slab_stride(C) floats per (p, d, query m). The D features of a p form groups of
+// G = slab_group(D) features (2 when D is even, else 1); inside a group the rows are blocked by 64 queries:
+//   [p][d / G][m / 64][d % G][m % 64][row]
+// so the D-fold reduce reads G * 64 contiguous rows at a time. Measured at the headline shape against the plain
+// [p][d][m] layout (G = 1): the reduce reads faster (0.57 vs 0.64 ms) for slightly slower walk stores (+0.03 ms);
+// G = 4, 8, 16 and 32- or 128-query blocks come within 1% of G = 2. A feature has slab_rows(M) rows, and a
+// (p, group) region stays far below 2^31 bytes (32-bit buffer offsets).
+constexpr int SLAB_QB_LOG = 6;
+constexpr int SLAB_QB = 1 << SLAB_QB_LOG;
+constexpr int SLAB_GMAX = 2;
+__host__ __device__ inline int slab_group(int D) {
+    for (int g = D < SLAB_GMAX ? D : SLAB_GMAX; g > 1; --g)
+        if (D % g == 0) return g;
+    return 1;
+}
+__host__ __device__ inline int slab_rows(int M) { return (M + SLAB_QB - 1) / SLAB_QB * SLAB_QB; }
+// float offset of segment (p, d)'s first row, and the bytes from there to the end of its group's region
+__host__ __device__ inline size_t slab_seg_base(int p, int d, int D, int M, int CR) {
+    const int G = slab_group(D);
+    return ((size_t)p * D + (size_t)(d / G) * G) * slab_rows(M) * CR + (size_t)(d % G) * SLAB_QB * CR;
+}
+__host__ __device__ inline uint32_t slab_seg_bytes(int d, int D, int M, int CR) {
+    const int G = slab_group(D);
+    return (uint32_t)(((size_t)G * slab_rows(M) - (size_t)(d % G) * SLAB_QB) * CR * 4);
+}
+// byte offset of query m's row from its segment's first row (G = slab_group(D))
+__host__ __device__ inline int slab_row_off(int m, int G, int CR) {
+    return (((m >> SLAB_QB_LOG) * G) * SLAB_QB + (m & (SLAB_QB - 1))) * CR * 4;
+}
+
 // Per feature d of p: slab[(p*D + d)*M + m][c] = sum_n exp(-|k_n - q_m|) v[p,n,c] (row stride slab_stride(C)),
 // uslab[(p*D + d)*M + i] = sum_n exp(-|k_n - q_(i)|) for the i-th smallest query of the feature. keep (P, N) bytes,
 // nonzero = kept, or null: the sums run over the kept keys only.

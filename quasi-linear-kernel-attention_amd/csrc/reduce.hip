@@ -1,8 +1,8 @@
 // D-reduction of the per-feature contributions (the last step of stage 4).
 //
-// The walks leave one contribution row per (p, d, query) in a slab: slab[(p*D + d)*M + m][0:C] (row stride
-// slab_stride(C), whole 128-byte lines), written with plain row stores. Summing over the D features of a p here is a
-// streaming read of the slab, so the D-fold accumulation costs one HBM write and one HBM read per contribution
+// The walks leave one contribution row per (p, d, query) in a slab (row stride slab_stride(C), whole 128-byte lines;
+// blocked by 64 queries within pairs of features, see slab_group), written with plain row stores. Summing over the
+// D features of a p here reads, per block of 64 queries, G * 64 contiguous rows per feature group, so the D-fold accumulation costs one HBM write and one HBM read per contribution
 // instead of one fp32 atomic per channel (the L2 atomic units of the chip sustain about one 4-byte atomic per
 // channel per clock, which bounds an atomic emission at P*D*M*C atomics well above the slab's traffic time).
 //
@@ -51,15 +51,19 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
     const long pm = i / CQ;
     const int p = (int)(pm / M);
     const int m = (int)(pm - (long)p * M);
-    const size_t dstride = (size_t)M * CR;                           // floats between features
-    const float* src = slab + ((size_t)p * D * M + m) * CR;
+    // rows of query m, d = 0 .. D-1 in order: groups of G features, SLAB_QB * CR floats between features of a group
+    const int G = slab_group(D);
+    const size_t gstride = (size_t)G * slab_rows(M) * CR;
+    const size_t fstride = (size_t)SLAB_QB * CR;
+    const float* src = slab + (size_t)p * D * slab_rows(M) * CR + (size_t)slab_row_off(m, G, CR) / 4;
     if constexpr (V4) {
         typedef float f4 __attribute__((ext_vector_type(4)));
-        const f4* s4 = reinterpret_cast<const f4*>(src) + c;
-        const size_t d4 = dstride / 4;
         f4 a = {0.f, 0.f, 0.f, 0.f};
+        for (int g0 = 0; g0 < D; g0 += G) {
+            const f4* s4 = reinterpret_cast<const f4*>(src + (size_t)(g0 / G) * gstride) + c;
 #pragma unroll 8
-        for (int d = 0; d < D; ++d) a += __builtin_nontemporal_load(s4 + (size_t)d * d4);   // streamed once
+            for (int dd = 0; dd < G; ++dd) a += __builtin_nontemporal_load(s4 + (size_t)dd * (fstride / 4));
+        }
         reinterpret_cast<f4*>(out + pm * C)[c] = a;
         if constexpr (WITH_U) {
             const size_t base = (size_t)p * D * M;
@@ -73,8 +77,11 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
         }
     } else {
         float a = 0.f;
+        for (int g0 = 0; g0 < D; g0 += G) {
+            const float* sg = src + (size_t)(g0 / G) * gstride + c;
 #pragma unroll 8
-        for (int d = 0; d < D; ++d) a += src[(size_t)d * dstride + c];
+            for (int dd = 0; dd < G; ++dd) a += sg[(size_t)dd * fstride];
+        }
         out[pm * C + c] = a;
     }
 }

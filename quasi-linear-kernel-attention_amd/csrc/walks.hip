@@ -371,7 +371,8 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
     const float* qseg = qs + (size_t)s * M;
     const uint32_t* qpseg = qp + (size_t)s * M;
     const rsrc_t vr = make_rsrc(v + (size_t)p * N * C, (uint32_t)((size_t)N * C * 4));
-    const rsrc_t sr_ = make_rsrc(slab + (size_t)s * M * CR, (uint32_t)((size_t)M * CR * 4));
+    const int SG = slab_group(D);
+    const rsrc_t sr_ = make_rsrc(slab + slab_seg_base(p, s - p * D, D, M, CR), slab_seg_bytes(s - p * D, D, M, CR));
     float* useg = uslab + (size_t)s * M;
     const int CS = range_stride(C);
     const EmitLanes el_(CR);
@@ -490,7 +491,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
             const float eL = lft ? __expf(-(qv - (t > 0 ? kpv : kbefore))) : 0.f;
             const float eR = (t < nk) ? __expf(-(knv - qv)) : 0.f;
             if (act) useg[qb0 + l] = eL * (t > 0 ? l1p : L1in) + eR * r1n;
-            sm.par[l] = f4_t{__int_as_float(t * RS * 4), __int_as_float((int)(mq * CR * 4)), eL, eR};
+            sm.par[l] = f4_t{__int_as_float(t * RS * 4), __int_as_float(slab_row_off((int)mq, SG, CR)), eL, eR};
 
             float Lc[NV];
 #pragma unroll
@@ -954,7 +955,9 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
 
     const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
     const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
-    const rsrc_t sr_ = ROW ? make_rsrc(a.slab + (size_t)s * Mq * a.CR, (uint32_t)((size_t)Mq * a.CR * 4))
+    const int SG = slab_group(a.D);
+    const rsrc_t sr_ = ROW ? make_rsrc(a.slab + slab_seg_base(p, s - p * a.D, a.D, Mq, a.CR),
+                                       slab_seg_bytes(s - p * a.D, a.D, Mq, a.CR))
                            : make_rsrc(nullptr, 0);
     const rsrc_t gr_ = DOT ? make_rsrc(a.g + (size_t)p * Mq * C, (uint32_t)((size_t)Mq * C * 4))
                            : make_rsrc(nullptr, 0);
@@ -1063,7 +1066,8 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
                         if constexpr (ROW) {
                             const f4_t bw = *reinterpret_cast<const f4_t*>(reinterpret_cast<const char*>(sm.b) + ro);
                             const f4_t o = pr[u].z * av + bw - pr[u].w * wt4;
-                            if (j < j1 && el_.ok) buf_store4_stream(o, sr_, m * a.CR * 4 + el_.c4 * 4, 0);
+                            if (j < j1 && el_.ok)
+                                buf_store4_stream(o, sr_, slab_row_off(m, SG, a.CR) + el_.c4 * 4, 0);
                         }
                         if constexpr (DOT) {
                             const f4_t w2 = 2.f * av - wt4;
