@@ -126,9 +126,10 @@ int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, 
 // ---- overlap of the query side (q sort, range boundaries) with the key side (range summaries, scan)
 // The two sides read and write disjoint parts of the workspace and both need only the sorted keys. The key side runs
 // on the caller's stream, the query side on a side stream of the calling thread (one per device, created on first
-// use, default priority, non-blocking). Events order the side stream after the work already on the caller's stream,
-// and the caller's stream after the side stream's work. A host thread issues its calls in order, so reusing its two
-// events is safe; a fork / join through events is also how work on a captured stream reaches another stream.
+// uncaptured use, default priority, non-blocking, kept until the process ends). Events order the side stream after
+// the work already on the caller's stream, and the caller's stream after the side stream's work. A host thread issues
+// its calls in order, so reusing its two events is safe; a fork / join through events is also how work on a captured
+// stream reaches another stream.
 struct SideStream { hipStream_t s = nullptr; hipEvent_t fork = nullptr, join = nullptr; };
 
 hipError_t side_stream(hipStream_t st, SideStream** out) {
@@ -146,6 +147,11 @@ hipError_t side_stream(hipStream_t st, SideStream** out) {
     if (cur >= MAX_DEVICES) return hipSuccess;
     SideStream& sd = sides[cur];
     if (sd.s == nullptr) {
+        // Creating a stream inside a stream capture would invalidate it: a thread whose first call is captured runs
+        // that call in order on the caller's stream and creates its side stream with a later, uncaptured call.
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if ((e = hipStreamIsCapturing(st, &cs)) != hipSuccess) return e;
+        if (cs != hipStreamCaptureStatusNone) return hipSuccess;
         SideStream n;
         if ((e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming)) != hipSuccess) return e;

@@ -74,3 +74,36 @@ def test_graph_replays_equal_eager(dev, case):
             busy = torch.randn(1 << 20, device=dev)       # eager work between replays
             assert torch.isfinite(busy.sum())
             torch.cuda.synchronize(dev)
+
+
+def test_first_call_of_a_thread_captured(dev):
+    # A thread whose very first library call is captured has no side stream yet; creating one inside the capture would
+    # invalidate it, so that call runs in order on the captured stream. Checked on a fresh thread, against eager.
+    import threading
+    shape, fn = _cases()["abs_full_walk"]
+    args = _inputs(dev, *shape, seed=7)
+    with torch.no_grad():
+        eager = [t.clone() for t in _flat(fn(*args))]
+    result = {}
+
+    def body():
+        try:
+            torch.cuda.set_device(dev)
+            with torch.no_grad():
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    captured = _flat(fn(*args))
+                for _ in range(2):
+                    for t in captured:
+                        t.fill_(float("nan"))
+                    graph.replay()
+                    torch.cuda.synchronize(dev)
+                    result.setdefault("equal", []).append(all(torch.equal(a, b) for a, b in zip(captured, eager)))
+        except Exception as e:                            # reported on the test's thread
+            result["error"] = repr(e)
+
+    th = threading.Thread(target=body)
+    th.start()
+    th.join()
+    assert "error" not in result, result.get("error")
+    assert result["equal"] == [True, True]
