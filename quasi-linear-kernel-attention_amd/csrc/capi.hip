@@ -66,7 +66,7 @@ int check_dims(int P, int D, int N, int M, int C) {
 struct SortedWs {
     float* ks; uint32_t* kp; float* qs; uint32_t* qp;
     void* sort_scratch; RangeArrays ra;
-    float* slab; float* uslab; uint32_t* qinv;
+    float* slab; float* uslab; float* uq;
 };
 
 struct WsSpec {
@@ -85,7 +85,7 @@ size_t ws_part(const WsSpec& w, int i) {
         case 5: return align256(range_arrays_bytes((int)S, w.range_stream_max, w.C));
         case 6: return w.slab_rows ? align256(S * slab_rows(w.slab_rows) * (size_t)slab_stride(w.C) * 4) : 0;
         case 7: return (w.slab_rows && w.want_u) ? align256(S * w.slab_rows * 4) : 0;
-        case 8: return (w.slab_rows && w.want_u) ? align256(S * w.M * 4) : 0;   // inverse perm of the q sort
+        case 8: return (w.slab_rows && w.want_u) ? align256(S * w.M * 4) : 0;   // v == 1 terms in query order
     }
     return 0;
 }
@@ -105,7 +105,7 @@ SortedWs carve(void* ws, const WsSpec& w) {
     r.sort_scratch = part[4];
     r.ra = carve_range_arrays(part[5], w.P * w.D, w.range_stream_max, w.C);
     r.slab = (float*)part[6]; r.uslab = (float*)part[7];
-    r.qinv = ws_part(w, 8) ? (uint32_t*)part[8] : nullptr;
+    r.uq = ws_part(w, 8) ? (float*)part[8] : nullptr;
     return r;
 }
 
@@ -116,9 +116,9 @@ int check_ws(void* ws, size_t have, size_t need) {
 }
 
 int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, hipStream_t st) {
-    int e = seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st);
+    int e = seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st);
     if (e) return hip_status(e, "segmented sort of k");
-    e = seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, st);
+    e = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, st);
     if (e) return hip_status(e, "segmented sort of q");
     return QLKA_OK;
 }
@@ -216,18 +216,18 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
         return hip_status(direct_fwd(1, q, k, v, out_w, out_u, P, D, N, M, C, st), "laplace direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
     int e = fork_join(st,
         [&](hipStream_t s) {
             return hip_status(laplace_prepare(w.ks, w.kp, v, nullptr, P, D, N, C, w.ra, s), "laplace ranges"); },
         [&](hipStream_t s) {
-            if (int r = seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, s))
+            if (int r = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s))
                 return hip_status(r, "segmented sort of q");
             return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, 0.f, S, N, M, C, s), "query bounds"); });
     if (e) return e;
     e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, nullptr, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
     if (e) return hip_status(e, "laplace walk");
-    e = reduce_slabs(w.slab, w.uslab, w.qinv, out_w, out_u, P, D, M, C, st);
+    e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "laplace reduce");
 }
 
@@ -264,17 +264,17 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
     a.out_dot = nullptr; a.out_rank = nullptr;
     a.sign = 1.f; a.P = P; a.D = D; a.C = C;
     const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
     int e = fork_join(st,
         [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); },
         [&](hipStream_t s) {
-            if (int r = seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, s))
+            if (int r = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s))
                 return hip_status(r, "segmented sort of q");
             return hip_status(range_bounds(a, w.ra.qb, s), "query bounds"); });
     if (e) return e;
     e = abs_emit(a, mode, w.ra, st);
     if (e) return hip_status(e, "abs walk");
-    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qinv, out_w, out_u, P, D, M, C, st);
+    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, w.uq, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "abs reduce");
 }
 
@@ -321,7 +321,7 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
     b.out_dot = grad_k; b.sign = 1.f; b.P = P; b.D = D; b.C = C;
     e = abs_walk(b, g_u ? (ABS_ROW | ABS_DOT | ABS_DOTX2) : (ABS_ROW | ABS_DOT), w.ra, st);
     if (e) return hip_status(e, "grad_k/grad_v walk");
-    e = reduce_slabs(w.slab, nullptr, nullptr, grad_v, nullptr, P, D, N, C, st);
+    e = reduce_slabs(w.slab, nullptr, nullptr, nullptr, grad_v, nullptr, P, D, N, C, st);
     return hip_status(e, "grad_v reduce");
 }
 
@@ -453,9 +453,9 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
     const int S = P * D;
     LayerWs L = carve_layer(kind, ws, spec);
     SortedWs& w = L.op;
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, nullptr, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
     auto sort_q = [&](hipStream_t s) {
-        return hip_status(seg_sort(q, w.qs, w.qp, w.qinv, S, M, w.sort_scratch, s), "segmented sort of q");
+        return hip_status(seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s), "segmented sort of q");
     };
     int e = 0;
     if (kind == LAYER_ADD_LAPLACE) {
@@ -468,7 +468,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         if (e) return e;
         e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, keep, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
         if (e) return hip_status(e, "laplace walk");
-        e = reduce_slabs(w.slab, w.uslab, w.qinv, L.w[0], L.u[0], P, D, M, C, st);
+        e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[0], L.u[0], P, D, M, C, st);
         if (e) return hip_status(e, "laplace reduce");
     } else {
         AbsWalkArgs a{};
@@ -504,7 +504,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
             ra.qb = qbs[ev];
             e = abs_emit(a, mode, ra, st);
             if (e) return hip_status(e, "abs walk");
-            e = reduce_slabs(w.slab, w.uslab, w.qinv, L.w[ev], L.u[ev], P, D, M, C, st);
+            e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[ev], L.u[ev], P, D, M, C, st);
             if (e) return hip_status(e, "abs reduce");
         }
     }
@@ -541,7 +541,7 @@ int qlka_seg_sort(const float* keys, float* sorted, uint32_t* perm, int num_segs
     if ((int64_t)num_segs * seg_len > (int64_t)INT32_MAX) return fail(QLKA_EINVAL, "num_segs*seg_len must fit int32");
     if (!keys || !sorted || !perm) return fail(QLKA_EINVAL, "keys, sorted and perm must be non-null");
     if (int e = check_ws(ws, ws_bytes, qlka_seg_sort_ws_bytes(num_segs, seg_len))) return e;
-    return hip_status(seg_sort(keys, sorted, perm, nullptr, num_segs, seg_len, ws, (hipStream_t)stream),
+    return hip_status(seg_sort(keys, sorted, perm, num_segs, seg_len, ws, (hipStream_t)stream),
                       "segmented sort");
 }
 

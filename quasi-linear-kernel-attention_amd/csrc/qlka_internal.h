@@ -25,9 +25,8 @@ constexpr int LDS_SORT_MAX = 16384;
 
 // ---- sort.hip ----
 size_t seg_sort_scratch_bytes(int S, int L);
-// Stable ascending sort of S contiguous segments of length L; out_inv (optional) receives the inverse permutation
-// (out_inv[perm[i]] = i, the sorted position of each element). Returns a hipError_t value (0 on success).
-int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, uint32_t* out_inv, int S, int L, void* scratch,
+// Stable ascending sort of S contiguous segments of length L. Returns a hipError_t value (0 on success).
+int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch,
              hipStream_t st);
 
 // ---- walks.hip ----
@@ -99,9 +98,10 @@ int laplace_emit(const float* ks, const uint32_t* kp, const float* qs, const uin
                  const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
                  hipStream_t st);
 
-// D-reduction of the slabs: out[p,m,c] = sum_d slab[(p*D+d)*M + m][c]; out_u[p,m] = sum_d uslab[(p*D+d)*M + qinv]
-// with qinv[(p*D+d)*M + m] the sorted position of query m in feature d. out_u / uslab / qinv may be null.
-int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qinv, float* out, float* out_u,
+// D-reduction of the slabs: out[p,m,c] = sum_d slab rows of (p, d, m); out_u[p,m] = sum_d uslab[(p*D+d)*M + i] with
+// qperm[(p*D+d)*M + i] = m (uslab in sorted-query order, qperm the sort's permutation), put in query order in uq
+// (P*D*M floats of scratch) first. out_u / uslab / qperm / uq may be null (no out_u).
+int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, float* uq, float* out, float* out_u,
                  int P, int D, int M, int C, hipStream_t st);
 
 // Emission modes of the abs-family walk (bit set).

@@ -7,8 +7,8 @@
 // channel per clock, which bounds an atomic emission at P*D*M*C atomics well above the slab's traffic time).
 //
 // The v == 1 sums (out_u) are one scalar per (p, d, query). The walks write them in sorted-query order (coalesced);
-// u_gather sums, for each query, its D contributions at the query's sorted position in each feature (the inverse
-// permutation written by the sort), so every read of the index array is coalesced and only the scalar reads gather.
+// u_to_query puts each segment's scalars in query order through LDS (coalesced reads of them and of the sort's
+// permutation, coalesced writes), and the reduce then sums them like the slab rows.
 #include "qlka_common.h"
 #include "qlka_internal.h"
 
@@ -16,33 +16,48 @@ namespace qlka {
 
 constexpr int RT = 256;        // threads per block
 
+// uq[s][qperm[s][i]] = uslab[s][i] for every segment s: one workgroup per segment, through LDS when the segment
+// fits (16384 floats), else scattered straight to HBM (the segment's lines fill in one L2).
+constexpr int UT_T = 1024;
+constexpr int UT_CAP = 16384;
+__global__ __launch_bounds__(UT_T)
+void u_to_query(const float* __restrict__ uslab, const uint32_t* __restrict__ qperm, float* __restrict__ uq,
+                const int M)
+{
+    __shared__ float buf[UT_CAP];
+    const size_t base = (size_t)blockIdx.x * M;
+    const int tid = threadIdx.x;
+    if (M <= UT_CAP) {
+        for (int i = tid; i < M; i += UT_T) buf[qperm[base + i]] = uslab[base + i];
+        __syncthreads();
+        for (int i = tid; i < M; i += UT_T) uq[base + i] = buf[i];
+    } else {
+        for (int i = tid; i < M; i += UT_T) uq[base + qperm[base + i]] = uslab[base + i];
+    }
+}
+
 __global__ __launch_bounds__(RT)
-void u_gather(const float* __restrict__ uslab, const uint32_t* __restrict__ qinv, float* __restrict__ out_u,
-              const int P, const int D, const int M)
+void u_sum(const float* __restrict__ uq, float* __restrict__ out_u, const int P, const int D, const int M)
 {
     const long i = (long)blockIdx.x * RT + threadIdx.x;
     if (i >= (long)P * M) return;
     const int p = (int)(i / M);
     const int m = (int)(i - (long)p * M);
-    const size_t base = (size_t)p * D * M;
+    const float* src = uq + (size_t)p * D * M + m;
     float u = 0.f;
 #pragma unroll 8
-    for (int d = 0; d < D; ++d) {
-        const size_t so = base + (size_t)d * M;
-        u += uslab[so + qinv[so + m]];
-    }
+    for (int d = 0; d < D; ++d) u += src[(size_t)d * M];
     out_u[i] = u;
 }
 
 // One thread per (p, m, 4 channels) (V4, C % 4 == 0) or per (p, m, channel); features summed in order d = 0..D-1.
 // With WITH_U (V4 and C / 4 a power of two, so the C / 4 lanes of one query row are aligned within a wave) the row's
-// lanes also produce out_u: lane j sums features d = j, j + C/4, ... of the v == 1 contributions through the inverse
-// permutation and the partial sums are combined with lane shuffles (fixed order, deterministic).
+// lanes also produce out_u: lane j sums features d = j, j + C/4, ... of the v == 1 contributions (query order) and the
+// partial sums are combined with lane shuffles (fixed order, deterministic).
 template <bool V4, bool WITH_U>
 __global__ __launch_bounds__(RT)
 void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const int P, const int D, const int M,
-                 const int C, const int CR, const float* __restrict__ uslab, const uint32_t* __restrict__ qinv,
-                 float* __restrict__ out_u)
+                 const int C, const int CR, const float* __restrict__ uq, float* __restrict__ out_u)
 {
     const int CQ = V4 ? C / 4 : C;
     const long i = (long)blockIdx.x * RT + threadIdx.x;
@@ -66,12 +81,9 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
         }
         reinterpret_cast<f4*>(out + pm * C)[c] = a;
         if constexpr (WITH_U) {
-            const size_t base = (size_t)p * D * M;
+            const float* us = uq + (size_t)p * D * M + m;
             float u = 0.f;
-            for (int d = c; d < D; d += CQ) {
-                const size_t so = base + (size_t)d * M;
-                u += uslab[so + qinv[so + m]];
-            }
+            for (int d = c; d < D; d += CQ) u += us[(size_t)d * M];
             for (int off = CQ >> 1; off >= 1; off >>= 1) u += __shfl_xor(u, off, WAVE);
             if (c == 0) out_u[pm] = u;
         }
@@ -86,29 +98,33 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
     }
 }
 
-int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qinv, float* out, float* out_u,
+int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, float* uq, float* out, float* out_u,
                  int P, int D, int M, int C, hipStream_t st) {
     const int CR = slab_stride(C);
     const bool v4 = (C % 4) == 0;
     const int cq = C / 4;
     const bool fused_u = out_u && v4 && (cq & (cq - 1)) == 0;     // row lanes aligned within a wave
+    if (out_u) {
+        StageTimer t("u_to_query", st);
+        hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
+    }
     if (out_u && !fused_u) {
-        StageTimer t("u_gather", st);
+        StageTimer t("u_sum", st);
         const long n = (long)P * M;
-        hipLaunchKernelGGL(u_gather, dim3((unsigned)((n + RT - 1) / RT)), dim3(RT), 0, st, uslab, qinv, out_u, P, D, M);
+        hipLaunchKernelGGL(u_sum, dim3((unsigned)((n + RT - 1) / RT)), dim3(RT), 0, st, uq, out_u, P, D, M);
     }
     const long threads = (long)P * M * (v4 ? C / 4 : C);
     const unsigned blocks = (unsigned)((threads + RT - 1) / RT);
     StageTimer t("slab_reduce", st);
     if (fused_u)
-        hipLaunchKernelGGL((slab_reduce<true, true>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR, uslab,
-                           qinv, out_u);
+        hipLaunchKernelGGL((slab_reduce<true, true>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR, uq,
+                           out_u);
     else if (v4)
         hipLaunchKernelGGL((slab_reduce<true, false>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR,
-                           nullptr, nullptr, nullptr);
+                           nullptr, nullptr);
     else
         hipLaunchKernelGGL((slab_reduce<false, false>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR,
-                           nullptr, nullptr, nullptr);
+                           nullptr, nullptr);
     return (int)hipGetLastError();
 }
 

@@ -20,7 +20,6 @@ template <int WAVES, int ITEMS>
 __global__ __launch_bounds__(WAVES * WAVE)
 void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int run_len, const int runs_per_seg,
                     float* __restrict__ out_keys, uint32_t* __restrict__ out_perm,        // direct output (1 run)
-                    uint32_t* __restrict__ out_inv,                                        // optional inverse perm
                     uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_idx)       // run output (merging)
 {
     constexpr int THREADS = WAVES * WAVE;
@@ -128,12 +127,6 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
             out_keys[seg_off + i] = ordered_to_float(skey[i]);
             out_perm[seg_off + i] = (uint32_t)start + sidx[i];
         }
-        if (out_inv != nullptr) {                         // inverse permutation: built in LDS, written coalesced
-            __syncthreads();                              // every read of skey above is done
-            for (int i = tid; i < len; i += THREADS) skey[sidx[i]] = (uint32_t)i;
-            __syncthreads();
-            for (int i = tid; i < len; i += THREADS) out_inv[seg_off + i] = skey[i];
-        }
     } else {
         for (int i = tid; i < len; i += THREADS) {
             run_keys[seg_off + start + i] = skey[i];
@@ -148,7 +141,7 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
 //     boundary) with a 64-way search per round (3 rounds for 64K-key runs instead of 16 dependent steps);
 //  2. the tile's A and B slices (MERGE_TILE keys + indices in total) are loaded into LDS, coalesced;
 //  3. each thread finds its MERGE_ITEMS outputs' start on the merge path inside LDS and merges them;
-//  4. the merged tile goes back through LDS and out coalesced (the final pass writes floats, perm and the inverse).
+//  4. the merged tile goes back through LDS and out coalesced (the final pass writes floats and perm).
 constexpr int MERGE_ITEMS   = 8;
 constexpr int MERGE_THREADS = 256;
 constexpr int MERGE_TILE    = MERGE_ITEMS * MERGE_THREADS;
@@ -175,7 +168,7 @@ __device__ int merge_path_wave(const uint32_t* __restrict__ A, const uint32_t* _
 __global__ __launch_bounds__(MERGE_THREADS)
 void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__ src_i,
                 uint32_t* __restrict__ dst_k, uint32_t* __restrict__ dst_i,
-                float* __restrict__ out_keys, uint32_t* __restrict__ out_perm, uint32_t* __restrict__ out_inv,
+                float* __restrict__ out_keys, uint32_t* __restrict__ out_perm,
                 const int seg_len, const int width, const int final_pass, const int blocks_per_seg)
 {
     __shared__ uint32_t sk[MERGE_TILE];
@@ -239,7 +232,6 @@ void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__
         for (int e = tid; e < n; e += MERGE_THREADS) {
             out_keys[so + o0 + e] = ordered_to_float(sk[e]);
             out_perm[so + o0 + e] = si[e];
-            if (out_inv != nullptr) out_inv[so + si[e]] = (uint32_t)(o0 + e);
         }
     } else {
         for (int e = tid; e < n; e += MERGE_THREADS) {
@@ -250,11 +242,11 @@ void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__
 }
 
 template <int WAVES, int ITEMS>
-static void launch_lds(const float* in, int S, int L, int run_len, int runs, float* ok, uint32_t* op, uint32_t* oi,
+static void launch_lds(const float* in, int S, int L, int run_len, int runs, float* ok, uint32_t* op,
                        uint32_t* rk, uint32_t* ri, hipStream_t st) {
     StageTimer t("lds_radix_sort", st);
     hipLaunchKernelGGL((lds_radix_sort<WAVES, ITEMS>), dim3(S * runs), dim3(WAVES * WAVE), 0, st,
-                       in, L, run_len, runs, ok, op, oi, rk, ri);
+                       in, L, run_len, runs, ok, op, rk, ri);
 }
 
 size_t seg_sort_scratch_bytes(int S, int L) {
@@ -262,20 +254,20 @@ size_t seg_sort_scratch_bytes(int S, int L) {
     return 4 * (size_t)S * (size_t)L * sizeof(uint32_t);   // two (key, idx) ping-pong buffers
 }
 
-int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, uint32_t* out_inv, int S, int L, void* scratch,
+int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch,
              hipStream_t st) {
     if (S <= 0 || L <= 0) return 0;
     if (L <= LDS_SORT_MAX) {
         // smallest (waves, items) whose capacity covers L; more waves for long runs keep 16 items per thread max
-        if      (L <= 64)    launch_lds<1, 1>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else if (L <= 128)   launch_lds<1, 2>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else if (L <= 256)   launch_lds<1, 4>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else if (L <= 512)   launch_lds<2, 4>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else if (L <= 1024)  launch_lds<4, 4>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else if (L <= 2048)  launch_lds<8, 4>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else if (L <= 4096)  launch_lds<16, 4>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else if (L <= 8192)  launch_lds<16, 8>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
-        else                 launch_lds<16, 16>(in, S, L, L, 1, out_keys, out_perm, out_inv, nullptr, nullptr, st);
+        if      (L <= 64)    launch_lds<1, 1>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 128)   launch_lds<1, 2>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 256)   launch_lds<1, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 512)   launch_lds<2, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 1024)  launch_lds<4, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 2048)  launch_lds<8, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 4096)  launch_lds<16, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else if (L <= 8192)  launch_lds<16, 8>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
+        else                 launch_lds<16, 16>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
         return (int)hipGetLastError();
     }
     const size_t n = (size_t)S * (size_t)L;
@@ -284,7 +276,7 @@ int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, uint32_t* out
     uint32_t* k1 = i0 + n;
     uint32_t* i1 = k1 + n;
     const int runs = (L + LDS_SORT_MAX - 1) / LDS_SORT_MAX;
-    launch_lds<16, 16>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, nullptr, k0, i0, st);
+    launch_lds<16, 16>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
     int err = (int)hipGetLastError();
     if (err) return err;
     const int bps = (L + MERGE_TILE - 1) / MERGE_TILE;
@@ -292,7 +284,7 @@ int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, uint32_t* out
     for (int width = LDS_SORT_MAX; width < L; width *= 2) {
         const int fin = (2 * width >= L);
         StageTimer t("merge_runs", st);
-        hipLaunchKernelGGL(merge_runs, grid, dim3(MERGE_THREADS), 0, st, k0, i0, k1, i1, out_keys, out_perm, out_inv,
+        hipLaunchKernelGGL(merge_runs, grid, dim3(MERGE_THREADS), 0, st, k0, i0, k1, i1, out_keys, out_perm,
                            L, width, fin, bps);
         err = (int)hipGetLastError();
         if (err) return err;
