@@ -98,9 +98,15 @@ int laplace_emit(const float* ks, const uint32_t* kp, const float* qs, const uin
                  const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
                  hipStream_t st);
 
-// D-reduction of the slabs: out[p,m,c] = sum_d slab rows of (p, d, m); out_u[p,m] = sum_d uslab[(p*D+d)*M + i] with
-// qperm[(p*D+d)*M + i] = m (uslab in sorted-query order, qperm the sort's permutation), put in query order in uq
-// (P*D*M floats of scratch) first. out_u / uslab / qperm / uq may be null (no out_u).
+// Order of the per-feature v == 1 terms (uslab) the walks write: sorted-query order (coalesced stores, put in query
+// order through LDS before the reduce) when a segment's M terms fit one workgroup's LDS, else query order (one
+// 4-byte store per query; a segment's waves run on one XCD, so its lines fill in that L2).
+constexpr int U_LDS_CAP = 16384;
+__host__ __device__ inline bool u_query_order(int M) { return M > U_LDS_CAP; }
+
+// D-reduction of the slabs: out[p,m,c] = sum_d slab rows of (p, d, m); out_u[p,m] = sum_d of the v == 1 terms of
+// (p, d, m). uslab as the walks write it (see u_query_order); for sorted order it is put in query order in uq (P*D*M
+// floats of scratch) by the sort's permutation qperm first. out_u / uslab / qperm / uq may be null (no out_u).
 int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, float* uq, float* out, float* out_u,
                  int P, int D, int M, int C, hipStream_t st);
 

@@ -6,9 +6,10 @@
 // instead of one fp32 atomic per channel (the L2 atomic units of the chip sustain about one 4-byte atomic per
 // channel per clock, which bounds an atomic emission at P*D*M*C atomics well above the slab's traffic time).
 //
-// The v == 1 sums (out_u) are one scalar per (p, d, query). The walks write them in sorted-query order (coalesced);
-// u_to_query puts each segment's scalars in query order through LDS (coalesced reads of them and of the sort's
-// permutation, coalesced writes), and the reduce then sums them like the slab rows.
+// The v == 1 sums (out_u) are one scalar per (p, d, query). For segments of up to U_LDS_CAP queries the walks write
+// them in sorted-query order (coalesced) and u_to_query puts each segment's scalars in query order through LDS
+// (coalesced reads of them and of the sort's permutation, coalesced writes); longer segments arrive in query order.
+// The reduce then sums them like the slab rows.
 #include "qlka_common.h"
 #include "qlka_internal.h"
 
@@ -16,24 +17,18 @@ namespace qlka {
 
 constexpr int RT = 256;        // threads per block
 
-// uq[s][qperm[s][i]] = uslab[s][i] for every segment s: one workgroup per segment, through LDS when the segment
-// fits (16384 floats), else scattered straight to HBM (the segment's lines fill in one L2).
+// uq[s][qperm[s][i]] = uslab[s][i] for every segment s (M <= U_LDS_CAP): one workgroup per segment, through LDS.
 constexpr int UT_T = 1024;
-constexpr int UT_CAP = 16384;
 __global__ __launch_bounds__(UT_T)
 void u_to_query(const float* __restrict__ uslab, const uint32_t* __restrict__ qperm, float* __restrict__ uq,
                 const int M)
 {
-    __shared__ float buf[UT_CAP];
+    __shared__ float buf[U_LDS_CAP];
     const size_t base = (size_t)blockIdx.x * M;
     const int tid = threadIdx.x;
-    if (M <= UT_CAP) {
-        for (int i = tid; i < M; i += UT_T) buf[qperm[base + i]] = uslab[base + i];
-        __syncthreads();
-        for (int i = tid; i < M; i += UT_T) uq[base + i] = buf[i];
-    } else {
-        for (int i = tid; i < M; i += UT_T) uq[base + qperm[base + i]] = uslab[base + i];
-    }
+    for (int i = tid; i < M; i += UT_T) buf[qperm[base + i]] = uslab[base + i];
+    __syncthreads();
+    for (int i = tid; i < M; i += UT_T) uq[base + i] = buf[i];
 }
 
 __global__ __launch_bounds__(RT)
@@ -104,9 +99,11 @@ int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, f
     const bool v4 = (C % 4) == 0;
     const int cq = C / 4;
     const bool fused_u = out_u && v4 && (cq & (cq - 1)) == 0;     // row lanes aligned within a wave
-    if (out_u) {
+    if (out_u && !u_query_order(M)) {
         StageTimer t("u_to_query", st);
         hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
+    } else if (out_u) {
+        uq = const_cast<float*>(uslab);                   // already in query order
     }
     if (out_u && !fused_u) {
         StageTimer t("u_sum", st);

@@ -490,7 +490,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
             const bool lft = t > 0 || has_prev;
             const float eL = lft ? __expf(-(qv - (t > 0 ? kpv : kbefore))) : 0.f;
             const float eR = (t < nk) ? __expf(-(knv - qv)) : 0.f;
-            if (act) useg[qb0 + l] = eL * (t > 0 ? l1p : L1in) + eR * r1n;
+            if (act) useg[u_query_order(M) ? (int)mq : qb0 + l] = eL * (t > 0 ? l1p : L1in) + eR * r1n;
             sm.par[l] = f4_t{__int_as_float(t * RS * 4), __int_as_float(slab_row_off((int)mq, SG, CR)), eL, eR};
 
             float Lc[NV];
@@ -961,7 +961,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
                            : make_rsrc(nullptr, 0);
     const rsrc_t gr_ = DOT ? make_rsrc(a.g + (size_t)p * Mq * C, (uint32_t)((size_t)Mq * C * 4))
                            : make_rsrc(nullptr, 0);
-    float* useg = ONES ? a.uslab + (size_t)s * Mq : nullptr;        // v == 1 contributions, sorted order
+    float* useg = ONES ? a.uslab + (size_t)s * Mq : nullptr;        // v == 1 terms, order: u_query_order
 
     // Owned queries in blocks of 64. Lane i takes query i: its rank t inside the range, its distances and its scalar
     // outputs (v == 1 sum, rank, dot extras) from the lane-parallel prefixes; its record (row offset of rank t in the
@@ -991,7 +991,7 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
                 below = PU + (t > 0 ? kp_ : 0.f);
                 all = Ut;
             }
-            if (act) useg[qb0 + l] = 2.f * (lq * below + b1) - B1t - qm * all;
+            if (act) useg[u_query_order(Mq) ? (int)mq : qb0 + l] = 2.f * (lq * below + b1) - B1t - qm * all;
         }
         if constexpr (EXTRA) {
             float e = 0.f;
