@@ -54,7 +54,7 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
  * weighted_abs_sum forward; out_u == NULL gives the plain op, out_u != NULL the _full op.
  *   out_w[p,m,c] = sum_{d,n} |k[p,d,n] - q[p,d,m]| v[p,n,c],  out_u[p,m] = sum_{d,n} |k[p,d,n] - q[p,d,m]|
  * path: -1 auto, 0 global, 1 fused (the fused path exists for max(N, M) <= 4096 only, as in the reference). Under
- * auto, max(N, M) <= 256 runs the dense evaluation of qlka_direct_fwd (the workspace is then unused).
+ * auto, short segments run the dense evaluation of qlka_direct_fwd (see qlka_set_direct_max).
  * Replaces _ext.weighted_abs_sum_forward / weighted_abs_sum_full_forward (Weighted_Abs_Sum/csrc/binding.cpp:229-239).
  */
 size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C);
@@ -71,6 +71,25 @@ size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C);
 int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
                  float* grad_q, float* grad_k, float* grad_v,
                  int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Forward and backward that share their sorts. The reference's backward sorts k and q again
+ * (Weighted_Abs_Sum/csrc/binding.cpp:242-380 after :229-239); here a forward can leave the sorted k and q and their
+ * permutations in caller buffers (k_sorted, k_perm: P*D*N each; q_sorted, q_perm: P*D*M each) for the backward of
+ * the same inputs. qlka_abs_bwd_walks tells whether qlka_abs_bwd would sort and walk at this shape (1) or run the
+ * dense kernels (0), i.e. whether keeping the sorts pays; qlka_abs_fwd_keep computes what qlka_abs_fwd computes and
+ * sets *kept = 1 when it filled the four buffers (0: left untouched, the backward would not use them); after
+ * *kept = 1, qlka_abs_bwd_sorted with the same q, k, v computes what qlka_abs_bwd computes without sorting. Same
+ * workspace sizes as qlka_abs_fwd / qlka_abs_bwd.
+ */
+int qlka_abs_bwd_walks(int P, int N, int M);
+int qlka_abs_fwd_keep(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                      int P, int D, int N, int M, int C, int path, float* k_sorted, uint32_t* k_perm,
+                      float* q_sorted, uint32_t* q_perm, int* kept, void* ws, size_t ws_bytes, void* stream);
+int qlka_abs_bwd_sorted(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                        float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C,
+                        const float* k_sorted, const uint32_t* k_perm, const float* q_sorted, const uint32_t* q_perm,
+                        void* ws, size_t ws_bytes, void* stream);
 
 /*
  * weighted_sgn_sum: out[p,d,m] = sum_n sgn(k[p,d,n] - q[p,d,m]) <v[p,n,:], g[p,m,:]>, with a tie counted +1

@@ -239,12 +239,22 @@ size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     return ws_bytes(abs_fwd_spec(P, D, N, M, C, true));
 }
 
-int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
-                 int P, int D, int N, int M, int C, int path, void* ws, size_t ws_bytes_given, void* stream) {
+}  // extern "C"
+
+namespace {
+// Sorted k and q of one call, in caller-owned buffers (k_sorted / q_sorted as sorted keys, k_perm / q_perm as their
+// permutations), so that the backward of the same inputs can skip both sorts.
+struct Presorted { float* ks; uint32_t* kp; float* qs; uint32_t* qp; };
+
+int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P, int D, int N, int M,
+                 int C, int path, const Presorted* keep, int* kept, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
+    if (kept) *kept = 0;
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (path < -1 || path > 1) return fail(QLKA_EINVAL, "path must be -1 (auto), 0 (global) or 1 (fused)");
     if (!q || !k || !v || !out_w) return fail(QLKA_EINVAL, "q, k, v and out_w must be non-null");
+    if (keep && (!keep->ks || !keep->kp || !keep->qs || !keep->qp || !kept))
+        return fail(QLKA_EINVAL, "the sorted-array buffers and the kept flag must be non-null");
     // The reference's fused kernel only covers max(N, M) <= 4096 (Weighted_Abs_Sum/csrc/binding.cpp:177-188).
     if (path == 1 && std::max(N, M) > 4096)
         return fail(QLKA_EINVAL, "fused path pinned but unavailable: needs max(N,M) <= 4096 and the "
@@ -253,10 +263,17 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
     const WsSpec spec = abs_fwd_spec(P, D, N, M, C, true);
     if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
     hipStream_t st = (hipStream_t)stream;
-    if (path == -1 && dense_abs_fwd(N, M))
-        return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
+    const bool keep_sorts = keep && !dense_sign(P, N, M);   // the backward will walk: hand it the sorts
+    if (keep_sorts) { w.ks = keep->ks; w.kp = keep->kp; w.qs = keep->qs; w.qp = keep->qp; }
+    if (path == -1 && dense_abs_fwd(N, M)) {
+        if (keep_sorts) {
+            if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+            *kept = 1;
+        }
+        return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
+    }
     AbsWalkArgs a{};
     a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
     a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
@@ -272,11 +289,29 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
                 return hip_status(r, "segmented sort of q");
             return hip_status(range_bounds(a, w.ra.qb, s), "query bounds"); });
     if (e) return e;
+    if (keep_sorts) *kept = 1;
     e = abs_emit(a, mode, w.ra, st);
     if (e) return hip_status(e, "abs walk");
     e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, w.uq, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "abs reduce");
 }
+}  // namespace
+
+extern "C" {
+
+int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                 int P, int D, int N, int M, int C, int path, void* ws, size_t ws_bytes_given, void* stream) {
+    return abs_fwd_impl(q, k, v, out_w, out_u, P, D, N, M, C, path, nullptr, nullptr, ws, ws_bytes_given, stream);
+}
+
+int qlka_abs_fwd_keep(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                      int P, int D, int N, int M, int C, int path, float* k_sorted, uint32_t* k_perm,
+                      float* q_sorted, uint32_t* q_perm, int* kept, void* ws, size_t ws_bytes_given, void* stream) {
+    const Presorted keep{k_sorted, k_perm, q_sorted, q_perm};
+    return abs_fwd_impl(q, k, v, out_w, out_u, P, D, N, M, C, path, &keep, kept, ws, ws_bytes_given, stream);
+}
+
+int qlka_abs_bwd_walks(int P, int N, int M) { return (P > 0 && N > 0 && M > 0 && !dense_sign(P, N, M)) ? 1 : 0; }
 
 // --------------------------------------------------------------------------------------------------- abs backward
 static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
@@ -288,9 +323,12 @@ size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
     return ws_bytes(abs_bwd_spec(P, D, N, M, C));
 }
 
-int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
-                 float* grad_q, float* grad_k, float* grad_v,
-                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
+}  // extern "C"
+
+namespace {
+int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
+                 float* grad_k, float* grad_v, int P, int D, int N, int M, int C, const Presorted* pre, void* ws,
+                 size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
@@ -303,7 +341,8 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
                           "dense backward");
     const int S = P * D;
     SortedWs w = carve(ws, spec);
-    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+    if (pre) { w.ks = pre->ks; w.kp = pre->kp; w.qs = pre->qs; w.qp = pre->qp; }   // sorted by the forward
+    else if (int e = sort_both(q, k, w, S, N, M, st)) return e;
 
     // grad_q: stream = sorted k with rows v, queries = q, dotted with g_w (+ g_u * (2 rank - N))
     AbsWalkArgs a{};
@@ -323,6 +362,28 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
     if (e) return hip_status(e, "grad_k/grad_v walk");
     e = reduce_slabs(w.slab, nullptr, nullptr, nullptr, grad_v, nullptr, P, D, N, C, st);
     return hip_status(e, "grad_v reduce");
+}
+}  // namespace
+
+extern "C" {
+
+int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                 float* grad_q, float* grad_k, float* grad_v,
+                 int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
+    return abs_bwd_impl(q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, nullptr, ws, ws_bytes_given, stream);
+}
+
+int qlka_abs_bwd_sorted(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                        float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C,
+                        const float* k_sorted, const uint32_t* k_perm, const float* q_sorted, const uint32_t* q_perm,
+                        void* ws, size_t ws_bytes_given, void* stream) {
+    if (!k_sorted || !k_perm || !q_sorted || !q_perm) {
+        g_err.clear();
+        return fail(QLKA_EINVAL, "the sorted k / q arrays and their permutations must be non-null");
+    }
+    const Presorted pre{const_cast<float*>(k_sorted), const_cast<uint32_t*>(k_perm), const_cast<float*>(q_sorted),
+                        const_cast<uint32_t*>(q_perm)};
+    return abs_bwd_impl(q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, &pre, ws, ws_bytes_given, stream);
 }
 
 // -------------------------------------------------------------------------------------------------------- sgn sum

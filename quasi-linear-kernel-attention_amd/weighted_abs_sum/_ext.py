@@ -5,6 +5,8 @@ Outputs and the workspace are allocated from torch's caching allocator on q's de
 current stream of that device. Errors raise RuntimeError with the reference's TORCH_CHECK messages.
 """
 
+import ctypes
+
 import torch
 
 from qlka import _lib
@@ -80,6 +82,60 @@ def weighted_abs_sum_forward(q, k, v, path=-1):
 def weighted_abs_sum_full_forward(q, k, v, path=-1):
     """(out_w, out_u) with out_u[p,m] = sum_{n,d} |k - q|  (Weighted_Abs_Sum/csrc/binding.cpp:235-239)."""
     return _forward(q, k, v, path, full=True)
+
+
+def weighted_abs_sum_forward_keep(q, k, v, path, full):
+    """The forward of weighted_abs_sum(_full) (qlka_abs_fwd_keep) that also returns the sorted k and q with their
+    permutations when the backward at this shape sorts and walks (else None), for
+    weighted_abs_sum_backward_sorted. Not in the reference's pybind module: its backward sorts again."""
+    P, D, N, M, C = _check_qkv(q, k, v)
+    if not (-1 <= int(path) <= 1):
+        raise RuntimeError("path must be -1 (auto), 0 (global) or 1 (fused)")
+    lib = _lib.load()
+    dev = q.device
+    with torch.cuda.device(dev):
+        out = torch.empty((P, M, C), dtype=q.dtype, device=dev)
+        out_u = torch.empty((P, M), dtype=q.dtype, device=dev) if full else None
+        srt = None
+        if lib.qlka_abs_bwd_walks(P, N, M):
+            srt = (torch.empty((P, D, N), dtype=q.dtype, device=dev),
+                   torch.empty((P, D, N), dtype=torch.int32, device=dev),
+                   torch.empty((P, D, M), dtype=q.dtype, device=dev),
+                   torch.empty((P, D, M), dtype=torch.int32, device=dev))
+        kept = ctypes.c_int(0)
+        ws = _lib.workspace(lib.qlka_abs_fwd_ws_bytes(P, D, N, M, C), dev)
+        if srt is None:
+            _lib.check(lib.qlka_abs_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(out_u),
+                                        P, D, N, M, C, int(path), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev)))
+        else:
+            _lib.check(lib.qlka_abs_fwd_keep(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out), _lib.ptr(out_u),
+                                             P, D, N, M, C, int(path), *(_lib.ptr(t) for t in srt),
+                                             ctypes.byref(kept), _lib.ptr(ws), ws.numel(), _lib.stream_of(dev)))
+    return out, out_u, (srt if kept.value else None)
+
+
+def weighted_abs_sum_backward_sorted(q, k, v, g_w, g_u, srt):
+    """The backward of weighted_abs_sum(_full) over the sorts a weighted_abs_sum_forward_keep of the same q, k, v
+    left (qlka_abs_bwd_sorted). g_u may be None. Not in the reference's pybind module."""
+    P, D, N, M, C = _check_qkv(q, k, v)
+    _check_grad("g_w", g_w, q, (P, M, C))
+    if g_u is not None:
+        _check_grad("g_u", g_u, q, (P, M))
+    ks, kp, qs, qp = srt
+    if not (ks.shape == (P, D, N) and kp.shape == (P, D, N) and qs.shape == (P, D, M) and qp.shape == (P, D, M)):
+        raise RuntimeError("sorted arrays do not match q and k")
+    lib = _lib.load()
+    dev = q.device
+    with torch.cuda.device(dev):
+        grad_q = torch.empty((P, D, M), dtype=q.dtype, device=dev)
+        grad_k = torch.empty((P, D, N), dtype=q.dtype, device=dev)
+        grad_v = torch.empty((P, N, C), dtype=q.dtype, device=dev)
+        ws = _lib.workspace(lib.qlka_abs_bwd_ws_bytes(P, D, N, M, C), dev)
+        _lib.check(lib.qlka_abs_bwd_sorted(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g_w), _lib.ptr(g_u),
+                                           _lib.ptr(grad_q), _lib.ptr(grad_k), _lib.ptr(grad_v), P, D, N, M, C,
+                                           *(_lib.ptr(t) for t in srt), _lib.ptr(ws), ws.numel(),
+                                           _lib.stream_of(dev)))
+    return grad_q, grad_k, grad_v
 
 
 def weighted_abs_sum_direct_forward(q, k, v, full):

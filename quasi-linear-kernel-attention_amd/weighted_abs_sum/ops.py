@@ -24,6 +24,18 @@ _PATH = {"cuda": -1, "cuda-fused": 1, "cuda-global": 0, "keops": _DIRECT}
 KEOPS_CUTOFF = 512
 
 
+# Keep the forward's sorted k and q for the backward (the reference's backward sorts again): costs 8*P*D*(N+M)
+# bytes per differentiable call until its backward runs, saves two segmented sorts per backward.
+KEEP_SORTS = True
+
+
+def set_keep_sorts(flag):
+    """Keep (True, default) or drop (False) the forward's sorts for the backward of differentiable calls."""
+    global KEEP_SORTS
+    KEEP_SORTS = bool(flag)
+    return KEEP_SORTS
+
+
 def set_keops_cutoff(n):
     """Set the max(N,M) below which backend='auto' uses the keops route (0 disables)."""
     global KEOPS_CUTOFF
@@ -43,53 +55,60 @@ def _resolve(backend, q, k, v):
     return "cuda"
 
 
+def _forward(ctx, q, k, v, path, full):
+    """Shared forward of the two Functions: the dense route for "keops", else the native ops, keeping the sorts
+    for the backward when a gradient is wanted and KEEP_SORTS is set."""
+    if path == _DIRECT:
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    ctx.set_materialize_grads(False)
+    ctx.direct = path == _DIRECT
+    srt = None
+    if ctx.direct:
+        out, out_u = _C.weighted_abs_sum_direct_forward(q, k, v, full=full)
+    elif KEEP_SORTS and any(ctx.needs_input_grad[:3]):
+        out, out_u, srt = _C.weighted_abs_sum_forward_keep(q, k, v, path, full)
+    elif full:
+        out, out_u = _C.weighted_abs_sum_full_forward(q, k, v, path)
+    else:
+        out, out_u = _C.weighted_abs_sum_forward(q, k, v, path), None
+    ctx.sorted = srt is not None
+    ctx.save_for_backward(q, k, v, *(srt or ()))
+    return out, out_u
+
+
+def _backward(ctx, g_w, g_u):
+    q, k, v = ctx.saved_tensors[:3]
+    if ctx.direct:          # the KeOps gradient: sign(0) = 0
+        return _C.weighted_abs_sum_direct_backward(q, k, v, g_w, g_u, tie=0.0)
+    if ctx.sorted:
+        return _C.weighted_abs_sum_backward_sorted(q, k, v, g_w, g_u, ctx.saved_tensors[3:])
+    if g_u is None:         # out_u unused -> the cheaper plain backward
+        return _C.weighted_abs_sum_backward(q, k, v, g_w)
+    return _C.weighted_abs_sum_full_backward(q, k, v, g_w, g_u)
+
+
 class _WeightedAbsSum(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, path):
-        if path == _DIRECT:
-            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        ctx.save_for_backward(q, k, v)
-        ctx.set_materialize_grads(False)
-        ctx.direct = path == _DIRECT
-        if ctx.direct:
-            return _C.weighted_abs_sum_direct_forward(q, k, v, full=False)[0]
-        return _C.weighted_abs_sum_forward(q, k, v, path)
+        return _forward(ctx, q, k, v, path, full=False)[0]
 
     @staticmethod
     def backward(ctx, g_w):
-        q, k, v = ctx.saved_tensors
-        if ctx.direct:      # the KeOps gradient: sign(0) = 0
-            grad_q, grad_k, grad_v = _C.weighted_abs_sum_direct_backward(q, k, v, g_w.contiguous(), None, tie=0.0)
-        else:
-            grad_q, grad_k, grad_v = _C.weighted_abs_sum_backward(q, k, v, g_w.contiguous())
+        grad_q, grad_k, grad_v = _backward(ctx, g_w.contiguous(), None)
         return grad_q, grad_k, grad_v, None
 
 
 class _WeightedAbsSumFull(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, path):
-        if path == _DIRECT:
-            q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-        ctx.save_for_backward(q, k, v)
-        ctx.set_materialize_grads(False)
-        ctx.direct = path == _DIRECT
-        if ctx.direct:
-            return _C.weighted_abs_sum_direct_forward(q, k, v, full=True)
-        return _C.weighted_abs_sum_full_forward(q, k, v, path)
+        return _forward(ctx, q, k, v, path, full=True)
 
     @staticmethod
     def backward(ctx, g_w, g_u):
-        q, k, v = ctx.saved_tensors
+        q, v = ctx.saved_tensors[0], ctx.saved_tensors[2]
         if g_w is None:
             g_w = torch.zeros(q.shape[0], q.shape[2], v.shape[2], device=q.device, dtype=q.dtype)
-        if ctx.direct:      # the KeOps gradient: sign(0) = 0
-            grad_q, grad_k, grad_v = _C.weighted_abs_sum_direct_backward(
-                q, k, v, g_w.contiguous(), None if g_u is None else g_u.contiguous(), tie=0.0)
-        elif g_u is None:   # out_u unused -> the cheaper plain backward
-            grad_q, grad_k, grad_v = _C.weighted_abs_sum_backward(q, k, v, g_w.contiguous())
-        else:
-            grad_q, grad_k, grad_v = _C.weighted_abs_sum_full_backward(
-                q, k, v, g_w.contiguous(), g_u.contiguous())
+        grad_q, grad_k, grad_v = _backward(ctx, g_w.contiguous(), None if g_u is None else g_u.contiguous())
         return grad_q, grad_k, grad_v, None
 
 

@@ -118,3 +118,17 @@ def test_direct_cutoff_setter(lib):
         assert lib.qlka_set_direct_max(prev) == 100   # a rejected value leaves the cutoff alone
     finally:
         lib.qlka_set_direct_max(prev)
+
+
+def test_keep_sorts_entries_validate(lib):
+    import ctypes
+    kept = ctypes.c_int(7)
+    # null sorted-array buffers are rejected before any launch, and *kept is cleared
+    rc = lib.qlka_abs_fwd_keep(1, 1, 1, 1, None, 1, 1, 8, 8, 4, -1, None, None, None, None, ctypes.byref(kept),
+                               None, 0, None)
+    assert rc != 0 and kept.value == 0
+    assert b"non-null" in lib.qlka_last_error()
+    rc = lib.qlka_abs_bwd_sorted(1, 1, 1, 1, None, 1, 1, 1, 1, 1, 8, 8, 4, None, None, None, None, None, 0, None)
+    assert rc != 0 and b"non-null" in lib.qlka_last_error()
+    assert lib.qlka_abs_bwd_walks(12, 16384, 16384) == 1
+    assert lib.qlka_abs_bwd_walks(512, 65, 65) == 0

@@ -226,6 +226,41 @@ def test_autograd_through_ops(dev, full):
     _assert_rel(_np(tv.grad), wv, nv, "autograd grad_v")
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 1500, 1300, 16),   # forward and backward walk
+                                   (2, 3, 800, 700, 12)])     # dense forward, walking backward: sorts kept anyway
+@pytest.mark.parametrize("full", [False, True])
+def test_autograd_keeps_sorts_for_backward(dev, shape, full):
+    # The "cuda" forward leaves its sorted k and q for the backward (ops.KEEP_SORTS): the gradients must equal those
+    # of a backward that sorts again, bit for bit, and the oracle's (a tie counts -1).
+    from weighted_abs_sum import ops, weighted_abs_sum, weighted_abs_sum_full
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape), kind="ties")
+    rng = np.random.default_rng(12)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    grads = {}
+    try:
+        for keep in (True, False):
+            ops.set_keep_sorts(keep)
+            tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+            if full:
+                w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+                loss = (w * _t(g_w, dev)).sum() + (u * _t(g_u, dev)).sum()
+            else:
+                w = weighted_abs_sum(tq, tk, tv, backend="cuda")
+                loss = (w * _t(g_w, dev)).sum()
+            loss.backward()
+            grads[keep] = [_np(t.grad) for t in (tq, tk, tv)]
+    finally:
+        ops.set_keep_sorts(True)
+    for name, a, b in zip(("grad_q", "grad_k", "grad_v"), grads[True], grads[False]):
+        np.testing.assert_array_equal(a, b, err_msg=f"{name}: kept sorts vs sorting again")
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u if full else None)
+    _assert_rel(grads[True][0], wq, nq, "kept-sorts grad_q")
+    _assert_rel(grads[True][1], wk, nk, "kept-sorts grad_k")
+    _assert_rel(grads[True][2], wv, nv, "kept-sorts grad_v")
+
+
 def test_full_backward_only_u(dev):
     # out_w unused: g_w is None inside the autograd Function and becomes zeros (ops.py:99-101)
     from weighted_abs_sum import weighted_abs_sum_full
