@@ -32,7 +32,7 @@ METRIC = "query-feature sums/sec (B·H·N·D) at N=16384 D=64 fp32; achieved HBM
 HBM_PEAK_GBS = 8000.0
 P, D, N, M, C = 12, 64, 16384, 16384, 64
 
-# Algorithmic bytes per (p, d, m) query-feature unit of one op call at N = M (B_scan of the hot-path survey):
+# Algorithmic bytes per (p, d, m) query-feature unit of one op call at N = M ("B_scan"):
 # read the key and query segments once (4 N + 4 M per (p, d)), stream v once in sorted order (4 N C), emit one fp32
 # contribution per (query, channel) (4 M C) plus out_u (4 M); divided by the M units of a (p, d) segment.
 def bscan_bytes_per_unit(n, m, c, with_u=True):
@@ -212,7 +212,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); this build has no multi-GPU path "
-              "(sharding over P or over d is described in DESIGN.md).", file=sys.stderr)
+              "(the ops would shard over P = B*H, or over the features d with one reduce-scatter of the partial outputs).",
+              file=sys.stderr)
         sys.exit(2)
 
     from qlka import _lib
