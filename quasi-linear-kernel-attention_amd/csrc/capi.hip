@@ -56,7 +56,7 @@ int check_dims(int P, int D, int N, int M, int C) {
     if (C < 1 || C > 128) return fail(QLKA_EINVAL, "C (v.size(2)) must be in [1, 128]");
     if (N > 131072 || M > 131072) return fail(QLKA_EINVAL, "N and M must be <= 131072");
     if ((int64_t)P * D * std::max(N, M) > (int64_t)INT32_MAX)
-        return fail(QLKA_EINVAL, "P*D*max(N,M) must fit int32 (cub sort offsets)");
+        return fail(QLKA_EINVAL, "P*D*max(N,M) must fit int32 (element offsets)");
     return QLKA_OK;
 }
 
@@ -121,6 +121,12 @@ int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, 
     e = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, st);
     if (e) return hip_status(e, "segmented sort of q");
     return QLKA_OK;
+}
+
+// The query side of a forward walk that keeps no sorts: q grouped by owning key range, with the range bounds, in one
+// pass (the walks take grouped queries as well as sorted ones).
+static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int M, int C, hipStream_t st) {
+    return hip_status(group_queries(w.ks, q, w.qs, w.qp, w.ra.qb, qshift, S, N, M, C, st), "query grouping");
 }
 
 // ---- overlap of the query side (q sort, range boundaries) with the key side (range summaries, scan)
@@ -217,15 +223,10 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     const int S = P * D;
     SortedWs w = carve(ws, spec);
     if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
-    int e = fork_join(st,
-        [&](hipStream_t s) {
-            return hip_status(laplace_prepare(w.ks, w.kp, v, nullptr, P, D, N, C, w.ra, s), "laplace ranges"); },
-        [&](hipStream_t s) {
-            if (int r = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s))
-                return hip_status(r, "segmented sort of q");
-            return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, 0.f, S, N, M, C, s), "query bounds"); });
+    if (int e = group_q(q, w, 0.f, S, N, M, C, st)) return e;
+    int e = hip_status(laplace_prepare(w.ks, w.kp, v, P, D, N, C, w.ra, st), "laplace ranges");
     if (e) return e;
-    e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, nullptr, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+    e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
     if (e) return hip_status(e, "laplace walk");
     e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, out_w, out_u, P, D, M, C, st);
     return hip_status(e, "laplace reduce");
@@ -282,12 +283,17 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
     a.sign = 1.f; a.P = P; a.D = D; a.C = C;
     const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
     if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
-    int e = fork_join(st,
-        [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); },
-        [&](hipStream_t s) {
+    auto key_side = [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); };
+    int e = 0;
+    if (!keep_sorts) {
+        e = group_q(q, w, 0.f, S, N, M, C, st);
+        if (!e) e = key_side(st);
+    } else {
+        e = fork_join(st, key_side, [&](hipStream_t s) {
             if (int r = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s))
                 return hip_status(r, "segmented sort of q");
             return hip_status(range_bounds(a, w.ra.qb, s), "query bounds"); });
+    }
     if (e) return e;
     if (keep_sorts) *kept = 1;
     e = abs_emit(a, mode, w.ra, st);
@@ -451,6 +457,7 @@ struct LayerWs {
     float* w[3]; float* u[3];
     void* pre; int* qb[2];
     float* qt;
+    float* kmask;
 };
 
 size_t layer_part(int kind, const WsSpec& s, int i) {
@@ -462,13 +469,14 @@ size_t layer_part(int kind, const WsSpec& s, int i) {
         case 2: return kind == LAYER_ADD_RIESZ ? align256(riesz_prefix_bytes(s.P, s.N, s.C)) : 0;
         case 3: return kind == LAYER_ADD_BUMP
                        ? 2 * align256((size_t)s.P * s.D * range_count(s.N, s.C) * sizeof(int)) : 0;
+        case 4: return kind == LAYER_ADD_LAPLACE ? align256((size_t)s.P * s.D * s.N * 4) : 0;   // masked keys
     }
     return 0;
 }
 
 size_t layer_ws_bytes(int kind, const WsSpec& s) {
     size_t b = 0;
-    for (int i = 0; i < 4; ++i) b += layer_part(kind, s, i);
+    for (int i = 0; i < 5; ++i) b += layer_part(kind, s, i);
     return b;
 }
 
@@ -491,6 +499,9 @@ LayerWs carve_layer(int kind, void* ws, const WsSpec& s) {
         r.qb[0] = (int*)b; b += qbb;
         r.qb[1] = (int*)b;
     }
+    char* p4 = (char*)ws;
+    for (int i = 0; i < 4; ++i) p4 += layer_part(kind, s, i);
+    r.kmask = layer_part(kind, s, 4) ? (float*)p4 : nullptr;
     return r;
 }
 }  // namespace
@@ -514,20 +525,21 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
     const int S = P * D;
     LayerWs L = carve_layer(kind, ws, spec);
     SortedWs& w = L.op;
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    // Masked add_laplace: masked keys become FLT_MAX (terms exactly 0, sorted last) and the unmasked walk runs.
+    const bool lap_masked = kind == LAYER_ADD_LAPLACE && keep != nullptr;
+    if (lap_masked)
+        if (int e = hip_status(mask_keys(k, keep, L.kmask, P, D, N, st), "masked keys")) return e;
+    const float* ksrc = lap_masked ? L.kmask : k;
+    if (int e = hip_status(seg_sort(ksrc, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
     auto sort_q = [&](hipStream_t s) {
         return hip_status(seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s), "segmented sort of q");
     };
     int e = 0;
     if (kind == LAYER_ADD_LAPLACE) {
-        e = fork_join(st,
-            [&](hipStream_t s) {
-                return hip_status(laplace_prepare(w.ks, w.kp, v, keep, P, D, N, C, w.ra, s), "laplace ranges"); },
-            [&](hipStream_t s) {
-                if (int r = sort_q(s)) return r;
-                return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, 0.f, S, N, M, C, s), "query bounds"); });
+        e = group_q(q, w, 0.f, S, N, M, C, st);
+        if (!e) e = hip_status(laplace_prepare(w.ks, w.kp, v, P, D, N, C, w.ra, st), "laplace ranges");
         if (e) return e;
-        e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, keep, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
+        e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
         if (e) return hip_status(e, "laplace walk");
         e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[0], L.u[0], P, D, M, C, st);
         if (e) return hip_status(e, "laplace reduce");
@@ -539,17 +551,20 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         a.out_dot = nullptr; a.out_rank = nullptr;
         a.sign = 1.f; a.P = P; a.D = D; a.C = C; a.qshift = 0.f;
         const int mode = ABS_ROW | ABS_ONES | (keep ? ABS_KEEP : 0);
-        // one sort of k and q, one set of range summaries and one scan serve every query shift: q + s has the sorted
-        // order of q, and the key side does not depend on the queries
+        // one sort of k and q, one set of range summaries and one scan serve every query shift of add_bump: q + s has
+        // the sorted order of q, and the key side does not depend on the queries (one shift: q grouped instead)
         const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
         const float shift[3] = {0.f, 1.f, -1.f};
         int* qbs[3] = {w.ra.qb, L.qb[0], L.qb[1]};
-        e = fork_join(st,
-            [&](hipStream_t s) {
-                if (int r = abs_prepare(a, mode, w.ra, s)) return hip_status(r, "abs ranges");
-                if (kind == LAYER_ADD_RIESZ)
-                    return hip_status(riesz_prefix(k, v, keep, L.pre, P, D, N, C, s), "riesz prefixes");
-                return QLKA_OK; },
+        auto key_side = [&](hipStream_t s) {
+            if (int r = abs_prepare(a, mode, w.ra, s)) return hip_status(r, "abs ranges");
+            if (kind == LAYER_ADD_RIESZ)
+                return hip_status(riesz_prefix(k, v, keep, L.pre, P, D, N, C, s), "riesz prefixes");
+            return QLKA_OK; };
+        if (nev == 1) {
+            e = group_q(q, w, 0.f, S, N, M, C, st);
+            if (!e) e = key_side(st);
+        } else e = fork_join(st, key_side,
             [&](hipStream_t s) {
                 if (int r = sort_q(s)) return r;
                 for (int ev = 0; ev < nev; ++ev) {

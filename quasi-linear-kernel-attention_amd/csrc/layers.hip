@@ -19,6 +19,9 @@
 // and add_bump drop their n_pad term, and add_riesz, whose u lost n_pad |q|_1, keeps the reference's algebra as
 //   den = (|q|_1 + EPS) * S + sum_kept |k_n|_1 - u - n_pad (|q|_1 + EPS),  n_pad = N - #kept,
 // with sum_n v and sum_n |k_n|_1 v_n over the kept keys.
+#include <algorithm>
+#include <cfloat>
+
 #include "qlka_common.h"
 #include "qlka_internal.h"
 
@@ -126,6 +129,30 @@ int riesz_prefix(const float* k, const float* v, const uint8_t* keep, void* pre,
     const int n = P * (2 * C + 2);
     hipLaunchKernelGGL(riesz_finish, dim3((unsigned)((n + RZ_T - 1) / RZ_T)), dim3(RZ_T), 0, st, part, vsum, akv, sak,
                        npad, P, N, C);
+    return (int)hipGetLastError();
+}
+
+// Masked keys of the Laplace layer: out[p][d][n] = k[p][d][n] if keep[p][n], else FLT_MAX. Every Laplace term of
+// such a key, e^{-(FLT_MAX - x)} for any query or key x below FLT_MAX, is exactly 0, two of them are FLT_MAX apart by 0
+// (no inf - inf), and they sort after every kept key, so the unmasked walk over these keys gives the sums over the
+// kept keys exactly. Grid: x over chunks of n, y (strided) over the P*D rows; no division per element.
+__global__ __launch_bounds__(RZ_T)
+void mask_keys_kernel(const float* __restrict__ k, const uint8_t* __restrict__ keep, float* __restrict__ out,
+                      const int D, const int N, const int PD)
+{
+    const int n = blockIdx.x * RZ_T + threadIdx.x;
+    if (n >= N) return;
+    for (int pd = blockIdx.y; pd < PD; pd += gridDim.y) {
+        const size_t i = (size_t)pd * N + n;
+        out[i] = keep[(size_t)(pd / D) * N + n] ? k[i] : FLT_MAX;
+    }
+}
+
+int mask_keys(const float* k, const uint8_t* keep, float* out, int P, int D, int N, hipStream_t st) {
+    const int PD = P * D;
+    StageTimer t("mask_keys", st);
+    hipLaunchKernelGGL(mask_keys_kernel, dim3((unsigned)((N + RZ_T - 1) / RZ_T), (unsigned)std::min(PD, 65535)),
+                       dim3(RZ_T), 0, st, k, keep, out, D, N, PD);
     return (int)hipGetLastError();
 }
 

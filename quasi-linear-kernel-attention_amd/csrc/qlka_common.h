@@ -50,6 +50,11 @@ __device__ __forceinline__ uint32_t bcast(uint32_t x, int src) {
     return (uint32_t)__builtin_amdgcn_readlane((int)x, src);
 }
 
+// number of lanes below this one whose bit is set in the wave-uniform mask m (v_mbcnt)
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, WAVE);

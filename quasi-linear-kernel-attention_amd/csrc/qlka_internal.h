@@ -84,19 +84,15 @@ __host__ __device__ inline int slab_row_off(int m, int G, int CR) {
     return (((m >> SLAB_QB_LOG) * G) * SLAB_QB + (m & (SLAB_QB - 1))) * CR * 4;
 }
 
-// Per feature d of p: slab[(p*D + d)*M + m][c] = sum_n exp(-|k_n - q_m|) v[p,n,c] (row stride slab_stride(C)),
-// uslab[(p*D + d)*M + i] = sum_n exp(-|k_n - q_(i)|) for the i-th smallest query of the feature. keep (P, N) bytes,
-// nonzero = kept, or null: the sums run over the kept keys only.
-int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
-                 hipStream_t st);
-// The parts of laplace_walk: the key side (range summaries and scan into ra.ta / ra.tb), which needs only the sorted
-// keys, and the walk, which also needs the sorted queries and their range boundaries (query_bounds into ra.qb).
-int laplace_prepare(const float* ks, const uint32_t* kp, const float* v, const uint8_t* keep, int P, int D, int N,
-                    int C, RangeArrays ra, hipStream_t st);
+// The Laplace walk, in two parts. Per feature d of p it writes slab[(p*D + d)*M + m][c] = sum_n exp(-|k_n - q_m|)
+// v[p,n,c] (row stride slab_stride(C)) and the v == 1 sums into uslab. laplace_prepare is the key side (range summaries
+// and scan into ra.ta / ra.tb) and needs only the sorted keys; laplace_emit is the walk, which also needs the sorted
+// queries and their range boundaries (query_bounds into ra.qb). A key of value FLT_MAX adds exactly 0 to the sums
+// of every query below FLT_MAX (its decay factor e^{-(FLT_MAX - q)} is 0): that is how masked keys drop out (mask_keys).
+int laplace_prepare(const float* ks, const uint32_t* kp, const float* v, int P, int D, int N, int C, RangeArrays ra,
+                    hipStream_t st);
 int laplace_emit(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
-                 hipStream_t st);
+                 float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st);
 
 // Order of the per-feature v == 1 terms (uslab) the walks write: sorted-query order (coalesced stores, put in query
 // order through LDS before the reduce) when a segment's M terms fit one workgroup's LDS, else query order (one
@@ -153,6 +149,11 @@ int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st);
 // queries qs (S segments of Mq), ranges of range_keys(C) keys
 int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S, int Ns, int Mq, int C,
                  hipStream_t st);
+// The queries of every segment grouped by owning key range for queries shifted by qshift: qs / qp (S segments of Mq)
+// get the values and original indices of range 0's queries, then range 1's, ...; the order inside a range is not
+// fixed. qb as query_bounds writes it. The forward walks accept grouped queries as well as sorted ones.
+int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int* qb, float qshift, int S, int Ns,
+                  int Mq, int C, hipStream_t st);
 int range_count(int Ns, int C);          // key ranges per segment
 
 // Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null
@@ -173,6 +174,8 @@ size_t riesz_prefix_bytes(int P, int N, int C);
 // akv[p][c] = sum_n |k_n|_1 v_n, sak[p] = sum_n |k_n|_1, npad[p] = N - #kept (pre must hold riesz_prefix_bytes)
 int riesz_prefix(const float* k, const float* v, const uint8_t* keep, void* pre, int P, int D, int N, int C,
                  hipStream_t st);
+// out[p][d][n] = keep[p][n] ? k[p][d][n] : FLT_MAX: keys whose every Laplace term is exactly 0 and which sort last
+int mask_keys(const float* k, const uint8_t* keep, float* out, int P, int D, int N, hipStream_t st);
 // out[p][m][:] from the op outputs: w0/u0 (and, for add_bump, w+/u+ and w-/u- of q + 1 and q - 1). masked: the op
 // outputs are sums over the kept keys and n_pad is ignored (add_riesz takes its n_pad from pre); else n_pad (P) is
 // the reference's padded-key count (null: none). qt: (P, M) scratch for the per-query d-reductions

@@ -126,8 +126,8 @@ __device__ __forceinline__ void mask_rows(float (&x)[RK][NV], const float kw) {
 template <int NV, int RK>
 __global__ __launch_bounds__(WPB * WAVE)
 void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ kp,
-                    const float* __restrict__ v, const uint8_t* __restrict__ keep, float* __restrict__ ta,
-                    float* __restrict__ tb, const int S, const int D, const int N, const int C, const int G)
+                    const float* __restrict__ v, float* __restrict__ ta, float* __restrict__ tb, const int S,
+                    const int D, const int N, const int C, const int G)
 {
     const long wv = (long)xcd_slice_block(blockIdx.x, gridDim.x) * WPB + wave_in_block();
     if (wv >= (long)S * G) return;
@@ -140,7 +140,7 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
     const float kl = kseg[li];
     const uint32_t pl = kp[(size_t)s * N + li];
     const float kfirst = kseg[base], klast = kseg[base + nk - 1];
-    const float kw = key_weight(keep, p, N, pl, l < nk);
+    const float kw = (l < nk) ? 1.f : 0.f;                   // pad lanes of a partial range weigh 0
     const float wl = kw * __expf(-(klast - kl));
     const float wr = kw * __expf(-(kl - kfirst));
 
@@ -349,11 +349,11 @@ struct QueryBlocks {
 
 constexpr int RPW = 1;             // consecutive key ranges walked by one wave of a walk kernel
 
-template <int NV, int RK, bool KEEP>
-__global__ __launch_bounds__(WPB * WAVE) __attribute__((amdgpu_waves_per_eu(KEEP && NV == 1 ? 4 : 1)))
+template <int NV, int RK>
+__global__ __launch_bounds__(WPB * WAVE)
 void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ kp, const float* __restrict__ qs,
-                    const uint32_t* __restrict__ qp, const float* __restrict__ v, const uint8_t* __restrict__ keep,
-                    const float* __restrict__ ta, const float* __restrict__ tb, const int* __restrict__ qb,
+                    const uint32_t* __restrict__ qp, const float* __restrict__ v, const float* __restrict__ ta,
+                    const float* __restrict__ tb, const int* __restrict__ qb,
                     float* __restrict__ slab, float* __restrict__ uslab,
                     const int S, const int D, const int N, const int M, const int C, const int CR, const int G)
 {
@@ -386,7 +386,7 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
         const bool has_prev = g > 0, has_next = g < G - 1;
         const float kbefore = has_prev ? kseg[base - 1] : 0.f;
         const float kafter  = has_next ? kseg[base + RK] : 0.f;
-        const float kw = KEEP ? key_weight(keep, p, N, kpseg[li], real) : (real ? 1.f : 0.f);
+        const float kw = real ? 1.f : 0.f;
 
         // value rows of the range, lane = channel (pad keys and pad channels: zero). The row indices are read with
         // scalar loads straight into SGPRs (the buffer offset of each row gather).
@@ -420,7 +420,6 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
                 for (int j = 0; j < NV; ++j)
                     x[t][j] = (t < nk && l + WAVE * j < C) ? x[t][j] : 0.f;
         }
-        if constexpr (KEEP) mask_rows<NV, RK>(x, kw);
 
         const float* ra = ta + ((size_t)s * (G + 1) + g) * CS;
         const float* rb = tb + ((size_t)s * (G + 1) + g) * CS;
@@ -565,8 +564,8 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
 }
 
 template <int NV, int RK>
-static int laplace_prepare_t(const float* ks, const uint32_t* kp, const float* v, const uint8_t* keep, int P, int D,
-                             int N, int C, RangeArrays ra, hipStream_t st) {
+static int laplace_prepare_t(const float* ks, const uint32_t* kp, const float* v, int P, int D, int N, int C,
+                             RangeArrays ra, hipStream_t st) {
     const int S = P * D;
     const int G = (N + RK - 1) / RK;
     const long waves = (long)S * G;
@@ -574,7 +573,7 @@ static int laplace_prepare_t(const float* ks, const uint32_t* kp, const float* v
     {
         StageTimer t("lap_range_sums", st);
         hipLaunchKernelGGL((lap_range_sums<NV, RK>), dim3(blocks), dim3(WPB * WAVE), 0, st,
-                           ks, kp, v, keep, ra.sa, ra.sb, S, D, N, C, G);
+                           ks, kp, v, ra.sa, ra.sb, S, D, N, C, G);
     }
     {
         StageTimer t("lap_range_scan", st);
@@ -586,45 +585,30 @@ static int laplace_prepare_t(const float* ks, const uint32_t* kp, const float* v
 
 template <int NV, int RK>
 static int laplace_emit_t(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                          const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C,
-                          RangeArrays ra, hipStream_t st) {
+                          float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
+                          hipStream_t st) {
     const int S = P * D;
     const int G = (N + RK - 1) / RK;
     {
         const long walk_waves = (long)S * ((G + RPW - 1) / RPW);
         const unsigned walk_blocks = (unsigned)((walk_waves + WPB - 1) / WPB);
         StageTimer t("lap_range_walk", st);
-        if (keep)
-            hipLaunchKernelGGL((lap_range_walk<NV, RK, true>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
-                               ks, kp, qs, qp, v, keep, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C),
-                               G);
-        else
-            hipLaunchKernelGGL((lap_range_walk<NV, RK, false>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
-                               ks, kp, qs, qp, v, nullptr, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C,
-                               slab_stride(C), G);
+        hipLaunchKernelGGL((lap_range_walk<NV, RK>), dim3(walk_blocks), dim3(WPB * WAVE), 0, st,
+                           ks, kp, qs, qp, v, ra.ta, ra.tb, ra.qb, slab, uslab, S, D, N, M, C, slab_stride(C), G);
     }
     return (int)hipGetLastError();
 }
 
-int laplace_prepare(const float* ks, const uint32_t* kp, const float* v, const uint8_t* keep, int P, int D, int N,
-                    int C, RangeArrays ra, hipStream_t st) {
-    if (C <= WAVE) return laplace_prepare_t<1, 64>(ks, kp, v, keep, P, D, N, C, ra, st);
-    return laplace_prepare_t<2, 32>(ks, kp, v, keep, P, D, N, C, ra, st);
+int laplace_prepare(const float* ks, const uint32_t* kp, const float* v, int P, int D, int N, int C, RangeArrays ra,
+                    hipStream_t st) {
+    if (C <= WAVE) return laplace_prepare_t<1, 64>(ks, kp, v, P, D, N, C, ra, st);
+    return laplace_prepare_t<2, 32>(ks, kp, v, P, D, N, C, ra, st);
 }
 
 int laplace_emit(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
-                 hipStream_t st) {
-    if (C <= WAVE) return laplace_emit_t<1, 64>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
-    return laplace_emit_t<2, 32>(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
-}
-
-int laplace_walk(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,
-                 const uint8_t* keep, float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra,
-                 hipStream_t st) {
-    if (int e = query_bounds(ks, qs, ra.qb, 0.f, P * D, N, M, C, st)) return e;
-    if (int e = laplace_prepare(ks, kp, v, keep, P, D, N, C, ra, st)) return e;
-    return laplace_emit(ks, kp, qs, qp, v, keep, slab, uslab, P, D, N, M, C, ra, st);
+                 float* slab, float* uslab, int P, int D, int N, int M, int C, RangeArrays ra, hipStream_t st) {
+    if (C <= WAVE) return laplace_emit_t<1, 64>(ks, kp, qs, qp, v, slab, uslab, P, D, N, M, C, ra, st);
+    return laplace_emit_t<2, 32>(ks, kp, qs, qp, v, slab, uslab, P, D, N, M, C, ra, st);
 }
 
 // =================================================================================================================
@@ -760,6 +744,210 @@ int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S,
         hipLaunchKernelGGL((query_bounds_kernel<64>), grid, dim3(RB_T), 0, st, ks, qs, qb, qshift, Ns, Mq, G, chunks);
     else
         hipLaunchKernelGGL((query_bounds_kernel<32>), grid, dim3(RB_T), 0, st, ks, qs, qb, qshift, Ns, Mq, G, chunks);
+    return (int)hipGetLastError();
+}
+
+// Queries grouped by key chunk, the forward walks' alternative to sorting them. The sorted keys of a segment fall into
+// chunks of CH = RK / 4 (four per key range, the walks' emission chunks); a query's bucket is the chunk holding the
+// first key >= q + qshift, b = #{c : klast_c < q + qshift} (Gc = ceil(Ns / CH) when it is above every key). Queries
+// come out in bucket order, so each range owns a contiguous run (range g: buckets 4g .. 4g + 3, the last range also
+// bucket Gc) and, inside it, its queries come chunk by chunk, which is all a walk needs of their order: it ranks each
+// query inside the range itself, and a block of 64 queries then covers consecutive chunks as with sorted queries.
+// qb[g] = #queries of ranges <= g, as query_bounds writes it. One workgroup per segment: the Gc chunk boundaries go to
+// LDS, every query finds its bucket by binary search there and counts it with an LDS atomic; an exclusive scan of the
+// Gc + 1 counts gives the bucket offsets; returning LDS atomics then hand out slots in each bucket, staged in LDS for
+// coalesced stores when the segment fits. The order inside a bucket is the order in which the atomics return, which
+// is not fixed; no output of any walk depends on it (each query's sums come from its own rank and go to its own index,
+// directly or through qp).
+constexpr int GQ_T = 1024;         // threads per workgroup
+constexpr int GQ_STAGE = 16384;    // longest segment staged in LDS (its values and indices: 128 KB)
+constexpr int GQ_STAGE_MAXB = 2048;        // most chunk buckets of a staged segment
+constexpr int GQ_MAXB = 4 * RB_MAXG;       // most chunk buckets
+
+template <int MAXB, int STAGE>
+struct GroupLds {
+    float bnd[MAXB];
+    float rb[MAXB / 4];
+    int off[MAXB + 1];
+    int wsum[GQ_T / WAVE];
+    float sv[STAGE];
+    uint32_t si[STAGE];
+};
+
+// Bucket of x among the nb chunk boundaries in LDS: #{c : bnd[c] < x} (bnd ascending). A branch-free descent over
+// the range boundaries rb (the last key of each range, in an array of their own so that the descent's reads spread
+// over the LDS banks) finds the range, then the range's first three chunk boundaries are compared at once; the NI
+// searches of a thread run interleaved step by step, so that their LDS reads overlap.
+template <int NI>
+__device__ __forceinline__ void buckets(const float* bnd, const float* rb, const int nb, const float (&x)[NI],
+                                        int (&b)[NI]) {
+    const int ng = (nb + 3) >> 2;
+    int g[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) g[j] = 0;
+    int step = 1;
+    while (step * 2 <= ng) step *= 2;
+    for (; step >= 1; step >>= 1) {
+        float y[NI];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) y[j] = rb[min(g[j] + step, ng) - 1];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) g[j] += (g[j] + step <= ng && y[j] < x[j]) ? step : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int c0 = min(4 * g[j], nb - 1);
+        const float y0 = bnd[c0], y1 = bnd[min(c0 + 1, nb - 1)], y2 = bnd[min(c0 + 2, nb - 1)];
+        b[j] = 4 * g[j];
+        if (g[j] < ng) b[j] += (y0 < x[j]) + (c0 + 1 < nb && y1 < x[j]) + (c0 + 2 < nb && y2 < x[j]);
+        else b[j] = nb;
+    }
+}
+
+// Exclusive scan of off[0..n) in place by the whole workgroup (thread t owns a contiguous piece), then the range
+// bounds: qb[g] = offset of bucket 4 (g + 1), or of bucket n - 1 = Gc for the last range.
+__device__ __forceinline__ void group_scan(int* off, int* wsum, const int n, int* qbs) {
+    const int tid = threadIdx.x;
+    const int E = (n + GQ_T - 1) / GQ_T;
+    const int e0 = min(tid * E, n), e1 = min(e0 + E, n);
+    int own = 0;
+    for (int c = e0; c < e1; ++c) own += off[c];
+    int incl = own;
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const int y = __shfl_up(incl, d, WAVE);
+        if (lane_id() >= d) incl += y;
+    }
+    if (lane_id() == WAVE - 1) wsum[tid / WAVE] = incl;
+    __syncthreads();
+    int base = incl - own;
+    for (int w = 0; w < tid / WAVE; ++w) base += wsum[w];
+    for (int c = e0; c < e1; ++c) {
+        const int cnt = off[c];
+        off[c] = base;
+        if (c > 0 && ((c & 3) == 0 || c == n - 1)) qbs[(c - 1) >> 2] = base;
+        base += cnt;
+    }
+    __syncthreads();
+}
+
+// Segments of up to GQ_STAGE queries: a thread's GQ_I queries stay in registers from the load to the placement (one
+// load and one search each), and the grouped segment is staged in LDS and stored coalesced.
+constexpr int GQ_I = GQ_STAGE / GQ_T;
+
+template <int CH>
+__global__ __launch_bounds__(GQ_T)
+void group_queries_staged(const float* __restrict__ ks, const float* __restrict__ q, float* __restrict__ qs,
+                          uint32_t* __restrict__ qp, int* __restrict__ qb, const float qshift, const int Ns,
+                          const int Mq, const int G, const int Gc)
+{
+    __shared__ GroupLds<GQ_STAGE_MAXB, GQ_STAGE> sm;
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const float* kseg = ks + (size_t)s * Ns;
+    const float* qseg = q + (size_t)s * Mq;
+    float x[GQ_I], xs[GQ_I];
+#pragma unroll
+    for (int j = 0; j < GQ_I; ++j) x[j] = qseg[min(tid + j * GQ_T, Mq - 1)];   // clamped: all loads in flight
+    for (int c = tid; c < Gc; c += GQ_T) {
+        const float y = kseg[min(Ns, (c + 1) * CH) - 1];
+        sm.bnd[c] = y;
+        if ((c & 3) == 3 || c == Gc - 1) sm.rb[c >> 2] = y;
+    }
+    for (int c = tid; c <= Gc; c += GQ_T) sm.off[c] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < GQ_I; ++j) xs[j] = x[j] + qshift;
+    int b[GQ_I];
+    buckets<GQ_I>(sm.bnd, sm.rb, Gc, xs, b);
+#pragma unroll
+    for (int j = 0; j < GQ_I; ++j)
+        if (tid + j * GQ_T < Mq) atomicAdd(&sm.off[b[j]], 1);
+    __syncthreads();
+    group_scan(sm.off, sm.wsum, Gc + 1, qb + (size_t)s * G);
+#pragma unroll
+    for (int j = 0; j < GQ_I; ++j) {
+        const int i = tid + j * GQ_T;
+        if (i < Mq) {
+            const int pos = atomicAdd(&sm.off[b[j]], 1);
+            sm.sv[pos] = x[j];
+            sm.si[pos] = (uint32_t)i;
+        }
+    }
+    __syncthreads();
+    float* qso = qs + (size_t)s * Mq;
+    uint32_t* qpo = qp + (size_t)s * Mq;
+    for (int i = tid; i < Mq; i += GQ_T) { qso[i] = sm.sv[i]; qpo[i] = sm.si[i]; }
+}
+
+// Any segment length: two passes over the queries (the second searches again) and direct scattered stores.
+template <int CH>
+__global__ __launch_bounds__(GQ_T)
+void group_queries_global(const float* __restrict__ ks, const float* __restrict__ q, float* __restrict__ qs,
+                          uint32_t* __restrict__ qp, int* __restrict__ qb, const float qshift, const int Ns,
+                          const int Mq, const int G, const int Gc)
+{
+    __shared__ GroupLds<GQ_MAXB, 1> sm;
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const float* kseg = ks + (size_t)s * Ns;
+    const float* qseg = q + (size_t)s * Mq;
+    for (int c = tid; c < Gc; c += GQ_T) {
+        const float y = kseg[min(Ns, (c + 1) * CH) - 1];
+        sm.bnd[c] = y;
+        if ((c & 3) == 3 || c == Gc - 1) sm.rb[c >> 2] = y;
+    }
+    for (int c = tid; c <= Gc; c += GQ_T) sm.off[c] = 0;
+    __syncthreads();
+    constexpr int NI = 4;
+    for (int i0 = 0; i0 < Mq; i0 += NI * GQ_T) {
+        float x[NI];
+        int b[NI];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)] + qshift;
+        buckets<NI>(sm.bnd, sm.rb, Gc, x, b);
+#pragma unroll
+        for (int j = 0; j < NI; ++j)
+            if (i0 + tid + j * GQ_T < Mq) atomicAdd(&sm.off[b[j]], 1);
+    }
+    __syncthreads();
+    group_scan(sm.off, sm.wsum, Gc + 1, qb + (size_t)s * G);
+    float* qso = qs + (size_t)s * Mq;
+    uint32_t* qpo = qp + (size_t)s * Mq;
+    for (int i0 = 0; i0 < Mq; i0 += NI * GQ_T) {
+        float x[NI], xs[NI];
+        int b[NI];
+#pragma unroll
+        for (int j = 0; j < NI; ++j) { x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)]; xs[j] = x[j] + qshift; }
+        buckets<NI>(sm.bnd, sm.rb, Gc, xs, b);
+#pragma unroll
+        for (int j = 0; j < NI; ++j) {
+            const int i = i0 + tid + j * GQ_T;
+            if (i < Mq) {
+                const int pos = atomicAdd(&sm.off[b[j]], 1);
+                qso[pos] = x[j];
+                qpo[pos] = (uint32_t)i;
+            }
+        }
+    }
+}
+
+int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int* qb, float qshift, int S, int Ns,
+                  int Mq, int C, hipStream_t st) {
+    const int RK = range_keys(C), CH = RK / 4;
+    const int G = (Ns + RK - 1) / RK, Gc = (Ns + CH - 1) / CH;
+    if (Gc > GQ_MAXB) return (int)hipErrorInvalidValue;
+    const bool staged = Mq <= GQ_STAGE && Gc <= GQ_STAGE_MAXB;
+    StageTimer t("group_queries", st);
+    if (CH == 16) {
+        if (staged) hipLaunchKernelGGL((group_queries_staged<16>), dim3(S), dim3(GQ_T), 0, st,
+                                       ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
+        else hipLaunchKernelGGL((group_queries_global<16>), dim3(S), dim3(GQ_T), 0, st,
+                                ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
+    } else {
+        if (staged) hipLaunchKernelGGL((group_queries_staged<8>), dim3(S), dim3(GQ_T), 0, st,
+                                       ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
+        else hipLaunchKernelGGL((group_queries_global<8>), dim3(S), dim3(GQ_T), 0, st,
+                                ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
+    }
     return (int)hipGetLastError();
 }
 

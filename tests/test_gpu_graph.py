@@ -35,6 +35,10 @@ def _cases():
         "abs_full_backward_walk": ((2, 3, 1500, 1400, 16),
                                    lambda q, k, v, gw, gu: _ext.weighted_abs_sum_full_backward(q, k, v, gw, gu)),
         "add_bump_layer": ((2, 3, 1500, 1500, 16), lambda q, k, v, gw, gu: layers.layer_forward("add_bump", q, k, v)),
+        # masked keys: the Laplace layer replaces them by FLT_MAX in its workspace before the sort
+        "add_laplace_masked_layer": ((2, 3, 1500, 1500, 16),
+                                     lambda q, k, v, gw, gu: layers.layer_forward("add_laplace", q, k, v,
+                                                                                  keep=v[:, :, 0] > -0.5)),
         # short segments: the dense kernels
         "abs_full_dense": ((64, 8, 65, 65, 32),
                            lambda q, k, v, gw, gu: weighted_abs_sum_full(q, k, v, backend="cuda")),
@@ -48,7 +52,7 @@ def _flat(out):
 
 
 @pytest.mark.parametrize("case", ["laplace_walk", "abs_full_walk", "abs_full_backward_walk", "add_bump_layer",
-                                  "abs_full_dense", "abs_backward_dense"])
+                                  "add_laplace_masked_layer", "abs_full_dense", "abs_backward_dense"])
 def test_graph_replays_equal_eager(dev, case):
     shape, fn = _cases()[case]
     args = _inputs(dev, *shape, seed=sum(shape))
