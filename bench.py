@@ -244,8 +244,9 @@ def main():
     torch.cuda.synchronize()
     ms_total = start.elapsed_time(stop)
     stages = {}
-    for name in ("lds_radix_sort", "merge_runs", "query_bounds", "fill_zero", "lap_range_sums", "lap_range_scan",
-                 "lap_range_walk", "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_to_query", "u_sum", "slab_reduce"):
+    for name in ("lds_radix_sort", "merge_runs", "group_queries", "query_bounds", "fill_zero", "lap_range_sums",
+                 "lap_range_scan", "lap_range_walk", "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_to_query",
+                 "u_sum", "slab_reduce"):
         ms, cnt = _lib.stage_time(name)
         if cnt:
             stages[name] = {"ms_total": ms, "launches": cnt, "ms_per_launch": ms / cnt}
