@@ -117,6 +117,41 @@ __device__ __forceinline__ void mask_rows(float (&x)[RK][NV], const float kw) {
     }
 }
 
+// The two weighted row sums of a 64-key range, oa = sum_t a_t x_t and ob = sum_t b_t x_t, x_t the v row of key t
+// (row index pl, weights a, b: lane t's values), for C <= 64 with C % 4 == 0; lane c returns channel c. 16 lanes
+// cover a row with one 16-byte load each and lane group r takes keys r, r + 4, ..., so the 64 rows take 16 load
+// instructions (64 with a lane per channel); each lane fetches its key's row offset and weights by a lane shuffle,
+// and the groups' partial sums meet across lanes at the end.
+__device__ __forceinline__ void range_row_sums_v4(const rsrc_t vr, const int C, const uint32_t pl, const float a,
+                                                  const float b, float& oa, float& ob) {
+    const int l = lane_id(), grp = l >> 4, sub = l & 15;
+    const int coff = min(4 * sub, C - 4) * 4;
+    f4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = 4 * i + grp;
+        const uint32_t row = (uint32_t)__shfl((int)pl, t, WAVE);
+        const float at = __shfl(a, t, WAVE), bt = __shfl(b, t, WAVE);
+        const f4_t x = buf_load4(vr, (int)(row * C * 4) + coff, 0);
+        sa += at * x;
+        sb += bt * x;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        sa[e] += __shfl_xor(sa[e], 16, WAVE);
+        sb[e] += __shfl_xor(sb[e], 16, WAVE);
+        sa[e] += __shfl_xor(sa[e], 32, WAVE);
+        sb[e] += __shfl_xor(sb[e], 32, WAVE);
+    }
+    // lane = channel: channel c sits in element c % 4 of lane c / 4
+    const int src = min(l, C - 1) >> 2, e = l & 3;
+    float ya[4], yb[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { ya[k] = __shfl(sa[k], src, WAVE); yb[k] = __shfl(sb[k], src, WAVE); }
+    oa = e == 0 ? ya[0] : e == 1 ? ya[1] : e == 2 ? ya[2] : ya[3];
+    ob = e == 0 ? yb[0] : e == 1 ? yb[1] : e == 2 ? yb[2] : yb[3];
+}
+
 // =================================================================================================================
 // Laplace
 // =================================================================================================================
@@ -148,17 +183,21 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
     float sl[NV], sr[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) { sl[j] = 0.f; sr[j] = 0.f; }
+    if (NV == 1 && RK == 64 && C % 4 == 0) {
+        range_row_sums_v4(vr, C, pl, wl, wr, sl[0], sr[0]);
+    } else {
 #pragma unroll
-    for (int t = 0; t < RK; ++t) {
-        const uint32_t row = bcast(pl, t);
-        const float a = bcast(wl, t), b = bcast(wr, t);
+        for (int t = 0; t < RK; ++t) {
+            const uint32_t row = bcast(pl, t);
+            const float a = bcast(wl, t), b = bcast(wr, t);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int c = l + WAVE * j;
-            const float xr = buf_load(vr, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
-            const float x = (c < C) ? xr : 0.f;
-            sl[j] += a * x;
-            sr[j] += b * x;
+            for (int j = 0; j < NV; ++j) {
+                const int c = l + WAVE * j;
+                const float xr = buf_load(vr, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
+                const float x = (c < C) ? xr : 0.f;
+                sl[j] += a * x;
+                sr[j] += b * x;
+            }
         }
     }
     const float l1 = wave_sum(wl), r1 = wave_sum(wr);
@@ -644,17 +683,21 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
     for (int j = 0; j < NV; ++j) { sw[j] = 0.f; sb[j] = 0.f; }
     if constexpr (WANT_W) {
         const rsrc_t wr_ = make_rsrc(w + (size_t)p * Ns * C, (uint32_t)((size_t)Ns * C * 4));
+        if (NV == 1 && RK == 64 && C % 4 == 0) {
+            range_row_sums_v4(wr_, C, pl, kw, dl, sw[0], sb[0]);
+        } else {
 #pragma unroll
-        for (int t = 0; t < RK; ++t) {
-            const uint32_t row = bcast(pl, t);
-            const float a = bcast(kw, t), b = bcast(dl, t);
+            for (int t = 0; t < RK; ++t) {
+                const uint32_t row = bcast(pl, t);
+                const float a = bcast(kw, t), b = bcast(dl, t);
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const int c = l + WAVE * j;
-                const float xr = buf_load(wr_, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
-                const float x = (c < C) ? xr : 0.f;
-                sw[j] += a * x;
-                sb[j] += b * x;
+                for (int j = 0; j < NV; ++j) {
+                    const int c = l + WAVE * j;
+                    const float xr = buf_load(wr_, min(c, C - 1) * 4, (int)(row * C * 4));   // unconditional gather
+                    const float x = (c < C) ? xr : 0.f;
+                    sw[j] += a * x;
+                    sb[j] += b * x;
+                }
             }
         }
     }
