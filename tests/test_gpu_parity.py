@@ -62,6 +62,7 @@ SHAPES = [
     (1, 3, 100, 90, 1),
     (2, 2, 5000, 4097, 32),
     (1, 2, 300, 20000, 33),   # more queries than one LDS transpose holds: v == 1 terms written in query order
+    (1, 1, 40000, 2000, 8),   # more key chunks than the staged query grouping holds: grouped straight to HBM
 ]
 
 
