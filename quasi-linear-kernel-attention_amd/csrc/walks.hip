@@ -1133,6 +1133,19 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         }
         if constexpr (KEEP) mask_rows<NV, RK>(x, kw);
     }
+    // owned queries [q0, q1) and (without a key mask, whose walk has no registers to spare) their first block of 64
+    // (value and index, clamped like the loop's loads), loaded right after the gathers so that their latency overlaps
+    // the prefix work below
+    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
+    const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
+    constexpr bool PREF = !KEEP;
+    float qv0 = 0.f;
+    uint32_t mq0 = 0;
+    if constexpr (PREF) {
+        const int qi0 = min(q0 + l, max(q1 - 1, 0));
+        qv0 = qseg[qi0];
+        mq0 = qpseg[qi0];
+    }
     float ul = 0.f;
     if constexpr (X2) {
         const float ur = a.u[(size_t)p * Ns + kpseg[li]];
@@ -1184,8 +1197,6 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     }
     if constexpr (X2) uli = wave_prefix_sum(ul);
 
-    const int q0 = has_prev ? qb[(size_t)s * G + g - 1] : 0;
-    const int q1 = has_next ? qb[(size_t)s * G + g] : Mq;
     const int SG = slab_group(a.D);
     const rsrc_t sr_ = ROW ? make_rsrc(a.slab + slab_seg_base(p, s - p * a.D, a.D, Mq, a.CR),
                                        slab_seg_bytes(s - p * a.D, a.D, Mq, a.CR))
@@ -1203,8 +1214,9 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         const int nq = min(WAVE, q1 - qb0);
         const bool act = l < nq;
         const int qi = min(qb0 + l, q1 - 1);              // clamped: unconditional loads
-        const float qv = qseg[qi] + a.qshift;
-        const uint32_t mq = qpseg[qi];
+        const bool first = PREF && qb0 == q0;
+        const float qv = (first ? qv0 : qseg[qi]) + a.qshift;
+        const uint32_t mq = first ? mq0 : qpseg[qi];
         const int t = range_rank<RK>(kl, nk, qv);
         const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
         const float lq = qv - (t > 0 ? kpv : kbefore);   // distance to the last key below q (unused when none)
