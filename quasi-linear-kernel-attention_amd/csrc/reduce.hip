@@ -23,12 +23,27 @@ __global__ __launch_bounds__(UT_T)
 void u_to_query(const float* __restrict__ uslab, const uint32_t* __restrict__ qperm, float* __restrict__ uq,
                 const int M)
 {
+    constexpr int UT_I = U_LDS_CAP / UT_T;          // items per thread; all of a thread's loads are issued at once
     __shared__ float buf[U_LDS_CAP];
     const size_t base = (size_t)blockIdx.x * M;
     const int tid = threadIdx.x;
-    for (int i = tid; i < M; i += UT_T) buf[qperm[base + i]] = uslab[base + i];
+    float x[UT_I];
+    uint32_t dst[UT_I];
+#pragma unroll
+    for (int j = 0; j < UT_I; ++j) {
+        const int i = min(tid + j * UT_T, M - 1);     // clamped: unconditional loads
+        x[j] = uslab[base + i];
+        dst[j] = qperm[base + i];
+    }
+#pragma unroll
+    for (int j = 0; j < UT_I; ++j)
+        if (tid + j * UT_T < M) buf[dst[j]] = x[j];
     __syncthreads();
-    for (int i = tid; i < M; i += UT_T) uq[base + i] = buf[i];
+#pragma unroll
+    for (int j = 0; j < UT_I; ++j) {
+        const int i = tid + j * UT_T;
+        if (i < M) uq[base + i] = buf[i];
+    }
 }
 
 __global__ __launch_bounds__(RT)

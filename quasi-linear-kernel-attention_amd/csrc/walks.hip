@@ -919,7 +919,11 @@ void group_queries_staged(const float* __restrict__ ks, const float* __restrict_
     __syncthreads();
     float* qso = qs + (size_t)s * Mq;
     uint32_t* qpo = qp + (size_t)s * Mq;
-    for (int i = tid; i < Mq; i += GQ_T) { qso[i] = sm.sv[i]; qpo[i] = sm.si[i]; }
+#pragma unroll
+    for (int j = 0; j < GQ_I; ++j) {
+        const int i = tid + j * GQ_T;
+        if (i < Mq) { qso[i] = sm.sv[i]; qpo[i] = sm.si[i]; }
+    }
 }
 
 // Any segment length: two passes over the queries (the second searches again) and direct scattered stores.
