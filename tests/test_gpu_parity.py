@@ -157,6 +157,37 @@ def test_abs_forward_full(dev, shape, kind, route):
     _assert_rel(_np(w0), ow, nw, "abs (plain) out")
 
 
+@pytest.mark.parametrize("layout", ["all_equal", "all_above", "all_below", "on_range_ends"])
+def test_forward_query_grouping_edges(dev, layout):
+    # The forward ops group the queries by key chunk instead of sorting them: one bucket holding every query (its
+    # LDS slot counter taken by every lane at once), every query above or below every key (the last and the first
+    # range own them all), and queries equal to the last key of a range (their bucket is that range, rank at its end).
+    from weighted_abs_sum import weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+    P, D, N, M, C = 2, 2, 1500, 3000, 16
+    q, k, v = _data(P, D, N, M, C, seed=11)
+    ks = np.sort(k, axis=2)
+    if layout == "all_equal":
+        q[:] = ks[:, :, N // 2][:, :, None] + np.float32(0.25)
+    elif layout == "all_above":
+        q = ks[:, :, -1:] + np.abs(q) + np.float32(1.0)
+    elif layout == "all_below":
+        q = ks[:, :, :1] - np.abs(q) - np.float32(1.0)
+    else:
+        ends = ks[:, :, 63::64]                                   # the last key of every 64-key range
+        q = ends[:, :, np.arange(M) % ends.shape[2]]
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    w, u = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, f"laplace out_w ({layout})")
+    _assert_rel(_np(u), ou, ou, f"laplace out_u ({layout})")
+    w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, f"abs out_w ({layout})")
+    _assert_rel(_np(u), ou, ou, f"abs out_u ({layout})")
+
+
 def test_abs_translation_far_from_zero(dev):
     # keys and queries centred at 1000: the distance-relative walk must not cancel catastrophically
     from weighted_abs_sum import weighted_abs_sum_full
