@@ -513,6 +513,17 @@ size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C) {
 
 // Both layer entry points: keep == null is the reference's composition over pre-masked k, v and n_pad; keep != null
 // applies the key mask inside the sums (k and v as given, no n_pad).
+// add_laplace / add_riesz: the query terms, then the slab reduce with the epilogue folded in (writes out).
+static int layer_reduce_folded(int kind, bool masked, const float* q, const float* n_pad, LayerWs& L, float* out,
+                               int P, int D, int M, int C, hipStream_t st) {
+    ReduceEpilogue ep{};
+    if (int e = layer_epilogue_params(kind, masked, q, n_pad, L.pre, L.qt, out, P, D, M, C, &ep, st))
+        return hip_status(e, "layer query terms");
+    SortedWs& w = L.op;
+    return hip_status(reduce_slabs_layer(kind, masked, ep, w.slab, w.uslab, w.qp, w.uq, P, D, M, C, st),
+                      "layer reduce");
+}
+
 static int layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad,
                      const uint8_t* keep, float* out, int P, int D, int N, int M, int C, void* ws,
                      size_t ws_bytes_given, void* stream) {
@@ -541,6 +552,8 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         if (e) return e;
         e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
         if (e) return hip_status(e, "laplace walk");
+        if (reduce_folds_epilogue(M, C))
+            return layer_reduce_folded(kind, keep != nullptr, q, n_pad, L, out, P, D, M, C, st);
         e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[0], L.u[0], P, D, M, C, st);
         if (e) return hip_status(e, "laplace reduce");
     } else {
@@ -580,6 +593,8 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
             ra.qb = qbs[ev];
             e = abs_emit(a, mode, ra, st);
             if (e) return hip_status(e, "abs walk");
+            if (kind == LAYER_ADD_RIESZ && reduce_folds_epilogue(M, C))
+                return layer_reduce_folded(kind, keep != nullptr, q, n_pad, L, out, P, D, M, C, st);
             e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[ev], L.u[ev], P, D, M, C, st);
             if (e) return hip_status(e, "abs reduce");
         }

@@ -27,8 +27,6 @@
 
 namespace qlka {
 
-constexpr float LAYER_CLAMP = 1e-6f;
-constexpr float LAYER_EPS = 1e-3f;
 constexpr int RZ_NB = 64;          // key chunks per p of the add_riesz prefix pass
 constexpr int RZ_T = 256;          // threads per block of the layer kernels
 
@@ -207,6 +205,30 @@ void layer_epilogue_kernel(const float* __restrict__ qt, const float* __restrict
         den = MASKED ? (up[pm] + um[pm]) / 2.f - u0[pm] : (up[pm] + um[pm]) / 2.f - u0[pm] - np * qt[pm];
     }
     out[i] = num / fmaxf(den, LAYER_CLAMP);
+}
+
+int layer_epilogue_params(int kind, bool masked, const float* q, const float* n_pad, const void* pre, float* qt,
+                          float* out, int P, int D, int M, int C, ReduceEpilogue* ep, hipStream_t st) {
+    ep->vsum = ep->akv = ep->sak = nullptr;
+    if (kind == LAYER_ADD_RIESZ) {
+        const char* b = (const char*)pre;
+        ep->vsum = (const float*)b;  b += al256((size_t)P * C * 4);
+        ep->akv = (const float*)b;   b += al256((size_t)P * C * 4);
+        ep->sak = (const float*)b;   b += al256((size_t)P * 4);
+        if (masked) n_pad = (const float*)b;              // N - kept keys, from riesz_prefix
+    }
+    if (masked && kind != LAYER_ADD_RIESZ) n_pad = nullptr;
+    ep->n_pad = n_pad; ep->qt = qt; ep->out = out;
+    const long nq = (long)P * M;
+    const unsigned qblocks = (unsigned)((nq + RZ_T - 1) / RZ_T);
+    StageTimer t("layer_query_terms", st);
+    if (kind == LAYER_ADD_LAPLACE)
+        hipLaunchKernelGGL(layer_query_terms<LAYER_ADD_LAPLACE>, dim3(qblocks), dim3(RZ_T), 0, st, q, qt, P, D, M);
+    else if (kind == LAYER_ADD_RIESZ)
+        hipLaunchKernelGGL(layer_query_terms<LAYER_ADD_RIESZ>, dim3(qblocks), dim3(RZ_T), 0, st, q, qt, P, D, M);
+    else
+        return (int)hipErrorInvalidValue;
+    return (int)hipGetLastError();
 }
 
 int layer_epilogue(int kind, bool masked, const float* q, const float* n_pad, const float* w0, const float* u0,

@@ -23,6 +23,10 @@ private:
 // Longest run the LDS radix sort handles in one workgroup (16384 keys * (4 B key + 4 B index) = 128 KB of LDS).
 constexpr int LDS_SORT_MAX = 16384;
 
+// Layer epilogue constants (Weighted_Laplace_Sum/attention.py: the denominator clamp and add_riesz's epsilon).
+constexpr float LAYER_CLAMP = 1e-6f;
+constexpr float LAYER_EPS = 1e-3f;
+
 // ---- sort.hip ----
 size_t seg_sort_scratch_bytes(int S, int L);
 // Stable ascending sort of S contiguous segments of length L. Returns a hipError_t value (0 on success).
@@ -182,5 +186,16 @@ int mask_keys(const float* k, const uint8_t* keep, float* out, int P, int D, int
 int layer_epilogue(int kind, bool masked, const float* q, const float* n_pad, const float* w0, const float* u0,
                    const float* wp, const float* up, const float* wm, const float* um, const void* pre, float* qt,
                    float* out, int P, int D, int N, int M, int C, hipStream_t st);
+// The add_laplace / add_riesz epilogue folded into the slab reduce: the reduce writes out = num / max(den, clamp)
+// instead of w and u (no 2 x 50 MB round trip, no separate pass). Applies when reduce_folds_epilogue(M, C); q gives
+// the query terms (written to qt first), pre the add_riesz constants; masked as for layer_epilogue.
+struct ReduceEpilogue {
+    const float* qt; const float* n_pad; const float* vsum; const float* akv; const float* sak; float* out;
+};
+bool reduce_folds_epilogue(int M, int C);
+int layer_epilogue_params(int kind, bool masked, const float* q, const float* n_pad, const void* pre, float* qt,
+                          float* out, int P, int D, int M, int C, ReduceEpilogue* ep, hipStream_t st);
+int reduce_slabs_layer(int kind, bool masked, const ReduceEpilogue& ep, const float* slab, const float* uslab,
+                       const uint32_t* qperm, float* uq, int P, int D, int M, int C, hipStream_t st);
 
 }  // namespace qlka

@@ -64,10 +64,13 @@ void u_sum(const float* __restrict__ uq, float* __restrict__ out_u, const int P,
 // With WITH_U (V4 and C / 4 a power of two, so the C / 4 lanes of one query row are aligned within a wave) the row's
 // lanes also produce out_u: lane j sums features d = j, j + C/4, ... of the v == 1 contributions (query order) and the
 // partial sums are combined with lane shuffles (fixed order, deterministic).
-template <bool V4, bool WITH_U>
+// EPI (with WITH_U): the add_laplace (LAYER_ADD_LAPLACE) or add_riesz (LAYER_ADD_RIESZ) epilogue on the row's w and u,
+// written to ep.out instead of out / out_u (the same arithmetic as layer_epilogue_kernel); EPI < 0: none.
+template <bool V4, bool WITH_U, int EPI = -1, bool MASKED = false>
 __global__ __launch_bounds__(RT)
 void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const int P, const int D, const int M,
-                 const int C, const int CR, const float* __restrict__ uq, float* __restrict__ out_u)
+                 const int C, const int CR, const float* __restrict__ uq, float* __restrict__ out_u,
+                 const ReduceEpilogue ep = ReduceEpilogue{})
 {
     const int CQ = V4 ? C / 4 : C;
     const long i = (long)blockIdx.x * RT + threadIdx.x;
@@ -89,12 +92,33 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
 #pragma unroll 8
             for (int dd = 0; dd < G; ++dd) a += __builtin_nontemporal_load(s4 + (size_t)dd * (fstride / 4));
         }
-        reinterpret_cast<f4*>(out + pm * C)[c] = a;
+        if constexpr (EPI < 0) reinterpret_cast<f4*>(out + pm * C)[c] = a;
         if constexpr (WITH_U) {
             const float* us = uq + (size_t)p * D * M + m;
             float u = 0.f;
             for (int d = c; d < D; d += CQ) u += us[(size_t)d * M];
             for (int off = CQ >> 1; off >= 1; off >>= 1) u += __shfl_xor(u, off, WAVE);
+            if constexpr (EPI >= 0) {
+                const float np = ep.n_pad ? ep.n_pad[p] : 0.f;
+                const float qv = ep.qt[pm];
+                f4 o;
+                if constexpr (EPI == LAYER_ADD_LAPLACE) {
+                    const float den = fmaxf(MASKED ? u : u - np * qv, LAYER_CLAMP);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = a[e] / den;
+                } else {
+                    const float aqe = qv + LAYER_EPS;
+                    const float den = fmaxf(MASKED ? aqe * (float)M + ep.sak[p] - u - np * aqe
+                                                   : aqe * (float)M + ep.sak[p] - u - LAYER_EPS * np, LAYER_CLAMP);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const size_t pc = (size_t)p * C + 4 * c + e;
+                        o[e] = (aqe * ep.vsum[pc] + ep.akv[pc] - a[e]) / den;
+                    }
+                }
+                reinterpret_cast<f4*>(ep.out + pm * C)[c] = o;
+                return;
+            }
             if (c == 0) out_u[pm] = u;
         }
     } else {
@@ -137,6 +161,43 @@ int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, f
     else
         hipLaunchKernelGGL((slab_reduce<false, false>), dim3(blocks), dim3(RT), 0, st, slab, out, P, D, M, C, CR,
                            nullptr, nullptr);
+    return (int)hipGetLastError();
+}
+
+}  // namespace qlka
+
+namespace qlka {
+
+bool reduce_folds_epilogue(int M, int C) {
+    const int cq = C / 4;
+    return C % 4 == 0 && (cq & (cq - 1)) == 0;
+}
+
+int reduce_slabs_layer(int kind, bool masked, const ReduceEpilogue& ep, const float* slab, const float* uslab,
+                       const uint32_t* qperm, float* uq, int P, int D, int M, int C, hipStream_t st) {
+    if (!reduce_folds_epilogue(M, C) || (kind != LAYER_ADD_LAPLACE && kind != LAYER_ADD_RIESZ))
+        return (int)hipErrorInvalidValue;
+    const int CR = slab_stride(C);
+    if (!u_query_order(M)) {
+        StageTimer t("u_to_query", st);
+        hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
+    } else {
+        uq = const_cast<float*>(uslab);
+    }
+    const long threads = (long)P * M * (C / 4);
+    const unsigned blocks = (unsigned)((threads + RT - 1) / RT);
+    StageTimer t("slab_reduce", st);
+#define QLKA_REDUCE_EPI(K, MK) \
+    hipLaunchKernelGGL((slab_reduce<true, true, K, MK>), dim3(blocks), dim3(RT), 0, st, slab, nullptr, P, D, M, C, CR, \
+                       uq, nullptr, ep)
+    if (kind == LAYER_ADD_LAPLACE) {
+        if (masked) QLKA_REDUCE_EPI(LAYER_ADD_LAPLACE, true);
+        else QLKA_REDUCE_EPI(LAYER_ADD_LAPLACE, false);
+    } else {
+        if (masked) QLKA_REDUCE_EPI(LAYER_ADD_RIESZ, true);
+        else QLKA_REDUCE_EPI(LAYER_ADD_RIESZ, false);
+    }
+#undef QLKA_REDUCE_EPI
     return (int)hipGetLastError();
 }
 
