@@ -123,8 +123,8 @@ int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, 
     return QLKA_OK;
 }
 
-// The query side of a forward walk that keeps no sorts: q grouped by owning key range, with the range bounds, in one
-// pass (the walks take grouped queries as well as sorted ones).
+// The query side of a forward walk that keeps no sorts: q grouped by key chunk, with the range bounds, in one pass
+// (the walks take grouped queries as well as sorted ones).
 static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int M, int C, hipStream_t st) {
     return hip_status(group_queries(w.ks, q, w.qs, w.qp, w.ra.qb, qshift, S, N, M, C, st), "query grouping");
 }

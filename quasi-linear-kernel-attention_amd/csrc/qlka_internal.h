@@ -153,9 +153,10 @@ int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st);
 // queries qs (S segments of Mq), ranges of range_keys(C) keys
 int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S, int Ns, int Mq, int C,
                  hipStream_t st);
-// The queries of every segment grouped by owning key range for queries shifted by qshift: qs / qp (S segments of Mq)
-// get the values and original indices of range 0's queries, then range 1's, ...; the order inside a range is not
-// fixed. qb as query_bounds writes it. The forward walks accept grouped queries as well as sorted ones.
+// The queries of every segment (shifted by qshift) grouped by key chunk, a quarter of a key range: qs / qp (S segments
+// of Mq) get the values and original indices of chunk 0's queries, then chunk 1's, ... (a query's chunk holds the first
+// key >= q + qshift), so each range's queries are contiguous and come chunk by chunk; the order inside a chunk is not
+// fixed. qb as query_bounds writes it. The forward walks accept these grouped queries as well as sorted ones.
 int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int* qb, float qshift, int S, int Ns,
                   int Mq, int C, hipStream_t st);
 int range_count(int Ns, int C);          // key ranges per segment
