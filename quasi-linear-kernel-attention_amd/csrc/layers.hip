@@ -146,11 +146,32 @@ void mask_keys_kernel(const float* __restrict__ k, const uint8_t* __restrict__ k
     }
 }
 
+// The same four keys at a time (N % 4 == 0, 16-byte aligned k and out, 4-byte aligned keep).
+__global__ __launch_bounds__(RZ_T)
+void mask_keys_kernel4(const float4* __restrict__ k, const uchar4* __restrict__ keep, float4* __restrict__ out,
+                       const int D, const int N4, const int PD)
+{
+    const int n = blockIdx.x * RZ_T + threadIdx.x;
+    if (n >= N4) return;
+    for (int pd = blockIdx.y; pd < PD; pd += gridDim.y) {
+        const size_t i = (size_t)pd * N4 + n;
+        const uchar4 kp = keep[(size_t)(pd / D) * N4 + n];
+        const float4 x = k[i];
+        out[i] = make_float4(kp.x ? x.x : FLT_MAX, kp.y ? x.y : FLT_MAX, kp.z ? x.z : FLT_MAX, kp.w ? x.w : FLT_MAX);
+    }
+}
+
 int mask_keys(const float* k, const uint8_t* keep, float* out, int P, int D, int N, hipStream_t st) {
     const int PD = P * D;
     StageTimer t("mask_keys", st);
-    hipLaunchKernelGGL(mask_keys_kernel, dim3((unsigned)((N + RZ_T - 1) / RZ_T), (unsigned)std::min(PD, 65535)),
-                       dim3(RZ_T), 0, st, k, keep, out, D, N, PD);
+    const bool v4 = N % 4 == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)keep & 3) == 0;
+    if (v4)
+        hipLaunchKernelGGL(mask_keys_kernel4,
+                           dim3((unsigned)((N / 4 + RZ_T - 1) / RZ_T), (unsigned)std::min(PD, 65535)), dim3(RZ_T), 0,
+                           st, (const float4*)k, (const uchar4*)keep, (float4*)out, D, N / 4, PD);
+    else
+        hipLaunchKernelGGL(mask_keys_kernel, dim3((unsigned)((N + RZ_T - 1) / RZ_T), (unsigned)std::min(PD, 65535)),
+                           dim3(RZ_T), 0, st, k, keep, out, D, N, PD);
     return (int)hipGetLastError();
 }
 
