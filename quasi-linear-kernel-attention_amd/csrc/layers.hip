@@ -56,8 +56,10 @@ void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, co
     for (int n = n0 + tid; n < n1; n += RZ_T) {
         const bool kn = !keep || keep[(size_t)p * N + n] != 0;
         float a = 0.f;
-        if (kn)
+        if (kn) {
+#pragma unroll 16
             for (int d = 0; d < D; ++d) a += fabsf(kp[(size_t)d * N + n]);
+        }
         aks[n - n0] = a;
         kept[n - n0] = kn;
         sak += a;
@@ -69,6 +71,7 @@ void riesz_partials(const float* __restrict__ k, const float* __restrict__ v, co
     float sv = 0.f, skv = 0.f;
     if (rg < G) {
         const float* vp = v + (size_t)p * N * C;
+#pragma unroll 8
         for (int n = n0 + rg; n < n1; n += G) {
             if (!kept[n - n0]) continue;
             const float x = vp[(size_t)n * C + c];
@@ -186,6 +189,7 @@ void layer_query_terms(const float* __restrict__ q, float* __restrict__ qt, cons
     const int p = (int)(i / M), m = (int)(i - (long)p * M);
     const float* qc = q + (size_t)p * D * M + m;
     float a = 0.f;
+#pragma unroll 16
     for (int d = 0; d < D; ++d) {
         const float x = fabsf(qc[(size_t)d * M]);
         if constexpr (KIND == LAYER_ADD_LAPLACE) a += expf(-x);
