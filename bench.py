@@ -4,10 +4,13 @@ One step = one weighted_laplace_sum forward and one weighted_abs_sum_full forwar
 add_riesz / add_bump layers call) over one batch of BASELINE.json configs[3]: B=1, H=12 (P=12), N=M=16384,
 D=Dv=64, fp32, q, k, v ~ N(0,1) drawn from numpy PCG64(seed 0) in the order q, k, v, resident in HBM before timing.
 
-Prints ONE JSON line (rank 0, N=1). `value` = query-feature sums per second over the whole step (2 * P*M*D units per
-step). `roofline` is for the dominant kernel, timed with hipEvents recorded by libqlka on the kernels' own stream
-inside the timed region. `cpu_baseline` times the reference's dense PyTorch path (restated in oracle/dense.py) on the
-host CPU on a bounded query sample of the same workload.
+Prints ONE JSON line (rank 0, N=1), only after both ops' outputs on the bench inputs match the fp64 oracle on a
+query subsample (`parity`). `value` = query-feature sums per second over the whole step (2 * P*M*D units per step),
+timed with events around the steps only. `roofline.frac` = B_scan of the step's two op calls / step time / 8 TB/s
+(the op-level figure the north-star target is set on, also per op in `op_frac`); `roofline.kernel` is the longest
+kernel on its own algorithmic bytes, its launch time taken in a second, instrumented pass (libqlka's hipEvent stage
+timer on the kernel's own stream). `cpu_baseline` times the reference's dense PyTorch path (restated in
+oracle/dense.py) on the host CPU on a bounded query sample of the same workload.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-layers] [--no-configs]
     python bench.py --profile-config I [--steps K]     (one other configuration alone, e.g. under rocprofv3)
@@ -169,6 +172,66 @@ def _cpu_model():
     return "unknown"
 
 
+STAGES = ("lds_radix_sort", "merge_runs", "group_queries", "query_bounds", "fill_zero", "lap_range_sums",
+          "lap_range_scan", "lap_range_walk", "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_to_query",
+          "u_sum", "slab_reduce")
+
+
+def kernel_algorithmic_bytes(name):
+    """Algorithmic bytes of one launch of a headline-op kernel (one op call's worth of its work):
+    walks read the sorted keys and their perm, the grouped queries and their indices, gather v once per key and
+    feature, and write one contribution row per (p, d, query) plus one v == 1 term; the reduce reads the D rows of
+    each query and writes one output row + out_u; the sort reads keys and writes sorted keys + perm; the range
+    sums gather v once per key and feature; the query grouping reads q and writes values + indices."""
+    S = P * D
+    walk = 4.0 * S * (2 * N + 2 * M + N * C + M * C + M)
+    table = {
+        "lap_range_walk": walk, "abs_range_walk": walk,
+        "slab_reduce": 4.0 * P * M * (D * C + D + C + 1),
+        "lds_radix_sort": 12.0 * S * N,
+        "lap_range_sums": 4.0 * S * (2 * N + N * C), "abs_range_sums": 4.0 * S * (2 * N + N * C),
+        "group_queries": 12.0 * S * M,
+    }
+    return table.get(name)
+
+
+def _op_traffic():
+    """Measured HBM bytes of one step (both ops): the sum over each op's kernels of FETCH_SIZE + WRITE_SIZE per launch
+    (rocprofv3 --pmc, copy-calibrated), committed in profiles/traffic.json; None when not measured."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            ops = json.load(f).get("ops", {})
+        return sum(ops[o]["bytes_per_call"] for o in ("weighted_laplace_sum", "weighted_abs_sum_full"))
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def oracle_check(q, k, v, laplace, abs_full, per_p=32, seed=1):
+    """Both ops on the bench inputs against the fp64 oracle (oracle/brute.py) on a seeded subsample of per_p queries
+    of every p (all keys, features and channels), at the north-star bar of 1e-5 of the sum of |term| per element.
+    Raises if either op misses it, so that no number is printed for wrong outputs."""
+    from oracle import brute, inputs
+    qn, kn, vn = (t.cpu().numpy() for t in (q, k, v))
+    idx = inputs.query_subsample(P, M, per_p=per_p, seed=seed)
+
+    def sub(a):
+        a = a.cpu().numpy()
+        return np.stack([a[p][idx[p]] for p in range(P)])
+
+    worst = {}
+    for name, fn, ref in (("weighted_laplace_sum", laplace, brute.laplace_sum),
+                          ("weighted_abs_sum_full", abs_full, brute.abs_sum)):
+        w, u = fn(q, k, v)
+        ow, ou, nw = ref(qn, kn, vn, qidx=idx)
+        err = max(float(brute.rel_err(sub(w), ow, nw).max()), float(brute.rel_err(sub(u), ou, ou).max()))
+        worst[name] = err
+        if not err <= 1e-5:
+            raise SystemExit(f"bench: {name} misses the oracle (max rel err {err:.3e} > 1e-5); no number reported")
+    return {"max_rel_err": worst, "bar": 1e-5, "queries_per_p": per_p,
+            "oracle": "fp64 brute force (oracle/brute.py), all keys, features and channels"}
+
+
 def _traffic(kernel):
     """HBM bytes per launch of `kernel` measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, copy-calibrated),
     committed in profiles/traffic.json; None when not measured."""
@@ -233,8 +296,8 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    lib.qlka_timing_enable(1)
-    lib.qlka_timing_reset()
+    # The timed region: library stage timer off, events around the steps only.
+    lib.qlka_timing_enable(0)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
@@ -243,35 +306,26 @@ def main():
     stop.record()
     torch.cuda.synchronize()
     ms_total = start.elapsed_time(stop)
+    ms_per_step = ms_total / args.steps
+    units = P * M * D
+    value = 2 * units / (ms_per_step / 1e3)
+
+    # Per-kernel times from a separate pass of the same steps, with libqlka's hipEvent stage timer on (each launch
+    # bracketed on its own stream).
+    lib.qlka_timing_reset()
+    lib.qlka_timing_enable(1)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
     stages = {}
-    for name in ("lds_radix_sort", "merge_runs", "group_queries", "query_bounds", "fill_zero", "lap_range_sums",
-                 "lap_range_scan", "lap_range_walk", "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_to_query",
-                 "u_sum", "slab_reduce"):
+    for name in STAGES:
         ms, cnt = _lib.stage_time(name)
         if cnt:
             stages[name] = {"ms_total": ms, "launches": cnt, "ms_per_launch": ms / cnt}
     lib.qlka_timing_enable(0)
 
-    ms_per_step = ms_total / args.steps
-    units = P * M * D
-    value = 2 * units / (ms_per_step / 1e3)
-
-    # Dominant kernel = longest launch; its roofline = algorithmic bytes per launch / launch duration. A walk launch
-    # reads the sorted k and q segments, streams v once in sorted order and emits the M*C contributions + M scalars of
-    # one op call: exactly B_scan (per-unit figure x P*D*M units). Other kernels get their own algorithmic bytes.
-    dom = max(stages, key=lambda s: stages[s]["ms_per_launch"])
-    per_unit = bscan_bytes_per_unit(N, M, C)
-    algo_bytes = {
-        "lds_radix_sort": 12.0 * P * D * N,                  # read keys, write sorted keys + perm
-        "slab_reduce": 4.0 * P * M * C * (D + 1),            # read D contribution rows, write one row per query
-    }
-    bytes_per_launch = algo_bytes.get(dom, per_unit * units)
-    achieved = bytes_per_launch / (stages[dom]["ms_per_launch"] / 1e3) / 1e9
-    roof = {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _traffic(dom),
-            "algorithmic_bytes_per_launch": bytes_per_launch}
-
-    # per-op time, each op timed alone over the same number of calls (north-star target: B_scan / op time)
+    # per-op time, each op timed alone over the same number of calls (north-star target: B_scan / op time), and the
+    # op's peak device memory (torch.cuda.max_memory_allocated over one call, inputs excluded)
     def op_time(fn):
         for _ in range(2):
             fn()
@@ -284,12 +338,43 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / args.steps
 
-    op_ms = {
-        "weighted_laplace_sum": op_time(lambda: weighted_laplace_sum(q, k, v)),
-        "weighted_abs_sum_full": op_time(lambda: weighted_abs_sum_full(q, k, v, backend="cuda")),
+    def op_peak(fn):
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        fn()
+        torch.cuda.synchronize()
+        return torch.cuda.max_memory_allocated() - base
+
+    ops = {
+        "weighted_laplace_sum": lambda: weighted_laplace_sum(q, k, v),
+        "weighted_abs_sum_full": lambda: weighted_abs_sum_full(q, k, v, backend="cuda"),
     }
-    bscan = per_unit * units
-    op_roof = {kk: round(bscan / (vv / 1e3) / 1e9 / HBM_PEAK_GBS, 4) for kk, vv in op_ms.items()}
+    op_ms = {name: op_time(fn) for name, fn in ops.items()}
+    op_peak_bytes = {name: op_peak(fn) for name, fn in ops.items()}
+    bscan = bscan_bytes_per_unit(N, M, C) * units
+    op_frac = {kk: round(bscan / (vv / 1e3) / 1e9 / HBM_PEAK_GBS, 4) for kk, vv in op_ms.items()}
+
+    # Roofline of the step: B_scan of both op calls / step time. The op is the unit the north-star target is set on;
+    # its measured HBM traffic (sum over its kernels of FETCH_SIZE + WRITE_SIZE, copy-calibrated) is `traffic`.
+    # `kernel` is the dominant (longest) launch on its own algorithmic bytes.
+    achieved = 2 * bscan / (ms_per_step / 1e3) / 1e9
+    dom = max(stages, key=lambda s_: stages[s_]["ms_per_launch"])
+    kbytes = kernel_algorithmic_bytes(dom)
+    kach = kbytes / (stages[dom]["ms_per_launch"] / 1e3) / 1e9 if kbytes else None
+    roof = {"bound": "hbm", "scope": "op: B_scan of weighted_laplace_sum + weighted_abs_sum_full per step",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": _op_traffic(),
+            "algorithmic_bytes_per_step": 2 * bscan, "op_frac": op_frac,
+            "kernel": {"name": dom, "ms_per_launch": round(stages[dom]["ms_per_launch"], 4),
+                       "algorithmic_bytes_per_launch": kbytes,
+                       "achieved": round(kach, 1) if kach else None,
+                       "frac": round(kach / HBM_PEAK_GBS, 4) if kach else None,
+                       "traffic": _traffic(dom)}}
+
+    # The numbers above are reported only if the ops' outputs on these inputs match the fp64 oracle.
+    parity = oracle_check(q, k, v, weighted_laplace_sum, weighted_abs_sum_full)
 
     # The three attention layers of configs[3] on the same q, k, v (already tau-scaled inputs do not change the
     # work): fused (one library call: ops + epilogue, add_bump's three abs sums sharing one sort) vs the reference's
@@ -334,7 +419,9 @@ def main():
                    "P": P, "D": D, "N": N, "M": M, "C": C, "units_per_step": 2 * units},
         "roofline": roof,
         "op_ms": {kk: round(vv, 4) for kk, vv in op_ms.items()},
-        "op_bscan_roofline_frac": op_roof,
+        "op_bscan_roofline_frac": op_frac,
+        "op_peak_mem_bytes": op_peak_bytes,
+        "parity": parity,
         "layer_ms": layer_ms,
         "stages": {kk: round(vv["ms_per_launch"], 4) for kk, vv in stages.items()},
         "device": torch.cuda.get_device_name(dev),

@@ -43,7 +43,8 @@ int qlka_set_direct_max(int n);
 /*
  * weighted_laplace_sum forward.
  *   out_w[p,m,c] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|) v[p,n,c],  out_u[p,m] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|)
- * max(N, M) <= 256 runs the dense evaluation of qlka_direct_fwd (the workspace is then unused).
+ * max(N, M) <= B (the dense cutoff, default 512; see qlka_set_direct_max) runs the dense evaluation of
+ * qlka_direct_fwd (the workspace is then unused).
  * Replaces _ext.weighted_laplace_sum_forward (Weighted_Laplace_Sum/csrc/binding.cpp:63-100).
  */
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C);

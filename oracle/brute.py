@@ -21,7 +21,22 @@ abs_backward                   binding.cpp:242-380, sgn_kernels.cu:8-15 (tie -1;
 stable_sort / merge_rank       sort_utils.cu:85-87, walk_common.cuh:10-20                       pure-Python stable sort / brute-force counts
 """
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
+from threadpoolctl import threadpool_limits
+
+
+def _map(fn, n):
+    """[fn(i) for i in range(n)], run on a thread pool (numpy's array loops release the GIL, so the per-p work of a
+    large check runs on all host cores); results in index order."""
+    workers = min(n, os.cpu_count() or 1, 16)
+    if workers <= 1:
+        return [fn(i) for i in range(n)]
+    # one BLAS thread per worker: nested BLAS thread pools oversubscribe the cores (and OpenBLAS then spins)
+    with threadpool_limits(limits=1), ThreadPoolExecutor(workers) as ex:
+        return list(ex.map(fn, range(n)))
 
 
 def _f64(x):
@@ -53,13 +68,12 @@ def abs_sum(q, k, v, qidx=None, keep=None):
     norm_w[p,m,c] = sum_{d,n} |k - q| |v[p,n,c]| (the per-element error normaliser); n over the kept keys."""
     qs, _ = _select(q, qidx)
     k, v = _f64(k), _f64(v)
-    P = qs.shape[0]
-    out_w, out_u, norm = [], [], []
-    for p in range(P):
+
+    def one(p):
         A = _pairwise(qs[p], k[p], np.abs) * _kept(keep, p, k.shape[2])[None, :]
-        out_w.append(A @ v[p])
-        out_u.append(A.sum(axis=1))
-        norm.append(A @ np.abs(v[p]))
+        return A @ v[p], A.sum(axis=1), A @ np.abs(v[p])
+
+    out_w, out_u, norm = zip(*_map(one, qs.shape[0]))
     return np.stack(out_w), np.stack(out_u), np.stack(norm)
 
 
@@ -67,13 +81,12 @@ def laplace_sum(q, k, v, qidx=None, keep=None):
     """(out_w, out_u, norm_w) with the Laplace kernel exp(-|k - q|) in place of |k - q|; n over the kept keys."""
     qs, _ = _select(q, qidx)
     k, v = _f64(k), _f64(v)
-    P = qs.shape[0]
-    out_w, out_u, norm = [], [], []
-    for p in range(P):
+
+    def one(p):
         A = _pairwise(qs[p], k[p], lambda x: np.exp(-np.abs(x))) * _kept(keep, p, k.shape[2])[None, :]
-        out_w.append(A @ v[p])
-        out_u.append(A.sum(axis=1))
-        norm.append(A @ np.abs(v[p]))
+        return A @ v[p], A.sum(axis=1), A @ np.abs(v[p])
+
+    out_w, out_u, norm = zip(*_map(one, qs.shape[0]))
     return np.stack(out_w), np.stack(out_u), np.stack(norm)
 
 
@@ -139,7 +152,8 @@ def abs_backward_sub(q, k, v, g_w, g_u, qidx, kidx):
     gq = np.zeros((P, D, mq)); nq = np.zeros_like(gq)
     gk = np.zeros((P, D, nk_)); nk = np.zeros_like(gk)
     gv = np.zeros((P, nk_, C)); nv = np.zeros_like(gv)
-    for p in range(P):
+
+    def one(p):                                           # writes only the slices of p
         qi, ki = qidx[p], kidx[p]
         Bq = g_w[p][qi] @ v[p].T                          # (mq, N)
         Bk = g_w[p] @ v[p][ki].T                          # (M, nk)
@@ -156,6 +170,8 @@ def abs_backward_sub(q, k, v, g_w, g_u, qidx, kidx):
             A = np.abs(xk)                                # |k_n - q_m|
             gv[p] += A.T @ g_w[p]
             nv[p] += A.T @ np.abs(g_w[p])
+
+    _map(one, P)
     return (gq, gk, gv), (nq, nk, nv)
 
 
@@ -164,7 +180,16 @@ def stable_sort(x):
     """(sorted, perm) along the last axis: np.argsort(kind="stable") on the fp32 values, -0.0 == +0.0, sorted values
     written as +0.0 for -0.0 (the CUB contract at Weighted_Abs_Sum/csrc/sort_utils.cu:85-87)."""
     x = np.asarray(x, dtype=np.float32)
-    perm = np.argsort(x, axis=-1, kind="stable")
+    flat = x.reshape(-1, x.shape[-1])
+    perm = np.empty(flat.shape, dtype=np.int64)
+    chunk = max(1, (flat.shape[0] + 15) // 16)
+
+    def one(i):                                           # rows [i * chunk, (i + 1) * chunk)
+        r = slice(i * chunk, (i + 1) * chunk)
+        perm[r] = np.argsort(flat[r], axis=-1, kind="stable")
+
+    _map(one, (flat.shape[0] + chunk - 1) // chunk)
+    perm = perm.reshape(x.shape)
     srt = np.take_along_axis(x, perm, axis=-1) + np.float32(0.0)   # -0.0 + 0.0 == +0.0
     return srt, perm
 
@@ -173,11 +198,10 @@ def merge_rank(q, k):
     """rank[..., m] = #{n : k[..., n] < q[..., m]} = np.searchsorted(sorted(k), q, side="left")."""
     q = np.asarray(q, dtype=np.float32)
     k = np.asarray(k, dtype=np.float32)
-    ks = np.sort(k, axis=-1)
     flat_q = q.reshape(-1, q.shape[-1])
-    flat_k = ks.reshape(-1, ks.shape[-1])
-    out = np.stack([np.searchsorted(flat_k[i], flat_q[i], side="left") for i in range(flat_q.shape[0])])
-    return out.reshape(q.shape)
+    flat_k = k.reshape(-1, k.shape[-1])
+    out = _map(lambda i: np.searchsorted(np.sort(flat_k[i]), flat_q[i], side="left"), flat_q.shape[0])
+    return np.stack(out).reshape(q.shape)
 
 
 # ------------------------------------------------------------------------------ independent formulation (pinning)

@@ -132,12 +132,17 @@ def test_laplace_forward(dev, shape, kind, route):
     _assert_rel(_np(u), ou, ou, "laplace out_u")
 
 
-def test_laplace_wide_spread_underflow(dev):
+@pytest.mark.parametrize("N,M", [(500, 400), (3000, 2500)])
+def test_laplace_wide_spread_underflow(dev, N, M, route):
+    """Spread 40: most decay factors underflow to 0 and whole key ranges are cut off from each other; both routes,
+    and N = 3000 walks on either (above the dense cutoff)."""
     from weighted_laplace_sum import weighted_laplace_sum
-    q, k, v = _data(2, 3, 500, 400, 16, seed=5, kind="wide")
+    _same_route(route, N, M)
+    q, k, v = _data(2, 3, N, M, 16, seed=5, kind="wide")
     w, u = weighted_laplace_sum(_t(q, dev), _t(k, dev), _t(v, dev))
     ow, ou, nw = brute.laplace_sum(q, k, v)
     _assert_rel(_np(w), ow, nw, "laplace out_w (wide)")
+    _assert_rel(_np(u), ou, ou, "laplace out_u (wide)")
     _assert_rel(_np(u), ou, ou, "laplace out_u (wide)")
 
 
@@ -335,6 +340,29 @@ def test_gpu_validation_errors(dev):
     # the fused path within its range runs
     w, u = weighted_abs_sum_full(q, k, torch.randn(1, 8, 4, device=dev), backend="cuda-fused")
     assert w.shape == (1, 8, 4) and u.shape == (1, 8)
+
+
+@pytest.mark.parametrize("backend", ["cuda-fused", "cuda-global"])
+@pytest.mark.parametrize("shape", [(2, 3, 600, 500, 64), (1, 2, 4096, 4096, 33)])
+def test_pinned_paths_against_oracle(dev, backend, shape):
+    """backend="cuda-fused" (path 1, max(N, M) <= 4096) and "cuda-global" (path 0) give the oracle's sums, forward and
+    backward, like "auto"."""
+    from weighted_abs_sum import weighted_abs_sum, weighted_abs_sum_full
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 7, kind="ties")
+    g_w = np.random.default_rng(8).standard_normal((P, M, C)).astype(np.float32)
+    tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+    w, u = weighted_abs_sum_full(tq, tk, tv, backend=backend)
+    (w * _t(g_w, dev)).sum().backward()
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _assert_rel(_np(w), ow, nw, f"{backend} out_w")
+    _assert_rel(_np(u), ou, ou, f"{backend} out_u")
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w)
+    _assert_rel(_np(tq.grad), wq, nq, f"{backend} grad_q")
+    _assert_rel(_np(tk.grad), wk, nk, f"{backend} grad_k")
+    _assert_rel(_np(tv.grad), wv, nv, f"{backend} grad_v")
+    w2 = weighted_abs_sum(tq.detach(), tk.detach(), tv.detach(), backend=backend)
+    _assert_rel(_np(w2), ow, nw, f"{backend} plain out_w")
 
 
 def test_non_default_stream_and_repeat(dev):

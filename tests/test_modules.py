@@ -51,10 +51,29 @@ def test_nomic_kernel_attention_loads_and_matches_softmax():
     with torch.no_grad():
         want = model(input_ids=ids, attention_mask=mask).last_hidden_state
         head_dim = model.config.hidden_size // model.config.num_attention_heads
+        params = {n: p.data_ptr() for n, p in model.named_parameters()}
         modules.use_kernel_attention(model, "softmax", tau=head_dim ** 0.25)
         for layer in model.layers:
-            assert type(layer.self_attn).__name__ == "KernelAttention"
+            assert layer.self_attn.qlka_kernel == ("softmax", head_dim ** 0.25, "efficient")
+        assert model.config._attn_implementation == modules.REGISTRY_NAME
+        assert {n: p.data_ptr() for n, p in model.named_parameters()} == params    # weights stay in place
         got = model(input_ids=ids, attention_mask=mask).last_hidden_state
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+
+def test_nomic_standalone_kernel_attention_matches_layer():
+    """KernelAttention(config, ...) takes a layer's state_dict and gives that layer's output under softmax."""
+    model = _nomic(layers=1)
+    head_dim = model.config.hidden_size // model.config.num_attention_heads
+    layer = model.layers[0].self_attn
+    attn = modules.KernelAttention(model.config, "softmax", tau=head_dim ** 0.25)
+    attn.load_state_dict(layer.state_dict())
+    assert model.config._attn_implementation == "sdpa"           # the model's own config is untouched
+    x = torch.randn(2, 9, model.config.hidden_size)
+    pos = model.rotary_emb(x, torch.arange(9)[None, :])
+    with torch.no_grad():
+        want, _ = layer(x, attention_mask=None, position_embeddings=pos)
+        got, _ = attn(x, attention_mask=None, position_embeddings=pos)
     torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
 
 
