@@ -39,6 +39,16 @@ int qlka_version(void);
  * (Weighted_Abs_Sum/weighted_abs_sum/ops.py:21-25), which picks the KeOps backend in Python.
  */
 int qlka_set_direct_max(int n);
+/*
+ * Workspace budget in bytes (default 8 GiB). Every operator below runs its whole pipeline on chunks of consecutive
+ * p = (batch, head) indices (every stage works on each p alone), taking the largest chunk the workspace it is given
+ * holds (at least one p), so the caller bounds device memory by the workspace it passes. The *_ws_bytes() queries
+ * report the workspace of the largest chunk within this budget (one p when even one p exceeds it); results do not
+ * depend on the chunking. Process-wide; returns the previous value. The reference has no counterpart: its
+ * workspace is O(P*D*(N+M)) (Weighted_Abs_Sum/csrc/binding.cpp:101-111), where this build's per-feature slab of
+ * contribution rows is O(P*D*M*C).
+ */
+size_t qlka_set_workspace_budget(size_t bytes);
 
 /*
  * weighted_laplace_sum forward.

@@ -115,6 +115,39 @@ int check_ws(void* ws, size_t have, size_t need) {
     return QLKA_OK;
 }
 
+// ---- p-chunking. Every stage of every operator works on each p = (batch, head) on its own, so a call can run its
+// whole pipeline (sorts, range passes, walks, reduce, epilogue) on a chunk of pc consecutive p at a time, with a
+// workspace sized for pc. An operator takes the largest chunk that the workspace it is given holds; the *_ws_bytes()
+// queries size the workspace for the largest chunk within the process-wide budget (qlka_set_workspace_budget).
+std::atomic<size_t> g_ws_budget{size_t(8) << 30};
+
+// largest pc in [1, P] with bytes(pc) <= cap, or 1 when even one p does not fit (bytes() grows with pc)
+template <class Bytes>
+int fit_chunk(int P, size_t cap, Bytes bytes) {
+    if (bytes(P) <= cap) return P;
+    int lo = 1, hi = P - 1;
+    while (lo < hi) {
+        const int mid = lo + (hi - lo + 1) / 2;
+        if (bytes(mid) <= cap) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// bytes(pc) of the chunk a workspace query reports: the largest within the budget
+template <class Bytes>
+size_t budget_bytes(int P, Bytes bytes) {
+    return bytes(fit_chunk(P, g_ws_budget.load(std::memory_order_relaxed), bytes));
+}
+
+// f(p0, np) for the chunks [p0, p0 + np) of [0, P); stops at the first error
+template <class F>
+int for_chunks(int P, int pc, F f) {
+    for (int p0 = 0; p0 < P; p0 += pc)
+        if (int e = f(p0, std::min(pc, P - p0))) return e;
+    return QLKA_OK;
+}
+
 int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, hipStream_t st) {
     int e = seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st);
     if (e) return hip_status(e, "segmented sort of k");
@@ -202,34 +235,53 @@ int qlka_set_direct_max(int n) {
     return g_direct_max.exchange(n);
 }
 
+size_t qlka_set_workspace_budget(size_t bytes) { return g_ws_budget.exchange(bytes); }
+
 // ------------------------------------------------------------------------------------------------ laplace forward
 static WsSpec laplace_spec(int P, int D, int N, int M, int C) { return WsSpec{P, D, N, M, C, N, M, true}; }
 
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return ws_bytes(laplace_spec(P, D, N, M, C));
+    return budget_bytes(P, [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); });
 }
+
+}  // extern "C"
+
+namespace {
+// One chunk of np p (pointers already offset to its first p): sort k, group q, range passes, walk, reduce.
+int laplace_chunk(const float* q, const float* k, const float* v, float* out_w, float* out_u, int np, int D, int N,
+                  int M, int C, void* ws, hipStream_t st) {
+    const int S = np * D;
+    SortedWs w = carve(ws, laplace_spec(np, D, N, M, C));
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    if (int e = group_q(q, w, 0.f, S, N, M, C, st)) return e;
+    int e = hip_status(laplace_prepare(w.ks, w.kp, v, np, D, N, C, w.ra, st), "laplace ranges");
+    if (e) return e;
+    e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, np, D, N, M, C, w.ra, st);
+    if (e) return hip_status(e, "laplace walk");
+    e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, out_w, out_u, np, D, M, C, st);
+    return hip_status(e, "laplace reduce");
+}
+}  // namespace
+
+extern "C" {
 
 int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
                      int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !out_w || !out_u) return fail(QLKA_EINVAL, "q, k, v, out_w and out_u must be non-null");
-    const WsSpec spec = laplace_spec(P, D, N, M, C);
-    if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
+    auto bytes = [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); };
+    const int pc = fit_chunk(P, ws_bytes_given, bytes);
+    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
     hipStream_t st = (hipStream_t)stream;
     if (dense_laplace_fwd(N, M))
         return hip_status(direct_fwd(1, q, k, v, out_w, out_u, P, D, N, M, C, st), "laplace direct sum");
-    const int S = P * D;
-    SortedWs w = carve(ws, spec);
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
-    if (int e = group_q(q, w, 0.f, S, N, M, C, st)) return e;
-    int e = hip_status(laplace_prepare(w.ks, w.kp, v, P, D, N, C, w.ra, st), "laplace ranges");
-    if (e) return e;
-    e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
-    if (e) return hip_status(e, "laplace walk");
-    e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, out_w, out_u, P, D, M, C, st);
-    return hip_status(e, "laplace reduce");
+    return for_chunks(P, pc, [&](int p0, int np) {
+        const size_t p = (size_t)p0;
+        return laplace_chunk(q + p * D * M, k + p * D * N, v + p * N * C, out_w + p * M * C, out_u + p * M, np, D, N,
+                             M, C, ws, st);
+    });
 }
 
 // ---------------------------------------------------------------------------------------------------- abs forward
@@ -237,7 +289,7 @@ static WsSpec abs_fwd_spec(int P, int D, int N, int M, int C, bool full) { retur
 
 size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return ws_bytes(abs_fwd_spec(P, D, N, M, C, true));
+    return budget_bytes(P, [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); });
 }
 
 }  // extern "C"
@@ -246,6 +298,42 @@ namespace {
 // Sorted k and q of one call, in caller-owned buffers (k_sorted / q_sorted as sorted keys, k_perm / q_perm as their
 // permutations), so that the backward of the same inputs can skip both sorts.
 struct Presorted { float* ks; uint32_t* kp; float* qs; uint32_t* qp; };
+
+Presorted offset(const Presorted& a, size_t p0, int D, int N, int M) {
+    return Presorted{a.ks + p0 * D * N, a.kp + p0 * D * N, a.qs + p0 * D * M, a.qp + p0 * D * M};
+}
+
+// One chunk of np p of the abs forward (pointers offset to its first p); keep: the sorts go to these buffers.
+int abs_fwd_chunk(const float* q, const float* k, const float* v, float* out_w, float* out_u, int np, int D, int N,
+                  int M, int C, const Presorted* keep, void* ws, hipStream_t st) {
+    const int S = np * D;
+    SortedWs w = carve(ws, abs_fwd_spec(np, D, N, M, C, true));
+    if (keep) { w.ks = keep->ks; w.kp = keep->kp; w.qs = keep->qs; w.qp = keep->qp; }
+    AbsWalkArgs a{};
+    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
+    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
+    a.slab = w.slab; a.uslab = out_u ? w.uslab : nullptr; a.CR = slab_stride(C);
+    a.out_dot = nullptr; a.out_rank = nullptr;
+    a.sign = 1.f; a.P = np; a.D = D; a.C = C;
+    const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    auto key_side = [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); };
+    int e = 0;
+    if (!keep) {
+        e = group_q(q, w, 0.f, S, N, M, C, st);
+        if (!e) e = key_side(st);
+    } else {
+        e = fork_join(st, key_side, [&](hipStream_t s) {
+            if (int r = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s))
+                return hip_status(r, "segmented sort of q");
+            return hip_status(range_bounds(a, w.ra.qb, s), "query bounds"); });
+    }
+    if (e) return e;
+    e = abs_emit(a, mode, w.ra, st);
+    if (e) return hip_status(e, "abs walk");
+    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, w.uq, out_w, out_u, np, D, M, C, st);
+    return hip_status(e, "abs reduce");
+}
 
 int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P, int D, int N, int M,
                  int C, int path, const Presorted* keep, int* kept, void* ws, size_t ws_bytes_given, void* stream) {
@@ -261,45 +349,33 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         return fail(QLKA_EINVAL, "fused path pinned but unavailable: needs max(N,M) <= 4096 and the "
                                  "bucket's shared memory to fit this device");
     // the workspace is sized for the _full op (an upper bound of the plain one), so one size serves both
-    const WsSpec spec = abs_fwd_spec(P, D, N, M, C, true);
-    if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
+    auto bytes = [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); };
+    const int pc = fit_chunk(P, ws_bytes_given, bytes);
+    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
     hipStream_t st = (hipStream_t)stream;
-    const int S = P * D;
-    SortedWs w = carve(ws, spec);
     const bool keep_sorts = keep && !dense_sign(P, N, M);   // the backward will walk: hand it the sorts
-    if (keep_sorts) { w.ks = keep->ks; w.kp = keep->kp; w.qs = keep->qs; w.qp = keep->qp; }
     if (path == -1 && dense_abs_fwd(N, M)) {
         if (keep_sorts) {
-            if (int e = sort_both(q, k, w, S, N, M, st)) return e;
+            const int e = for_chunks(P, pc, [&](int p0, int np) {
+                const Presorted ks = offset(*keep, (size_t)p0, D, N, M);
+                SortedWs w = carve(ws, abs_fwd_spec(np, D, N, M, C, true));
+                w.ks = ks.ks; w.kp = ks.kp; w.qs = ks.qs; w.qp = ks.qp;
+                const size_t p = (size_t)p0;
+                return sort_both(q + p * D * M, k + p * D * N, w, np * D, N, M, st); });
+            if (e) return e;
             *kept = 1;
         }
         return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
     }
-    AbsWalkArgs a{};
-    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
-    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
-    a.slab = w.slab; a.uslab = out_u ? w.uslab : nullptr; a.CR = slab_stride(C);
-    a.out_dot = nullptr; a.out_rank = nullptr;
-    a.sign = 1.f; a.P = P; a.D = D; a.C = C;
-    const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
-    auto key_side = [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); };
-    int e = 0;
-    if (!keep_sorts) {
-        e = group_q(q, w, 0.f, S, N, M, C, st);
-        if (!e) e = key_side(st);
-    } else {
-        e = fork_join(st, key_side, [&](hipStream_t s) {
-            if (int r = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s))
-                return hip_status(r, "segmented sort of q");
-            return hip_status(range_bounds(a, w.ra.qb, s), "query bounds"); });
-    }
+    const int e = for_chunks(P, pc, [&](int p0, int np) {
+        const size_t p = (size_t)p0;
+        const Presorted ks = keep_sorts ? offset(*keep, p, D, N, M) : Presorted{};
+        return abs_fwd_chunk(q + p * D * M, k + p * D * N, v + p * N * C, out_w + p * M * C,
+                             out_u ? out_u + p * M : nullptr, np, D, N, M, C, keep_sorts ? &ks : nullptr, ws, st);
+    });
     if (e) return e;
     if (keep_sorts) *kept = 1;
-    e = abs_emit(a, mode, w.ra, st);
-    if (e) return hip_status(e, "abs walk");
-    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, w.uq, out_w, out_u, P, D, M, C, st);
-    return hip_status(e, "abs reduce");
+    return QLKA_OK;
 }
 }  // namespace
 
@@ -326,27 +402,18 @@ static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
 
 size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return ws_bytes(abs_bwd_spec(P, D, N, M, C));
+    return budget_bytes(P, [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); });
 }
 
 }  // extern "C"
 
 namespace {
-int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
-                 float* grad_k, float* grad_v, int P, int D, int N, int M, int C, const Presorted* pre, void* ws,
-                 size_t ws_bytes_given, void* stream) {
-    g_err.clear();
-    if (int e = check_dims(P, D, N, M, C)) return e;
-    if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
-        return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
-    const WsSpec spec = abs_bwd_spec(P, D, N, M, C);
-    if (int e = check_ws(ws, ws_bytes_given, ws_bytes(spec))) return e;
-    hipStream_t st = (hipStream_t)stream;
-    if (dense_sign(P, N, M))     // the walks' convention: a tie counts -1 in both gradients
-        return hip_status(direct_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st),
-                          "dense backward");
-    const int S = P * D;
-    SortedWs w = carve(ws, spec);
+// One chunk of np p of the abs backward (pointers offset to its first p); pre: the forward's sorts of the chunk.
+int abs_bwd_chunk(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
+                  float* grad_k, float* grad_v, int np, int D, int N, int M, int C, const Presorted* pre, void* ws,
+                  hipStream_t st) {
+    const int S = np * D;
+    SortedWs w = carve(ws, abs_bwd_spec(np, D, N, M, C));
     if (pre) { w.ks = pre->ks; w.kp = pre->kp; w.qs = pre->qs; w.qp = pre->qp; }   // sorted by the forward
     else if (int e = sort_both(q, k, w, S, N, M, st)) return e;
 
@@ -354,7 +421,7 @@ int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_
     AbsWalkArgs a{};
     a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
     a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g_w; a.uq = g_u;
-    a.out_dot = grad_q; a.sign = 1.f; a.P = P; a.D = D; a.C = C;
+    a.out_dot = grad_q; a.sign = 1.f; a.P = np; a.D = D; a.C = C;
     int e = abs_walk(a, g_u ? (ABS_DOT | ABS_DOTX1) : ABS_DOT, w.ra, st);
     if (e) return hip_status(e, "grad_q walk");
 
@@ -363,11 +430,34 @@ int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_
     b.ks = w.qs; b.kp = w.qp; b.Ns = M; b.w = g_w; b.u = g_u;
     b.qs = w.ks; b.qp = w.kp; b.Mq = N; b.g = v; b.uq = nullptr;
     b.slab = w.slab; b.uslab = nullptr; b.CR = slab_stride(C);
-    b.out_dot = grad_k; b.sign = 1.f; b.P = P; b.D = D; b.C = C;
+    b.out_dot = grad_k; b.sign = 1.f; b.P = np; b.D = D; b.C = C;
     e = abs_walk(b, g_u ? (ABS_ROW | ABS_DOT | ABS_DOTX2) : (ABS_ROW | ABS_DOT), w.ra, st);
     if (e) return hip_status(e, "grad_k/grad_v walk");
-    e = reduce_slabs(w.slab, nullptr, nullptr, nullptr, grad_v, nullptr, P, D, N, C, st);
+    e = reduce_slabs(w.slab, nullptr, nullptr, nullptr, grad_v, nullptr, np, D, N, C, st);
     return hip_status(e, "grad_v reduce");
+}
+
+int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
+                 float* grad_k, float* grad_v, int P, int D, int N, int M, int C, const Presorted* pre, void* ws,
+                 size_t ws_bytes_given, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
+        return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
+    auto bytes = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
+    const int pc = fit_chunk(P, ws_bytes_given, bytes);
+    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    if (dense_sign(P, N, M))     // the walks' convention: a tie counts -1 in both gradients
+        return hip_status(direct_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st),
+                          "dense backward");
+    return for_chunks(P, pc, [&](int p0, int np) {
+        const size_t p = (size_t)p0;
+        const Presorted ps = pre ? offset(*pre, p, D, N, M) : Presorted{};
+        return abs_bwd_chunk(q + p * D * M, k + p * D * N, v + p * N * C, g_w + p * M * C, g_u ? g_u + p * M : nullptr,
+                             grad_q + p * D * M, grad_k + p * D * N, grad_v + p * N * C, np, D, N, M, C,
+                             pre ? &ps : nullptr, ws, st);
+    });
 }
 }  // namespace
 
@@ -393,9 +483,11 @@ int qlka_abs_bwd_sorted(const float* q, const float* k, const float* v, const fl
 }
 
 // -------------------------------------------------------------------------------------------------------- sgn sum
+static WsSpec sgn_spec(int P, int D, int N, int M, int C) { return WsSpec{P, D, N, M, C, N, 0, false}; }
+
 size_t qlka_sgn_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return ws_bytes(WsSpec{P, D, N, M, C, N, 0, false});
+    return budget_bytes(P, [&](int pc) { return ws_bytes(sgn_spec(pc, D, N, M, C)); });
 }
 
 int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g, float* out,
@@ -403,19 +495,22 @@ int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g,
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g || !out) return fail(QLKA_EINVAL, "q, k, v, g and out must be non-null");
-    if (int e = check_ws(ws, ws_bytes_given, qlka_sgn_fwd_ws_bytes(P, D, N, M, C))) return e;
+    auto bytes = [&](int pc) { return ws_bytes(sgn_spec(pc, D, N, M, C)); };
+    const int pc = fit_chunk(P, ws_bytes_given, bytes);
+    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
     hipStream_t st = (hipStream_t)stream;
     if (dense_sign(P, N, M))     // sgn(k - q) with a tie counted +1 == -(s(q - k) with a tie counted -1)
         return hip_status(direct_sign(true, q, k, g, v, nullptr, out, -1.f, -1.f, P, D, M, N, C, st), "dense sgn sum");
-    const int S = P * D;
-    SortedWs w = carve(ws, WsSpec{P, D, N, M, C, N, 0, false});
-    if (int e = sort_both(q, k, w, S, N, M, st)) return e;
-    AbsWalkArgs a{};
-    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v;
-    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g;
-    a.out_dot = out; a.sign = -1.f; a.P = P; a.D = D; a.C = C;
-    int e = abs_walk(a, ABS_DOT, w.ra, st);
-    return hip_status(e, "sgn walk");
+    return for_chunks(P, pc, [&](int p0, int np) {
+        const size_t p = (size_t)p0;
+        SortedWs w = carve(ws, sgn_spec(np, D, N, M, C));
+        if (int e = sort_both(q + p * D * M, k + p * D * N, w, np * D, N, M, st)) return e;
+        AbsWalkArgs a{};
+        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v + p * N * C;
+        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g + p * M * C;
+        a.out_dot = out + p * D * M; a.sign = -1.f; a.P = np; a.D = D; a.C = C;
+        return hip_status(abs_walk(a, ABS_DOT, w.ra, st), "sgn walk");
+    });
 }
 
 // -------------------------------------------------------------------------------------------- direct evaluation
@@ -508,7 +603,7 @@ LayerWs carve_layer(int kind, void* ws, const WsSpec& s) {
 
 size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || kind < 0 || kind > 2) return 0;
-    return layer_ws_bytes(kind, WsSpec{P, D, N, M, C, N, M, true});
+    return budget_bytes(P, [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); });
 }
 
 // Both layer entry points: keep == null is the reference's composition over pre-masked k, v and n_pad; keep != null
@@ -524,15 +619,10 @@ static int layer_reduce_folded(int kind, bool masked, const float* q, const floa
                       "layer reduce");
 }
 
-static int layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad,
-                     const uint8_t* keep, float* out, int P, int D, int N, int M, int C, void* ws,
-                     size_t ws_bytes_given, void* stream) {
-    if (kind < 0 || kind > 2) return fail(QLKA_EINVAL, "kind must be 0 (add_laplace), 1 (add_riesz) or 2 (add_bump)");
-    if (int e = check_dims(P, D, N, M, C)) return e;
-    if (!q || !k || !v || !out) return fail(QLKA_EINVAL, "q, k, v and out must be non-null");
+// One chunk of P p of a layer (pointers offset to its first p).
+static int layer_chunk(int kind, const float* q, const float* k, const float* v, const float* n_pad,
+                       const uint8_t* keep, float* out, int P, int D, int N, int M, int C, void* ws, hipStream_t st) {
     const WsSpec spec{P, D, N, M, C, N, M, true};
-    if (int e = check_ws(ws, ws_bytes_given, layer_ws_bytes(kind, spec))) return e;
-    hipStream_t st = (hipStream_t)stream;
     const int S = P * D;
     LayerWs L = carve_layer(kind, ws, spec);
     SortedWs& w = L.op;
@@ -606,6 +696,22 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
     return hip_status(e, "layer epilogue");
 }
 
+static int layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad,
+                     const uint8_t* keep, float* out, int P, int D, int N, int M, int C, void* ws,
+                     size_t ws_bytes_given, void* stream) {
+    if (kind < 0 || kind > 2) return fail(QLKA_EINVAL, "kind must be 0 (add_laplace), 1 (add_riesz) or 2 (add_bump)");
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !out) return fail(QLKA_EINVAL, "q, k, v and out must be non-null");
+    auto bytes = [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); };
+    const int pc = fit_chunk(P, ws_bytes_given, bytes);
+    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
+    return for_chunks(P, pc, [&](int p0, int np) {
+        const size_t p = (size_t)p0;
+        return layer_chunk(kind, q + p * D * M, k + p * D * N, v + p * N * C, n_pad ? n_pad + p : nullptr,
+                           keep ? keep + p * N : nullptr, out + p * M * C, np, D, N, M, C, ws, (hipStream_t)stream);
+    });
+}
+
 int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad, float* out,
                    int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
@@ -658,3 +764,13 @@ int qlka_merge_rank(const float* q, const float* k, int32_t* rank, int num_segs,
 }
 
 }  // extern "C"
+
+namespace qlka {
+// For the allocation-free entry point (noalloc.hip), which runs qlka_laplace_fwd over its own static workspace.
+int validate_dims(int P, int D, int N, int M, int C) {
+    g_err.clear();
+    return check_dims(P, D, N, M, C);
+}
+size_t laplace_fwd_chunk_ws(int pc, int D, int N, int M, int C) { return ws_bytes(laplace_spec(pc, D, N, M, C)); }
+int report_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace qlka

@@ -199,4 +199,11 @@ int layer_epilogue_params(int kind, bool masked, const float* q, const float* n_
 int reduce_slabs_layer(int kind, bool masked, const ReduceEpilogue& ep, const float* slab, const float* uslab,
                        const uint32_t* qperm, float* uq, int P, int D, int M, int C, hipStream_t st);
 
+// ---- capi.hip helpers for noalloc.hip
+// check_dims of the C ABI (clears the thread's error first); the workspace of a Laplace forward over pc p at a time;
+// set the thread's error message and return code
+int validate_dims(int P, int D, int N, int M, int C);
+size_t laplace_fwd_chunk_ws(int pc, int D, int N, int M, int C);
+int report_error(int code, const char* msg);
+
 }  // namespace qlka

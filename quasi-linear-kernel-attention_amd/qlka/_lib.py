@@ -42,6 +42,7 @@ _SIGNATURES = {
     "qlka_merge_rank_ws_bytes": (_c_size, [_c_int] * 3),
     "qlka_merge_rank": (_c_int, [_c_ptr] * 3 + [_c_int] * 3 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_set_direct_max": (_c_int, [_c_int]),
+    "qlka_set_workspace_budget": (_c_size, [_c_size]),
     "qlka_timing_enable": (_c_int, [_c_int]),
     "qlka_timing_reset": (_c_int, []),
     "qlka_timing_read": (_c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_longlong)]),

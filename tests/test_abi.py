@@ -54,6 +54,24 @@ def test_version_and_workspace_sizes(lib):
     assert lib.qlka_laplace_fwd_ws_bytes(0, 1, 1, 1, 1) == 0
 
 
+def test_workspace_budget_sizes_the_queries(lib):
+    """The budget picks the largest chunk of p whose workspace fits it (one p at least); no GPU is touched."""
+    prev = lib.qlka_set_workspace_budget(8 << 30)
+    try:
+        dims = (12, 64, 16384, 16384, 64)
+        full = lib.qlka_laplace_fwd_ws_bytes(*dims)
+        one = lib.qlka_laplace_fwd_ws_bytes(1, *dims[1:])
+        assert lib.qlka_set_workspace_budget(1) == 8 << 30
+        assert lib.qlka_laplace_fwd_ws_bytes(*dims) == one
+        assert lib.qlka_abs_bwd_ws_bytes(*dims) == lib.qlka_abs_bwd_ws_bytes(1, *dims[1:])
+        lib.qlka_set_workspace_budget(3 * one + 10)
+        assert lib.qlka_laplace_fwd_ws_bytes(*dims) == lib.qlka_laplace_fwd_ws_bytes(3, *dims[1:])
+        lib.qlka_set_workspace_budget(1 << 62)
+        assert lib.qlka_laplace_fwd_ws_bytes(*dims) == full
+    finally:
+        lib.qlka_set_workspace_budget(prev)
+
+
 @pytest.mark.parametrize("dims,msg", [
     ((1, 1, 8, 8, 129), "C (v.size(2)) must be in [1, 128]"),
     ((1, 1, 8, 8, 0), "C (v.size(2)) must be in [1, 128]"),
