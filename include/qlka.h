@@ -60,6 +60,18 @@ size_t qlka_set_workspace_budget(size_t bytes);
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C);
 int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
                      int P, int D, int N, int M, int C, void* ws, size_t ws_bytes, void* stream);
+/*
+ * qlka_laplace_fwd without a workspace argument and without any device allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Its workspace is a static 512 MiB device array of the library, held on every device the
+ * library runs on until the process ends; the call runs qlka_laplace_fwd over it one chunk of p at a time and gives
+ * the same results. Shapes whose single-p workspace (qlka_laplace_fwd_ws_bytes(1, D, N, M, C)) exceeds 512 MiB are
+ * refused with QLKA_EINVAL (N = M = 16384, D = C = 64 needs 297 MiB). `stream` must belong to the current device.
+ * All calls on one device share the array: calls that overlap in time on one device (e.g. on two streams) race and
+ * must be serialised by the caller.
+ */
+int qlka_laplace_fwd_noalloc(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                             int P, int D, int N, int M, int C, void* stream);
 
 /*
  * weighted_abs_sum forward; out_u == NULL gives the plain op, out_u != NULL the _full op.

@@ -22,6 +22,7 @@ _SIGNATURES = {
     "qlka_version": (_c_int, []),
     "qlka_laplace_fwd_ws_bytes": (_c_size, [_c_int] * 5),
     "qlka_laplace_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
+    "qlka_laplace_fwd_noalloc": (_c_int, [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr]),
     "qlka_abs_fwd_ws_bytes": (_c_size, [_c_int] * 5),
     "qlka_abs_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] * 6 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_abs_bwd_ws_bytes": (_c_size, [_c_int] * 5),
