@@ -169,7 +169,11 @@ static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int 
 // the work already on the caller's stream, and the caller's stream after the side stream's work. A host thread issues
 // its calls in order, so reusing its two events is safe; a fork / join through events is also how work on a captured
 // stream reaches another stream.
-struct SideStream { hipStream_t s = nullptr; hipEvent_t fork = nullptr, join = nullptr; };
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+    hipEvent_t walked = nullptr, reduced[2] = {nullptr, nullptr};   // the chunk pipeline's events (run_pipeline)
+};
 
 hipError_t side_stream(hipStream_t st, SideStream** out) {
     *out = nullptr;
@@ -195,6 +199,9 @@ hipError_t side_stream(hipStream_t st, SideStream** out) {
         if ((e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&n.join, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&n.walked, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&n.reduced[0], hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&n.reduced[1], hipEventDisableTiming)) != hipSuccess) return e;
         sd = n;
     }
     *out = &sd;
@@ -221,6 +228,78 @@ int fork_join(hipStream_t st, KeySide key_side, QuerySide query_side) {
     return w == hipSuccess ? QLKA_OK : hip_status((int)w, "join");
 }
 
+// ---- pipelined p-chunks
+// A chunk's work falls in three parts: prep (the sorts and the query grouping: LDS- and VALU-bound), main (the range
+// passes and the walk) and back (the reduce of the chunk's slab: an HBM-bound stream). With two workspace copies the
+// chunks are pipelined over the caller's stream and the side stream: prep and main of chunk j run on the caller's
+// stream, its back on the side stream once its walk is done, so that the reduce of chunk j runs beside the prep of
+// chunk j + 1. The main part of chunk j + 1 waits for that reduce: measured beside it, the range passes' gathers ran
+// 3x slower (71 -> 212 us a pass at the headline shape), the sorts and the grouping at about their own speed. The
+// prep of chunk j + 2 overwrites copy j % 2 and so waits for the reduce of chunk j. With one copy, or without a side
+// stream (a thread's first call inside a stream capture, a stream of another device), the chunks run in order on the
+// caller's stream. Every fork is joined back to the caller's stream before returning, errors included.
+constexpr int PIPE_CHUNKS = 3;       // chunks of a pipelined call (3 of 2, 3, 4, 6 measured fastest at the headline)
+
+struct Plan { int pc; int nbuf; };
+
+// Chunking of a call over P p whose chunk buffer of pc p needs bytes1(pc) workspace bytes, within `cap` bytes:
+// pipelined (PIPE_CHUNKS chunks, two copies) when `pipeline` and P >= 2, with smaller chunks if needed to fit two
+// copies; else in order with one copy, the largest chunk that fits (one p at least).
+template <class Bytes>
+Plan plan_chunks(int P, size_t cap, bool pipeline, Bytes bytes1) {
+    if (pipeline && P >= 2) {
+        const int nc = std::min(P, PIPE_CHUNKS);
+        const int pc = (P + nc - 1) / nc;
+        if (2 * bytes1(pc) <= cap) return Plan{pc, 2};
+        const int pc2 = fit_chunk(P, cap, [&](int c) { return 2 * bytes1(c); });
+        if (2 * bytes1(pc2) <= cap) return Plan{pc2, 2};
+    }
+    return Plan{fit_chunk(P, cap, bytes1), 1};
+}
+
+template <class Bytes>
+size_t plan_bytes(const Plan& pl, Bytes bytes1) { return (size_t)pl.nbuf * bytes1(pl.pc); }
+
+// A call is pipelined when each of its chunks still fills the GPU many times over (below about 4M query-features
+// the per-chunk launch tails outweigh the overlap).
+inline bool pipelined(int P, int D, int M) { return P >= 2 && (int64_t)P * D * M >= (int64_t(1) << 22); }
+
+// prep / main / back: int(p0, np, buf, stream) for the chunk [p0, p0 + np) over workspace copy `buf`.
+template <class Prep, class Main, class Back>
+int run_pipeline(int P, const Plan& pl, void* ws, size_t copy, hipStream_t st, Prep prep, Main main, Back back) {
+    SideStream* sd = nullptr;
+    if (pl.nbuf == 2 && (P + pl.pc - 1) / pl.pc > 1) {
+        if (hipError_t e = side_stream(st, &sd)) return hip_status((int)e, "side stream");
+    }
+    if (sd == nullptr) {
+        return for_chunks(P, pl.pc, [&](int p0, int np) {
+            if (int e = prep(p0, np, ws, st)) return e;
+            if (int e = main(p0, np, ws, st)) return e;
+            return back(p0, np, ws, st); });
+    }
+    auto hipc = [](hipError_t e, const char* what) { return e == hipSuccess ? QLKA_OK : hip_status((int)e, what); };
+    int err = hipc(hipEventRecord(sd->fork, st), "fork");
+    if (!err) err = hipc(hipStreamWaitEvent(sd->s, sd->fork, 0), "fork");
+    int j = 0;
+    for (int p0 = 0; p0 < P && !err; p0 += pl.pc, ++j) {
+        const int np = std::min(pl.pc, P - p0);
+        void* buf = (char*)ws + (size_t)(j % 2) * copy;
+        if (j >= 2) err = hipc(hipStreamWaitEvent(st, sd->reduced[j % 2], 0), "pipeline");
+        if (!err) err = prep(p0, np, buf, st);
+        if (!err && j >= 1) err = hipc(hipStreamWaitEvent(st, sd->reduced[(j - 1) % 2], 0), "pipeline");
+        if (!err) err = main(p0, np, buf, st);
+        if (!err) err = hipc(hipEventRecord(sd->walked, st), "pipeline");
+        if (!err) err = hipc(hipStreamWaitEvent(sd->s, sd->walked, 0), "pipeline");
+        if (!err) err = back(p0, np, buf, sd->s);
+        if (!err) err = hipc(hipEventRecord(sd->reduced[j % 2], sd->s), "pipeline");
+    }
+    // join whatever happened, so that nothing later on st can overtake work issued on the side stream
+    const hipError_t r = hipEventRecord(sd->join, sd->s);
+    const hipError_t w = r == hipSuccess ? hipStreamWaitEvent(st, sd->join, 0) : r;
+    if (err) return err;
+    return w == hipSuccess ? QLKA_OK : hip_status((int)w, "join");
+}
+
 }  // namespace
 
 extern "C" {
@@ -242,46 +321,43 @@ static WsSpec laplace_spec(int P, int D, int N, int M, int C) { return WsSpec{P,
 
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return budget_bytes(P, [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); });
+    auto b1 = [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); };
+    return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, M), b1), b1);
 }
-
-}  // extern "C"
-
-namespace {
-// One chunk of np p (pointers already offset to its first p): sort k, group q, range passes, walk, reduce.
-int laplace_chunk(const float* q, const float* k, const float* v, float* out_w, float* out_u, int np, int D, int N,
-                  int M, int C, void* ws, hipStream_t st) {
-    const int S = np * D;
-    SortedWs w = carve(ws, laplace_spec(np, D, N, M, C));
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
-    if (int e = group_q(q, w, 0.f, S, N, M, C, st)) return e;
-    int e = hip_status(laplace_prepare(w.ks, w.kp, v, np, D, N, C, w.ra, st), "laplace ranges");
-    if (e) return e;
-    e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, np, D, N, M, C, w.ra, st);
-    if (e) return hip_status(e, "laplace walk");
-    e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, out_w, out_u, np, D, M, C, st);
-    return hip_status(e, "laplace reduce");
-}
-}  // namespace
-
-extern "C" {
 
 int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_w, float* out_u,
                      int P, int D, int N, int M, int C, void* ws, size_t ws_bytes_given, void* stream) {
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !out_w || !out_u) return fail(QLKA_EINVAL, "q, k, v, out_w and out_u must be non-null");
-    auto bytes = [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); };
-    const int pc = fit_chunk(P, ws_bytes_given, bytes);
-    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
+    auto b1 = [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); };
+    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, M), b1);
+    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     hipStream_t st = (hipStream_t)stream;
     if (dense_laplace_fwd(N, M))
         return hip_status(direct_fwd(1, q, k, v, out_w, out_u, P, D, N, M, C, st), "laplace direct sum");
-    return for_chunks(P, pc, [&](int p0, int np) {
+    // per chunk: sort k and group q; range passes and walk; reduce
+    auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
         const size_t p = (size_t)p0;
-        return laplace_chunk(q + p * D * M, k + p * D * N, v + p * N * C, out_w + p * M * C, out_u + p * M, np, D, N,
-                             M, C, ws, st);
-    });
+        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s), "segmented sort of k"))
+            return e;
+        return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
+    };
+    auto main = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
+        const float* vp = v + (size_t)p0 * N * C;
+        if (int e = hip_status(laplace_prepare(w.ks, w.kp, vp, np, D, N, C, w.ra, s), "laplace ranges")) return e;
+        return hip_status(laplace_emit(w.ks, w.kp, w.qs, w.qp, vp, w.slab, w.uslab, np, D, N, M, C, w.ra, s),
+                          "laplace walk");
+    };
+    auto back = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
+        const size_t p = (size_t)p0;
+        return hip_status(reduce_slabs(w.slab, w.uslab, w.qp, w.uq, out_w + p * M * C, out_u + p * M, np, D, M, C, s),
+                          "laplace reduce");
+    };
+    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back);
 }
 
 // ---------------------------------------------------------------------------------------------------- abs forward
@@ -289,7 +365,8 @@ static WsSpec abs_fwd_spec(int P, int D, int N, int M, int C, bool full) { retur
 
 size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return budget_bytes(P, [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); });
+    auto b1 = [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); };
+    return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, M), b1), b1);
 }
 
 }  // extern "C"
@@ -301,38 +378,6 @@ struct Presorted { float* ks; uint32_t* kp; float* qs; uint32_t* qp; };
 
 Presorted offset(const Presorted& a, size_t p0, int D, int N, int M) {
     return Presorted{a.ks + p0 * D * N, a.kp + p0 * D * N, a.qs + p0 * D * M, a.qp + p0 * D * M};
-}
-
-// One chunk of np p of the abs forward (pointers offset to its first p); keep: the sorts go to these buffers.
-int abs_fwd_chunk(const float* q, const float* k, const float* v, float* out_w, float* out_u, int np, int D, int N,
-                  int M, int C, const Presorted* keep, void* ws, hipStream_t st) {
-    const int S = np * D;
-    SortedWs w = carve(ws, abs_fwd_spec(np, D, N, M, C, true));
-    if (keep) { w.ks = keep->ks; w.kp = keep->kp; w.qs = keep->qs; w.qp = keep->qp; }
-    AbsWalkArgs a{};
-    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
-    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
-    a.slab = w.slab; a.uslab = out_u ? w.uslab : nullptr; a.CR = slab_stride(C);
-    a.out_dot = nullptr; a.out_rank = nullptr;
-    a.sign = 1.f; a.P = np; a.D = D; a.C = C;
-    const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
-    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
-    auto key_side = [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); };
-    int e = 0;
-    if (!keep) {
-        e = group_q(q, w, 0.f, S, N, M, C, st);
-        if (!e) e = key_side(st);
-    } else {
-        e = fork_join(st, key_side, [&](hipStream_t s) {
-            if (int r = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s))
-                return hip_status(r, "segmented sort of q");
-            return hip_status(range_bounds(a, w.ra.qb, s), "query bounds"); });
-    }
-    if (e) return e;
-    e = abs_emit(a, mode, w.ra, st);
-    if (e) return hip_status(e, "abs walk");
-    e = reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, w.uq, out_w, out_u, np, D, M, C, st);
-    return hip_status(e, "abs reduce");
 }
 
 int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P, int D, int N, int M,
@@ -349,14 +394,14 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         return fail(QLKA_EINVAL, "fused path pinned but unavailable: needs max(N,M) <= 4096 and the "
                                  "bucket's shared memory to fit this device");
     // the workspace is sized for the _full op (an upper bound of the plain one), so one size serves both
-    auto bytes = [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); };
-    const int pc = fit_chunk(P, ws_bytes_given, bytes);
-    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
+    auto b1 = [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); };
+    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, M), b1);
+    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     hipStream_t st = (hipStream_t)stream;
     const bool keep_sorts = keep && !dense_sign(P, N, M);   // the backward will walk: hand it the sorts
     if (path == -1 && dense_abs_fwd(N, M)) {
         if (keep_sorts) {
-            const int e = for_chunks(P, pc, [&](int p0, int np) {
+            const int e = for_chunks(P, pl.pc, [&](int p0, int np) {
                 const Presorted ks = offset(*keep, (size_t)p0, D, N, M);
                 SortedWs w = carve(ws, abs_fwd_spec(np, D, N, M, C, true));
                 w.ks = ks.ks; w.kp = ks.kp; w.qs = ks.qs; w.qp = ks.qp;
@@ -367,13 +412,48 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         }
         return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
     }
-    const int e = for_chunks(P, pc, [&](int p0, int np) {
+    const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
+    // the chunk's workspace view, with the sorted arrays in the caller's buffers when the sorts are kept
+    auto view = [&](int p0, int np, void* buf, SortedWs& w, AbsWalkArgs& a) {
+        w = carve(buf, abs_fwd_spec(np, D, N, M, C, true));
+        if (keep_sorts) {
+            const Presorted ks = offset(*keep, (size_t)p0, D, N, M);
+            w.ks = ks.ks; w.kp = ks.kp; w.qs = ks.qs; w.qp = ks.qp;
+        }
+        a = AbsWalkArgs{};
+        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v + (size_t)p0 * N * C; a.u = nullptr;
+        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
+        a.slab = w.slab; a.uslab = out_u ? w.uslab : nullptr; a.CR = slab_stride(C);
+        a.out_dot = nullptr; a.out_rank = nullptr;
+        a.sign = 1.f; a.P = np; a.D = D; a.C = C;
+    };
+    // per chunk: sort k and group q (or, keeping the sorts, sort q and find the query bounds); range passes and walk;
+    // reduce
+    auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w; AbsWalkArgs a;
+        view(p0, np, buf, w, a);
         const size_t p = (size_t)p0;
-        const Presorted ks = keep_sorts ? offset(*keep, p, D, N, M) : Presorted{};
-        return abs_fwd_chunk(q + p * D * M, k + p * D * N, v + p * N * C, out_w + p * M * C,
-                             out_u ? out_u + p * M : nullptr, np, D, N, M, C, keep_sorts ? &ks : nullptr, ws, st);
-    });
-    if (e) return e;
+        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s), "segmented sort of k"))
+            return e;
+        if (!keep_sorts) return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
+        if (int e = seg_sort(q + p * D * M, w.qs, w.qp, np * D, M, w.sort_scratch, s))
+            return hip_status(e, "segmented sort of q");
+        return hip_status(range_bounds(a, w.ra.qb, s), "query bounds");
+    };
+    auto main = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w; AbsWalkArgs a;
+        view(p0, np, buf, w, a);
+        if (int e = hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges")) return e;
+        return hip_status(abs_emit(a, mode, w.ra, s), "abs walk");
+    };
+    auto back = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w; AbsWalkArgs a;
+        view(p0, np, buf, w, a);
+        const size_t p = (size_t)p0;
+        return hip_status(reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, w.uq, out_w + p * M * C,
+                                       out_u ? out_u + p * M : nullptr, np, D, M, C, s), "abs reduce");
+    };
+    if (int e = run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back)) return e;
     if (keep_sorts) *kept = 1;
     return QLKA_OK;
 }
@@ -402,41 +482,13 @@ static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
 
 size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
-    return budget_bytes(P, [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); });
+    auto b1 = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
+    return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, N), b1), b1);
 }
 
 }  // extern "C"
 
 namespace {
-// One chunk of np p of the abs backward (pointers offset to its first p); pre: the forward's sorts of the chunk.
-int abs_bwd_chunk(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
-                  float* grad_k, float* grad_v, int np, int D, int N, int M, int C, const Presorted* pre, void* ws,
-                  hipStream_t st) {
-    const int S = np * D;
-    SortedWs w = carve(ws, abs_bwd_spec(np, D, N, M, C));
-    if (pre) { w.ks = pre->ks; w.kp = pre->kp; w.qs = pre->qs; w.qp = pre->qp; }   // sorted by the forward
-    else if (int e = sort_both(q, k, w, S, N, M, st)) return e;
-
-    // grad_q: stream = sorted k with rows v, queries = q, dotted with g_w (+ g_u * (2 rank - N))
-    AbsWalkArgs a{};
-    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr;
-    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g_w; a.uq = g_u;
-    a.out_dot = grad_q; a.sign = 1.f; a.P = np; a.D = D; a.C = C;
-    int e = abs_walk(a, g_u ? (ABS_DOT | ABS_DOTX1) : ABS_DOT, w.ra, st);
-    if (e) return hip_status(e, "grad_q walk");
-
-    // grad_k and grad_v: stream = sorted q with rows g_w (+ scalars g_u), queries = k
-    AbsWalkArgs b{};
-    b.ks = w.qs; b.kp = w.qp; b.Ns = M; b.w = g_w; b.u = g_u;
-    b.qs = w.ks; b.qp = w.kp; b.Mq = N; b.g = v; b.uq = nullptr;
-    b.slab = w.slab; b.uslab = nullptr; b.CR = slab_stride(C);
-    b.out_dot = grad_k; b.sign = 1.f; b.P = np; b.D = D; b.C = C;
-    e = abs_walk(b, g_u ? (ABS_ROW | ABS_DOT | ABS_DOTX2) : (ABS_ROW | ABS_DOT), w.ra, st);
-    if (e) return hip_status(e, "grad_k/grad_v walk");
-    e = reduce_slabs(w.slab, nullptr, nullptr, nullptr, grad_v, nullptr, np, D, N, C, st);
-    return hip_status(e, "grad_v reduce");
-}
-
 int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
                  float* grad_k, float* grad_v, int P, int D, int N, int M, int C, const Presorted* pre, void* ws,
                  size_t ws_bytes_given, void* stream) {
@@ -444,20 +496,55 @@ int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
         return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
-    auto bytes = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
-    const int pc = fit_chunk(P, ws_bytes_given, bytes);
-    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
+    auto b1 = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
+    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, N), b1);
+    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     hipStream_t st = (hipStream_t)stream;
     if (dense_sign(P, N, M))     // the walks' convention: a tie counts -1 in both gradients
         return hip_status(direct_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st),
                           "dense backward");
-    return for_chunks(P, pc, [&](int p0, int np) {
+    // the chunk's workspace view, with the forward's sorts of the chunk when given
+    auto view = [&](int p0, int np, void* buf) {
+        SortedWs w = carve(buf, abs_bwd_spec(np, D, N, M, C));
+        if (pre) {
+            const Presorted ps = offset(*pre, (size_t)p0, D, N, M);
+            w.ks = ps.ks; w.kp = ps.kp; w.qs = ps.qs; w.qp = ps.qp;
+        }
+        return w;
+    };
+    // per chunk: the sorts (unless the forward kept them); the grad_q walk and the grad_k / grad_v walk; the grad_v
+    // reduce
+    auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
+        if (pre) return QLKA_OK;
+        SortedWs w = view(p0, np, buf);
         const size_t p = (size_t)p0;
-        const Presorted ps = pre ? offset(*pre, p, D, N, M) : Presorted{};
-        return abs_bwd_chunk(q + p * D * M, k + p * D * N, v + p * N * C, g_w + p * M * C, g_u ? g_u + p * M : nullptr,
-                             grad_q + p * D * M, grad_k + p * D * N, grad_v + p * N * C, np, D, N, M, C,
-                             pre ? &ps : nullptr, ws, st);
-    });
+        return sort_both(q + p * D * M, k + p * D * N, w, np * D, N, M, s);
+    };
+    auto main = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w = view(p0, np, buf);
+        const size_t p = (size_t)p0;
+        // grad_q: stream = sorted k with rows v, queries = q, dotted with g_w (+ g_u * (2 rank - N))
+        AbsWalkArgs a{};
+        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v + p * N * C; a.u = nullptr;
+        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g_w + p * M * C; a.uq = g_u ? g_u + p * M : nullptr;
+        a.out_dot = grad_q + p * D * M; a.sign = 1.f; a.P = np; a.D = D; a.C = C;
+        if (int e = abs_walk(a, g_u ? (ABS_DOT | ABS_DOTX1) : ABS_DOT, w.ra, s)) return hip_status(e, "grad_q walk");
+        // grad_k and grad_v: stream = sorted q with rows g_w (+ scalars g_u), queries = k
+        AbsWalkArgs b{};
+        b.ks = w.qs; b.kp = w.qp; b.Ns = M; b.w = g_w + p * M * C; b.u = g_u ? g_u + p * M : nullptr;
+        b.qs = w.ks; b.qp = w.kp; b.Mq = N; b.g = v + p * N * C; b.uq = nullptr;
+        b.slab = w.slab; b.uslab = nullptr; b.CR = slab_stride(C);
+        b.out_dot = grad_k + p * D * N; b.sign = 1.f; b.P = np; b.D = D; b.C = C;
+        const int e = abs_walk(b, g_u ? (ABS_ROW | ABS_DOT | ABS_DOTX2) : (ABS_ROW | ABS_DOT), w.ra, s);
+        return hip_status(e, "grad_k/grad_v walk");
+    };
+    auto back = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w = view(p0, np, buf);
+        const int e = reduce_slabs(w.slab, nullptr, nullptr, nullptr, grad_v + (size_t)p0 * N * C, nullptr, np, D, N,
+                                   C, s);
+        return hip_status(e, "grad_v reduce");
+    };
+    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back);
 }
 }  // namespace
 
@@ -601,9 +688,14 @@ LayerWs carve_layer(int kind, void* ws, const WsSpec& s) {
 }
 }  // namespace
 
+// add_bump runs three walks and reduces over one slab per chunk, so its chunks run in order
+static bool layer_pipelined(int kind, int P, int D, int M) { return kind != LAYER_ADD_BUMP && pipelined(P, D, M); }
+
 size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || kind < 0 || kind > 2) return 0;
-    return budget_bytes(P, [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); });
+    auto b1 = [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); };
+    return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), layer_pipelined(kind, P, D, M), b1),
+                      b1);
 }
 
 // Both layer entry points: keep == null is the reference's composition over pre-masked k, v and n_pad; keep != null
@@ -702,14 +794,71 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
     if (kind < 0 || kind > 2) return fail(QLKA_EINVAL, "kind must be 0 (add_laplace), 1 (add_riesz) or 2 (add_bump)");
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !out) return fail(QLKA_EINVAL, "q, k, v and out must be non-null");
-    auto bytes = [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); };
-    const int pc = fit_chunk(P, ws_bytes_given, bytes);
-    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
-    return for_chunks(P, pc, [&](int p0, int np) {
+    auto b1 = [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); };
+    const Plan pl = plan_chunks(P, ws_bytes_given, layer_pipelined(kind, P, D, M), b1);
+    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
+    hipStream_t st = (hipStream_t)stream;
+    auto chunk_in = [&](int p0, const float*& qc, const float*& kc, const float*& vc, const float*& npc,
+                        const uint8_t*& keepc, float*& outc) {
         const size_t p = (size_t)p0;
-        return layer_chunk(kind, q + p * D * M, k + p * D * N, v + p * N * C, n_pad ? n_pad + p : nullptr,
-                           keep ? keep + p * N : nullptr, out + p * M * C, np, D, N, M, C, ws, (hipStream_t)stream);
-    });
+        qc = q + p * D * M; kc = k + p * D * N; vc = v + p * N * C;
+        npc = n_pad ? n_pad + p : nullptr; keepc = keep ? keep + p * N : nullptr; outc = out + p * M * C;
+    };
+    if (kind == LAYER_ADD_BUMP)      // three walks and reduces over one slab per chunk: chunks in order
+        return for_chunks(P, pl.pc, [&](int p0, int np) {
+            const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
+            chunk_in(p0, qc, kc, vc, npc, keepc, outc);
+            return layer_chunk(kind, qc, kc, vc, npc, keepc, outc, np, D, N, M, C, ws, st); });
+    // add_laplace / add_riesz, per chunk: (mask keys,) sort k, group q; range passes (+ riesz prefixes) and walk;
+    // reduce and epilogue
+    const bool masked = keep != nullptr;
+    auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
+        const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
+        chunk_in(p0, qc, kc, vc, npc, keepc, outc);
+        LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
+        // masked add_laplace: masked keys become FLT_MAX (terms exactly 0, sorted last) and the unmasked walk runs
+        const bool lap_masked = kind == LAYER_ADD_LAPLACE && masked;
+        if (lap_masked)
+            if (int e = hip_status(mask_keys(kc, keepc, L.kmask, np, D, N, s), "masked keys")) return e;
+        if (int e = hip_status(seg_sort(lap_masked ? L.kmask : kc, L.op.ks, L.op.kp, np * D, N, L.op.sort_scratch, s),
+                               "segmented sort of k"))
+            return e;
+        return group_q(qc, L.op, 0.f, np * D, N, M, C, s);
+    };
+    auto main = [&](int p0, int np, void* buf, hipStream_t s) {
+        const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
+        chunk_in(p0, qc, kc, vc, npc, keepc, outc);
+        LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
+        SortedWs& w = L.op;
+        if (kind == LAYER_ADD_LAPLACE) {
+            if (int e = hip_status(laplace_prepare(w.ks, w.kp, vc, np, D, N, C, w.ra, s), "laplace ranges")) return e;
+            return hip_status(laplace_emit(w.ks, w.kp, w.qs, w.qp, vc, w.slab, w.uslab, np, D, N, M, C, w.ra, s),
+                              "laplace walk");
+        }
+        AbsWalkArgs a{};
+        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = vc; a.u = nullptr; a.keep = keepc;
+        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
+        a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
+        a.out_dot = nullptr; a.out_rank = nullptr;
+        a.sign = 1.f; a.P = np; a.D = D; a.C = C; a.qshift = 0.f;
+        const int mode = ABS_ROW | ABS_ONES | (masked ? ABS_KEEP : 0);
+        if (int e = abs_prepare(a, mode, w.ra, s)) return hip_status(e, "abs ranges");
+        if (int e = riesz_prefix(kc, vc, keepc, L.pre, np, D, N, C, s)) return hip_status(e, "riesz prefixes");
+        return hip_status(abs_emit(a, mode, w.ra, s), "abs walk");
+    };
+    auto back = [&](int p0, int np, void* buf, hipStream_t s) {
+        const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
+        chunk_in(p0, qc, kc, vc, npc, keepc, outc);
+        LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
+        SortedWs& w = L.op;
+        if (reduce_folds_epilogue(M, C))
+            return layer_reduce_folded(kind, masked, qc, npc, L, outc, np, D, M, C, s);
+        if (int e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[0], L.u[0], np, D, M, C, s))
+            return hip_status(e, "layer reduce");
+        return hip_status(layer_epilogue(kind, masked, qc, npc, L.w[0], L.u[0], nullptr, nullptr, nullptr, nullptr,
+                                         L.pre, L.qt, outc, np, D, N, M, C, s), "layer epilogue");
+    };
+    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back);
 }
 
 int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad, float* out,

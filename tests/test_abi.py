@@ -44,10 +44,10 @@ def test_version_and_workspace_sizes(lib):
     small = lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4)
     big = lib.qlka_laplace_fwd_ws_bytes(12, 64, 16384, 16384, 64)
     assert 0 < small < big
-    # the row-emitting ops carry one contribution row per (p, d, query): the D-fold slab
-    assert big >= 12 * 64 * 16384 * 64 * 4
-    assert lib.qlka_abs_bwd_ws_bytes(12, 64, 16384, 16384, 64) >= 12 * 64 * 16384 * 64 * 4
-    assert lib.qlka_sgn_fwd_ws_bytes(12, 64, 16384, 16384, 64) < 12 * 64 * 16384 * 64 * 4
+    # the row-emitting ops carry one contribution row per (p, d, query) of a chunk: the D-fold slab
+    assert lib.qlka_laplace_fwd_ws_bytes(1, 64, 16384, 16384, 64) >= 64 * 16384 * 64 * 4
+    assert lib.qlka_abs_bwd_ws_bytes(1, 64, 16384, 16384, 64) >= 64 * 16384 * 64 * 4
+    assert lib.qlka_sgn_fwd_ws_bytes(1, 64, 16384, 16384, 64) < 64 * 16384 * 64 * 4
     # the global (multi-run) sort needs scratch, the LDS sort none
     assert lib.qlka_seg_sort_ws_bytes(4, 16384) == 0
     assert lib.qlka_seg_sort_ws_bytes(4, 16385) > 0
@@ -55,17 +55,20 @@ def test_version_and_workspace_sizes(lib):
 
 
 def test_workspace_budget_sizes_the_queries(lib):
-    """The budget picks the largest chunk of p whose workspace fits it (one p at least); no GPU is touched."""
+    """The budget picks the chunking of a call; no GPU is touched. At the headline shape a call is pipelined: three
+    chunks of four p with two workspace copies; below that budget, smaller chunks with two copies, and one p with one
+    copy when two do not fit."""
     prev = lib.qlka_set_workspace_budget(8 << 30)
     try:
         dims = (12, 64, 16384, 16384, 64)
+        one = lib.qlka_laplace_fwd_ws_bytes(1, *dims[1:])       # one p: not pipelined, one copy
         full = lib.qlka_laplace_fwd_ws_bytes(*dims)
-        one = lib.qlka_laplace_fwd_ws_bytes(1, *dims[1:])
+        assert abs(full - 2 * 4 * one) < 64 << 10                 # two copies of a 4-p chunk (alignment slack)
         assert lib.qlka_set_workspace_budget(1) == 8 << 30
         assert lib.qlka_laplace_fwd_ws_bytes(*dims) == one
         assert lib.qlka_abs_bwd_ws_bytes(*dims) == lib.qlka_abs_bwd_ws_bytes(1, *dims[1:])
         lib.qlka_set_workspace_budget(3 * one + 10)
-        assert lib.qlka_laplace_fwd_ws_bytes(*dims) == lib.qlka_laplace_fwd_ws_bytes(3, *dims[1:])
+        assert lib.qlka_laplace_fwd_ws_bytes(*dims) == 2 * one   # two copies of a 1-p chunk
         lib.qlka_set_workspace_budget(1 << 62)
         assert lib.qlka_laplace_fwd_ws_bytes(*dims) == full
     finally:
@@ -102,10 +105,10 @@ def test_path_and_workspace_errors(lib):
 
 
 def test_layer_workspace_and_validation(lib):
-    dims = (12, 64, 16384, 16384, 64)
+    dims = (1, 64, 16384, 16384, 64)                          # one p: one chunk, one copy
     op = lib.qlka_abs_fwd_ws_bytes(*dims)
     lap, riesz, bump = (lib.qlka_layer_fwd_ws_bytes(kind, *dims) for kind in (0, 1, 2))
-    one_eval = 12 * 16384 * 64 * 4 + 12 * 16384 * 4          # out_w + out_u of one op evaluation
+    one_eval = 16384 * 64 * 4 + 16384 * 4                      # out_w + out_u of one op evaluation
     assert lap >= lib.qlka_laplace_fwd_ws_bytes(*dims) + one_eval
     assert riesz >= op + one_eval
     assert bump >= op + 3 * one_eval                          # three shifted evaluations, one shared slab
