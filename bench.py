@@ -358,7 +358,7 @@ def main():
 
     # Roofline of the step: B_scan of both op calls / step time. The op is the unit the north-star target is set on;
     # its measured HBM traffic (sum over its kernels of FETCH_SIZE + WRITE_SIZE, copy-calibrated) is `traffic`.
-    # `kernel` is the dominant (longest) launch on its own algorithmic bytes.
+    # `kernel` is the kernel with the most GPU time in the step, on its own algorithmic bytes per launch.
     achieved = 2 * bscan / (ms_per_step / 1e3) / 1e9
     dom = max(stages, key=lambda s_: stages[s_]["ms_total"])
     # the ops run their kernels once per chunk of p: a launch does (op-call bytes) / (launches per op call)
