@@ -348,13 +348,16 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
         SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
         const float* vp = v + (size_t)p0 * N * C;
         if (int e = hip_status(laplace_prepare(w.ks, w.kp, vp, np, D, N, C, w.ra, s), "laplace ranges")) return e;
-        return hip_status(laplace_emit(w.ks, w.kp, w.qs, w.qp, vp, w.slab, w.uslab, np, D, N, M, C, w.ra, s),
-                          "laplace walk");
+        if (int e = laplace_emit(w.ks, w.kp, w.qs, w.qp, vp, w.slab, w.uslab, np, D, N, M, C, w.ra, s))
+            return hip_status(e, "laplace walk");
+        order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
+        return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
     };
     auto back = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
         const size_t p = (size_t)p0;
-        return hip_status(reduce_slabs(w.slab, w.uslab, w.qp, w.uq, out_w + p * M * C, out_u + p * M, np, D, M, C, s),
+        const float* uq = u_query_order(M) ? w.uslab : w.uq;
+        return hip_status(reduce_slabs(w.slab, uq, nullptr, nullptr, out_w + p * M * C, out_u + p * M, np, D, M, C, s),
                           "laplace reduce");
     };
     return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back);
@@ -444,13 +447,16 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         SortedWs w; AbsWalkArgs a;
         view(p0, np, buf, w, a);
         if (int e = hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges")) return e;
-        return hip_status(abs_emit(a, mode, w.ra, s), "abs walk");
+        if (int e = hip_status(abs_emit(a, mode, w.ra, s), "abs walk")) return e;
+        if (out_u) order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
+        return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
     };
     auto back = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w; AbsWalkArgs a;
         view(p0, np, buf, w, a);
         const size_t p = (size_t)p0;
-        return hip_status(reduce_slabs(w.slab, out_u ? w.uslab : nullptr, w.qp, w.uq, out_w + p * M * C,
+        const float* uq = out_u ? (u_query_order(M) ? w.uslab : w.uq) : nullptr;
+        return hip_status(reduce_slabs(w.slab, uq, nullptr, nullptr, out_w + p * M * C,
                                        out_u ? out_u + p * M : nullptr, np, D, M, C, s), "abs reduce");
     };
     if (int e = run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back)) return e;
@@ -832,8 +838,10 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         SortedWs& w = L.op;
         if (kind == LAYER_ADD_LAPLACE) {
             if (int e = hip_status(laplace_prepare(w.ks, w.kp, vc, np, D, N, C, w.ra, s), "laplace ranges")) return e;
-            return hip_status(laplace_emit(w.ks, w.kp, w.qs, w.qp, vc, w.slab, w.uslab, np, D, N, M, C, w.ra, s),
-                              "laplace walk");
+            if (int e = laplace_emit(w.ks, w.kp, w.qs, w.qp, vc, w.slab, w.uslab, np, D, N, M, C, w.ra, s))
+                return hip_status(e, "laplace walk");
+            order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
+            return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
         }
         AbsWalkArgs a{};
         a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = vc; a.u = nullptr; a.keep = keepc;
@@ -844,16 +852,20 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         const int mode = ABS_ROW | ABS_ONES | (masked ? ABS_KEEP : 0);
         if (int e = abs_prepare(a, mode, w.ra, s)) return hip_status(e, "abs ranges");
         if (int e = riesz_prefix(kc, vc, keepc, L.pre, np, D, N, C, s)) return hip_status(e, "riesz prefixes");
-        return hip_status(abs_emit(a, mode, w.ra, s), "abs walk");
+        if (int e = hip_status(abs_emit(a, mode, w.ra, s), "abs walk")) return e;
+        order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
+        return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
     };
     auto back = [&](int p0, int np, void* buf, hipStream_t s) {
         const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
         chunk_in(p0, qc, kc, vc, npc, keepc, outc);
         LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
         SortedWs& w = L.op;
+        w.uslab = u_query_order(M) ? w.uslab : w.uq;       // query order (main put the terms there)
+        w.qp = nullptr;
         if (reduce_folds_epilogue(M, C))
             return layer_reduce_folded(kind, masked, qc, npc, L, outc, np, D, M, C, s);
-        if (int e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[0], L.u[0], np, D, M, C, s))
+        if (int e = reduce_slabs(w.slab, w.uslab, nullptr, nullptr, L.w[0], L.u[0], np, D, M, C, s))
             return hip_status(e, "layer reduce");
         return hip_status(layer_epilogue(kind, masked, qc, npc, L.w[0], L.u[0], nullptr, nullptr, nullptr, nullptr,
                                          L.pre, L.qt, outc, np, D, N, M, C, s), "layer epilogue");

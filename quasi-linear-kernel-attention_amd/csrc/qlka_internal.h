@@ -106,9 +106,13 @@ __host__ __device__ inline bool u_query_order(int M) { return M > U_LDS_CAP; }
 
 // D-reduction of the slabs: out[p,m,c] = sum_d slab rows of (p, d, m); out_u[p,m] = sum_d of the v == 1 terms of
 // (p, d, m). uslab as the walks write it (see u_query_order); for sorted order it is put in query order in uq (P*D*M
-// floats of scratch) by the sort's permutation qperm first. out_u / uslab / qperm / uq may be null (no out_u).
+// floats of scratch) by the sort's permutation qperm first; qperm == null: uslab is already in query order (from
+// order_u_terms). out_u / uslab / qperm / uq may be null (no out_u).
 int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, float* uq, float* out, float* out_u,
                  int P, int D, int M, int C, hipStream_t st);
+// The v == 1 terms in query order: uslab itself when the walks wrote them so, else uq after the transpose through
+// LDS by the permutation qperm (launched on st).
+const float* order_u_terms(const float* uslab, const uint32_t* qperm, float* uq, int P, int D, int M, hipStream_t st);
 
 // Emission modes of the abs-family walk (bit set).
 enum AbsMode : int {

@@ -138,7 +138,7 @@ int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, f
     const bool v4 = (C % 4) == 0;
     const int cq = C / 4;
     const bool fused_u = out_u && v4 && (cq & (cq - 1)) == 0;     // row lanes aligned within a wave
-    if (out_u && !u_query_order(M)) {
+    if (out_u && qperm && !u_query_order(M)) {
         StageTimer t("u_to_query", st);
         hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
     } else if (out_u) {
@@ -168,6 +168,13 @@ int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, f
 
 namespace qlka {
 
+const float* order_u_terms(const float* uslab, const uint32_t* qperm, float* uq, int P, int D, int M, hipStream_t st) {
+    if (u_query_order(M)) return uslab;
+    StageTimer t("u_to_query", st);
+    hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
+    return uq;
+}
+
 bool reduce_folds_epilogue(int M, int C) {
     const int cq = C / 4;
     return C % 4 == 0 && (cq & (cq - 1)) == 0;
@@ -178,11 +185,11 @@ int reduce_slabs_layer(int kind, bool masked, const ReduceEpilogue& ep, const fl
     if (!reduce_folds_epilogue(M, C) || (kind != LAYER_ADD_LAPLACE && kind != LAYER_ADD_RIESZ))
         return (int)hipErrorInvalidValue;
     const int CR = slab_stride(C);
-    if (!u_query_order(M)) {
+    if (qperm && !u_query_order(M)) {
         StageTimer t("u_to_query", st);
         hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
     } else {
-        uq = const_cast<float*>(uslab);
+        uq = const_cast<float*>(uslab);                   // already in query order
     }
     const long threads = (long)P * M * (C / 4);
     const unsigned blocks = (unsigned)((threads + RT - 1) / RT);

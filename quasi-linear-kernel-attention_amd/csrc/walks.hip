@@ -226,7 +226,7 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 // the piece again from the true incoming state, writing every range's entry (exit) state. Slot C+1 of every summary
 // row holds the range's link to its neighbour (a decay factor or a key gap, written by the sums kernel), so the scan
 // loop is loads and FMAs only.
-constexpr int SCAN_W = 8;
+constexpr int SCAN_W = 16;
 constexpr int SCAN_BATCH = 8;      // rows loaded ahead in a piece
 
 template <int NV>
