@@ -637,8 +637,10 @@ int qlka_direct_sgn(float tie, const float* q, const float* k, const float* v, c
 }
 
 // ------------------------------------------------------------------------------------------- fused attention layers
-// Workspace: the op's (sorted k/q, ranges, slab) + per op evaluation a (P, M, C) + (P, M) pair of out_w / out_u
-// (three for add_bump) + the add_riesz prefixes + the query boundaries of add_bump's two shifted query sets.
+// Workspace: the op's (sorted k/q, ranges, slab) + per-query terms + the add_riesz prefixes + the masked keys of
+// add_laplace. add_bump, with the epilogue folded into its reduce: the query bounds of its two shifted query sets and
+// a second and third slab (+ v == 1 terms) for them; otherwise an out_w / out_u pair per evaluation (the op's slab
+// serves the three evaluations in turn). add_laplace / add_riesz fold their epilogue into the reduce or use one pair.
 namespace {
 struct LayerWs {
     SortedWs op;
@@ -646,11 +648,14 @@ struct LayerWs {
     void* pre; int* qb[2];
     float* qt;
     float* kmask;
+    float* slab2[2]; float* uslab2[2]; float* uq2[2];   // add_bump's q + 1 and q - 1 rows (folded epilogue)
 };
+
+bool bump_folded(int kind, const WsSpec& s) { return kind == LAYER_ADD_BUMP && reduce_folds_epilogue(s.M, s.C); }
 
 size_t layer_part(int kind, const WsSpec& s, int i) {
     const size_t PMC = (size_t)s.P * s.M * s.C, PM = (size_t)s.P * s.M;
-    const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
+    const int nev = bump_folded(kind, s) ? 0 : (kind == LAYER_ADD_BUMP) ? 3 : 1;
     switch (i) {
         case 0: return ws_bytes(s);
         case 1: return nev * (align256(PMC * 4) + align256(PM * 4)) + align256(PM * 4);   // + per-query terms
@@ -658,49 +663,59 @@ size_t layer_part(int kind, const WsSpec& s, int i) {
         case 3: return kind == LAYER_ADD_BUMP
                        ? 2 * align256((size_t)s.P * s.D * range_count(s.N, s.C) * sizeof(int)) : 0;
         case 4: return kind == LAYER_ADD_LAPLACE ? align256((size_t)s.P * s.D * s.N * 4) : 0;   // masked keys
+        case 5: return bump_folded(kind, s) ? 2 * (ws_part(s, 6) + ws_part(s, 7) + ws_part(s, 8)) : 0;
     }
     return 0;
 }
 
 size_t layer_ws_bytes(int kind, const WsSpec& s) {
     size_t b = 0;
-    for (int i = 0; i < 5; ++i) b += layer_part(kind, s, i);
+    for (int i = 0; i < 6; ++i) b += layer_part(kind, s, i);
     return b;
 }
 
 LayerWs carve_layer(int kind, void* ws, const WsSpec& s) {
     LayerWs r{};
+    char* part[6];
     char* b = (char*)ws;
-    r.op = carve(b, s);
-    b += layer_part(kind, s, 0);
+    for (int i = 0; i < 6; ++i) { part[i] = b; b += layer_part(kind, s, i); }
+    r.op = carve(part[0], s);
     const size_t PMC = (size_t)s.P * s.M * s.C, PM = (size_t)s.P * s.M;
-    const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
+    const int nev = bump_folded(kind, s) ? 0 : (kind == LAYER_ADD_BUMP) ? 3 : 1;
+    b = part[1];
     for (int e = 0; e < nev; ++e) {
         r.w[e] = (float*)b; b += align256(PMC * 4);
         r.u[e] = (float*)b; b += align256(PM * 4);
     }
-    r.qt = (float*)b; b += align256(PM * 4);
-    r.pre = layer_part(kind, s, 2) ? (void*)b : nullptr;
-    b += layer_part(kind, s, 2);
+    r.qt = (float*)b;
+    r.pre = layer_part(kind, s, 2) ? (void*)part[2] : nullptr;
     if (kind == LAYER_ADD_BUMP) {
         const size_t qbb = align256((size_t)s.P * s.D * range_count(s.N, s.C) * sizeof(int));
-        r.qb[0] = (int*)b; b += qbb;
-        r.qb[1] = (int*)b;
+        r.qb[0] = (int*)part[3];
+        r.qb[1] = (int*)(part[3] + qbb);
     }
-    char* p4 = (char*)ws;
-    for (int i = 0; i < 4; ++i) p4 += layer_part(kind, s, i);
-    r.kmask = layer_part(kind, s, 4) ? (float*)p4 : nullptr;
+    r.kmask = layer_part(kind, s, 4) ? (float*)part[4] : nullptr;
+    if (bump_folded(kind, s)) {
+        b = part[5];
+        for (int e = 0; e < 2; ++e) {
+            r.slab2[e] = (float*)b;  b += ws_part(s, 6);
+            r.uslab2[e] = (float*)b; b += ws_part(s, 7);
+            r.uq2[e] = (float*)b;    b += ws_part(s, 8);
+        }
+    }
     return r;
 }
 }  // namespace
 
-// add_bump runs three walks and reduces over one slab per chunk, so its chunks run in order
-static bool layer_pipelined(int kind, int P, int D, int M) { return kind != LAYER_ADD_BUMP && pipelined(P, D, M); }
+// add_bump without a foldable epilogue runs three walks and reduces over one slab per chunk: its chunks run in order
+static bool layer_pipelined(int kind, int P, int D, int M, int C) {
+    return (kind != LAYER_ADD_BUMP || reduce_folds_epilogue(M, C)) && pipelined(P, D, M);
+}
 
 size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || kind < 0 || kind > 2) return 0;
     auto b1 = [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); };
-    return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), layer_pipelined(kind, P, D, M), b1),
+    return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), layer_pipelined(kind, P, D, M, C), b1),
                       b1);
 }
 
@@ -801,7 +816,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !out) return fail(QLKA_EINVAL, "q, k, v and out must be non-null");
     auto b1 = [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); };
-    const Plan pl = plan_chunks(P, ws_bytes_given, layer_pipelined(kind, P, D, M), b1);
+    const Plan pl = plan_chunks(P, ws_bytes_given, layer_pipelined(kind, P, D, M, C), b1);
     if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     hipStream_t st = (hipStream_t)stream;
     auto chunk_in = [&](int p0, const float*& qc, const float*& kc, const float*& vc, const float*& npc,
@@ -810,18 +825,34 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         qc = q + p * D * M; kc = k + p * D * N; vc = v + p * N * C;
         npc = n_pad ? n_pad + p : nullptr; keepc = keep ? keep + p * N : nullptr; outc = out + p * M * C;
     };
-    if (kind == LAYER_ADD_BUMP)      // three walks and reduces over one slab per chunk: chunks in order
+    const bool bump = kind == LAYER_ADD_BUMP;
+    if (bump && !reduce_folds_epilogue(M, C))   // three walks and reduces over one slab per chunk: chunks in order
         return for_chunks(P, pl.pc, [&](int p0, int np) {
             const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
             chunk_in(p0, qc, kc, vc, npc, keepc, outc);
             return layer_chunk(kind, qc, kc, vc, npc, keepc, outc, np, D, N, M, C, ws, st); });
-    // add_laplace / add_riesz, per chunk: (mask keys,) sort k, group q; range passes (+ riesz prefixes) and walk;
-    // reduce and epilogue
+    // Per chunk: (mask keys,) sort k, group q (add_bump: sort q and find the range bounds of q, q + 1, q - 1); range
+    // passes (+ riesz prefixes) and the walk (add_bump: one walk over the three query sets into three slabs); the
+    // reduce with the epilogue. fp32 addition of a constant is monotone, so q + 1 and q - 1 keep the sorted order of q,
+    // and every walk sees exactly the fp32 values q + 1 and q - 1 the reference passes.
     const bool masked = keep != nullptr;
+    const float shift[3] = {0.f, 1.f, -1.f};
     auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
         const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
         chunk_in(p0, qc, kc, vc, npc, keepc, outc);
         LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
+        if (bump) {
+            SortedWs& w = L.op;
+            if (int e = hip_status(seg_sort(kc, w.ks, w.kp, np * D, N, w.sort_scratch, s), "segmented sort of k"))
+                return e;
+            if (int e = hip_status(seg_sort(qc, w.qs, w.qp, np * D, M, w.sort_scratch, s), "segmented sort of q"))
+                return e;
+            int* qbs[3] = {w.ra.qb, L.qb[0], L.qb[1]};
+            for (int ev = 0; ev < 3; ++ev)
+                if (int e = query_bounds(w.ks, w.qs, qbs[ev], shift[ev], np * D, N, M, C, s))
+                    return hip_status(e, "query bounds");
+            return QLKA_OK;
+        }
         // masked add_laplace: masked keys become FLT_MAX (terms exactly 0, sorted last) and the unmasked walk runs
         const bool lap_masked = kind == LAYER_ADD_LAPLACE && masked;
         if (lap_masked)
@@ -851,9 +882,21 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         a.sign = 1.f; a.P = np; a.D = D; a.C = C; a.qshift = 0.f;
         const int mode = ABS_ROW | ABS_ONES | (masked ? ABS_KEEP : 0);
         if (int e = abs_prepare(a, mode, w.ra, s)) return hip_status(e, "abs ranges");
-        if (int e = riesz_prefix(kc, vc, keepc, L.pre, np, D, N, C, s)) return hip_status(e, "riesz prefixes");
+        if (!bump)
+            if (int e = riesz_prefix(kc, vc, keepc, L.pre, np, D, N, C, s)) return hip_status(e, "riesz prefixes");
+        if (bump) {
+            a.nsets = 3;
+            for (int ev = 1; ev < 3; ++ev) {
+                a.set_shift[ev] = shift[ev];
+                a.set_qb[ev] = L.qb[ev - 1];
+                a.set_slab[ev] = L.slab2[ev - 1];
+                a.set_uslab[ev] = L.uslab2[ev - 1];
+            }
+        }
         if (int e = hip_status(abs_emit(a, mode, w.ra, s), "abs walk")) return e;
         order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
+        if (bump)
+            for (int ev = 0; ev < 2; ++ev) order_u_terms(L.uslab2[ev], w.qp, L.uq2[ev], np, D, M, s);
         return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
     };
     auto back = [&](int p0, int np, void* buf, hipStream_t s) {
@@ -863,6 +906,15 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         SortedWs& w = L.op;
         w.uslab = u_query_order(M) ? w.uslab : w.uq;       // query order (main put the terms there)
         w.qp = nullptr;
+        if (bump) {
+            ReduceEpilogue ep{};
+            if (int e = layer_epilogue_params(kind, masked, qc, npc, L.pre, L.qt, outc, np, D, M, C, &ep, s))
+                return hip_status(e, "layer query terms");
+            const float* slabs[3] = {w.slab, L.slab2[0], L.slab2[1]};
+            const float* uqs[3] = {w.uslab, u_query_order(M) ? L.uslab2[0] : L.uq2[0],
+                                   u_query_order(M) ? L.uslab2[1] : L.uq2[1]};
+            return hip_status(reduce_slabs_bump(masked, ep, slabs, uqs, np, D, M, C, s), "layer reduce");
+        }
         if (reduce_folds_epilogue(M, C))
             return layer_reduce_folded(kind, masked, qc, npc, L, outc, np, D, M, C, s);
         if (int e = reduce_slabs(w.slab, w.uslab, nullptr, nullptr, L.w[0], L.u[0], np, D, M, C, s))

@@ -251,6 +251,8 @@ int layer_epilogue_params(int kind, bool masked, const float* q, const float* n_
         hipLaunchKernelGGL(layer_query_terms<LAYER_ADD_LAPLACE>, dim3(qblocks), dim3(RZ_T), 0, st, q, qt, P, D, M);
     else if (kind == LAYER_ADD_RIESZ)
         hipLaunchKernelGGL(layer_query_terms<LAYER_ADD_RIESZ>, dim3(qblocks), dim3(RZ_T), 0, st, q, qt, P, D, M);
+    else if (kind == LAYER_ADD_BUMP)
+        hipLaunchKernelGGL(layer_query_terms<LAYER_ADD_BUMP>, dim3(qblocks), dim3(RZ_T), 0, st, q, qt, P, D, M);
     else
         return (int)hipErrorInvalidValue;
     return (int)hipGetLastError();

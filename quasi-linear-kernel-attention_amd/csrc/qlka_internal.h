@@ -143,6 +143,14 @@ struct AbsWalkArgs {
     float sign;
     int P, D, C;
     float qshift;            // added to every query value (0: the queries as given); the sorted order is unchanged
+    // More query sets over the same sorted queries (nsets = 3, ROW | ONES walks only): set i > 0 adds set_shift[i]
+    // to the queries, has its own range bounds set_qb[i] (query_bounds for that shift) and writes set_slab[i] /
+    // set_uslab[i]. Set 0 is qshift / the walk's qb / slab / uslab. nsets = 0 or 1: one set.
+    int nsets;
+    float set_shift[3];
+    const int* set_qb[3];
+    float* set_slab[3];
+    float* set_uslab[3];
 };
 // query boundaries + sums + scan + walk
 int abs_walk(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st);
@@ -202,6 +210,10 @@ int layer_epilogue_params(int kind, bool masked, const float* q, const float* n_
                           float* out, int P, int D, int M, int C, ReduceEpilogue* ep, hipStream_t st);
 int reduce_slabs_layer(int kind, bool masked, const ReduceEpilogue& ep, const float* slab, const float* uslab,
                        const uint32_t* qperm, float* uq, int P, int D, int M, int C, hipStream_t st);
+// add_bump in one reduce: the slabs and query-order v == 1 terms of the abs sums at q, q + 1, q - 1 (indices 0, 1, 2),
+// with the bump epilogue folded in (writes ep.out); requires reduce_folds_epilogue(M, C)
+int reduce_slabs_bump(bool masked, const ReduceEpilogue& ep, const float* const slab[3], const float* const uq[3],
+                      int P, int D, int M, int C, hipStream_t st);
 
 // ---- capi.hip helpers for noalloc.hip
 // check_dims of the C ABI (clears the thread's error first); the workspace of a Laplace forward over pc p at a time;

@@ -168,6 +168,79 @@ int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, f
 
 namespace qlka {
 
+// add_bump in one pass: the three slabs of the abs sums at q, q + 1 and q - 1 (one walk over the three query sets) and
+// their v == 1 terms (query order), each summed over d = 0..D-1 exactly as slab_reduce<true, true> sums one, then the
+// bump epilogue of layer_epilogue_kernel on the three sums: num = (w+ + w-) / 2 - w0, den = (u+ + u-) / 2 - u0
+// (- n_pad * sum_d max(0, 1 - |q_d|) unmasked), out = num / max(den, clamp). One thread per (p, m, 4 channels);
+// C / 4 a power of two.
+template <bool MASKED>
+__global__ __launch_bounds__(RT)
+void slab_reduce_bump(const float* __restrict__ s0, const float* __restrict__ sp, const float* __restrict__ sm,
+                      const float* __restrict__ u0q, const float* __restrict__ upq, const float* __restrict__ umq,
+                      const ReduceEpilogue ep, const int P, const int D, const int M, const int C, const int CR)
+{
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int CQ = C / 4;
+    const long i = (long)blockIdx.x * RT + threadIdx.x;
+    if (i >= (long)P * M * CQ) return;                 // P*M*CQ is a multiple of CQ: whole rows return
+    const int c = (int)(i % CQ);
+    const long pm = i / CQ;
+    const int p = (int)(pm / M);
+    const int m = (int)(pm - (long)p * M);
+    const int G = slab_group(D);
+    const size_t gstride = (size_t)G * slab_rows(M) * CR;
+    const size_t fstride = (size_t)SLAB_QB * CR;
+    const size_t off = (size_t)p * D * slab_rows(M) * CR + (size_t)slab_row_off(m, G, CR) / 4;
+    f4 a0 = {0.f, 0.f, 0.f, 0.f}, ap = a0, am = a0;
+    for (int g0 = 0; g0 < D; g0 += G) {
+        const size_t go = off + (size_t)(g0 / G) * gstride;
+        const f4* r0 = reinterpret_cast<const f4*>(s0 + go) + c;
+        const f4* rp = reinterpret_cast<const f4*>(sp + go) + c;
+        const f4* rm = reinterpret_cast<const f4*>(sm + go) + c;
+#pragma unroll 4
+        for (int dd = 0; dd < G; ++dd) {
+            const size_t o = (size_t)dd * (fstride / 4);
+            a0 += __builtin_nontemporal_load(r0 + o);
+            ap += __builtin_nontemporal_load(rp + o);
+            am += __builtin_nontemporal_load(rm + o);
+        }
+    }
+    const size_t ub = (size_t)p * D * M + m;
+    float u0 = 0.f, up = 0.f, um = 0.f;
+    for (int d = c; d < D; d += CQ) {
+        u0 += u0q[ub + (size_t)d * M];
+        up += upq[ub + (size_t)d * M];
+        um += umq[ub + (size_t)d * M];
+    }
+    for (int o = CQ >> 1; o >= 1; o >>= 1) {
+        u0 += __shfl_xor(u0, o, WAVE);
+        up += __shfl_xor(up, o, WAVE);
+        um += __shfl_xor(um, o, WAVE);
+    }
+    const float np = ep.n_pad ? ep.n_pad[p] : 0.f;
+    const float den = MASKED ? (up + um) / 2.f - u0 : (up + um) / 2.f - u0 - np * ep.qt[pm];
+    f4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = ((ap[e] + am[e]) / 2.f - a0[e]) / fmaxf(den, LAYER_CLAMP);
+    reinterpret_cast<f4*>(ep.out + pm * C)[c] = o;
+}
+
+int reduce_slabs_bump(bool masked, const ReduceEpilogue& ep, const float* const slab[3], const float* const uq[3],
+                      int P, int D, int M, int C, hipStream_t st) {
+    if (!reduce_folds_epilogue(M, C)) return (int)hipErrorInvalidValue;
+    const int CR = slab_stride(C);
+    const long threads = (long)P * M * (C / 4);
+    const unsigned blocks = (unsigned)((threads + RT - 1) / RT);
+    StageTimer t("slab_reduce", st);
+    if (masked)
+        hipLaunchKernelGGL(slab_reduce_bump<true>, dim3(blocks), dim3(RT), 0, st, slab[0], slab[1], slab[2], uq[0],
+                           uq[1], uq[2], ep, P, D, M, C, CR);
+    else
+        hipLaunchKernelGGL(slab_reduce_bump<false>, dim3(blocks), dim3(RT), 0, st, slab[0], slab[1], slab[2], uq[0],
+                           uq[1], uq[2], ep, P, D, M, C, CR);
+    return (int)hipGetLastError();
+}
+
 const float* order_u_terms(const float* uslab, const uint32_t* qperm, float* uq, int P, int D, int M, hipStream_t st) {
     if (u_query_order(M)) return uslab;
     StageTimer t("u_to_query", st);

@@ -1072,11 +1072,15 @@ void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
     }
 }
 
-template <int NV, int RK, int MODE>
+// NS = 1: the queries a.qs (+ a.qshift) with bounds qb, rows to a.slab / a.uslab. NS = 3 (ROW | ONES only): also the
+// query sets 1 and 2 of a.set_* (add_bump's q + 1 and q - 1: the same sorted order, their own bounds and slabs), each
+// walked over the same gathered rows and key-side states as set 0.
+template <int NV, int RK, int MODE, int NS>
 __global__ __launch_bounds__(WPB * WAVE)
 void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __restrict__ tb,
                     const int* __restrict__ qb, const int G)
 {
+    static_assert(NS == 1 || (NS == 3 && (MODE & ~ABS_KEEP) == (ABS_ROW | ABS_ONES)), "query sets: row walks only");
     constexpr bool ROW = MODE & ABS_ROW, ONES = MODE & ABS_ONES, DOT = MODE & ABS_DOT;
     constexpr bool X1 = MODE & ABS_DOTX1, X2 = MODE & ABS_DOTX2, RANK = MODE & ABS_RANK, KEEP = MODE & ABS_KEEP;
     constexpr bool EMIT = ROW || DOT;                     // rows gathered, states staged in LDS, emission
@@ -1202,24 +1206,35 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     if constexpr (X2) uli = wave_prefix_sum(ul);
 
     const int SG = slab_group(a.D);
-    const rsrc_t sr_ = ROW ? make_rsrc(a.slab + slab_seg_base(p, s - p * a.D, a.D, Mq, a.CR),
-                                       slab_seg_bytes(s - p * a.D, a.D, Mq, a.CR))
-                           : make_rsrc(nullptr, 0);
     const rsrc_t gr_ = DOT ? make_rsrc(a.g + (size_t)p * Mq * C, (uint32_t)((size_t)Mq * C * 4))
                            : make_rsrc(nullptr, 0);
-    float* useg = ONES ? a.uslab + (size_t)s * Mq : nullptr;        // v == 1 terms, order: u_query_order
+#pragma unroll 1
+    for (int set = 0; set < NS; ++set) {
+    int sq0 = q0, sq1 = q1;                               // the set's owned queries
+    if (set > 0) {
+        const int* sqb = a.set_qb[set];
+        sq0 = has_prev ? sqb[(size_t)s * G + g - 1] : 0;
+        sq1 = has_next ? sqb[(size_t)s * G + g] : Mq;
+    }
+    const float qshift = set == 0 ? a.qshift : a.set_shift[set];
+    float* const slab_s = set == 0 ? a.slab : a.set_slab[set];
+    const rsrc_t sr_ = ROW ? make_rsrc(slab_s + slab_seg_base(p, s - p * a.D, a.D, Mq, a.CR),
+                                       slab_seg_bytes(s - p * a.D, a.D, Mq, a.CR))
+                           : make_rsrc(nullptr, 0);
+    float* useg = ONES ? (set == 0 ? a.uslab : a.set_uslab[set]) + (size_t)s * Mq
+                       : nullptr;                         // v == 1 terms, order: u_query_order
 
     // Owned queries in blocks of 64. Lane i takes query i: its rank t inside the range, its distances and its scalar
     // outputs (v == 1 sum, rank, dot extras) from the lane-parallel prefixes; its record (row offset of rank t in the
     // chunk buffers, query index, 2 (q - k_prev), q - k_max) goes to LDS. Then the keys are walked in 4 chunks of CH:
     // the chunk's states PW and 2B - Btot before each key go to LDS and the queries ranked in the chunk are emitted,
     //   row:  2 (q - k_prev) PW + (2B - Btot) - (q - k_max) Wtot,     dot:  <g_q, 2 PW - Wtot> + extra.
-    for (int qb0 = q0; qb0 < q1; qb0 += WAVE) {
-        const int nq = min(WAVE, q1 - qb0);
+    for (int qb0 = sq0; qb0 < sq1; qb0 += WAVE) {
+        const int nq = min(WAVE, sq1 - qb0);
         const bool act = l < nq;
-        const int qi = min(qb0 + l, q1 - 1);              // clamped: unconditional loads
-        const bool first = PREF && qb0 == q0;
-        const float qv = (first ? qv0 : qseg[qi]) + a.qshift;
+        const int qi = min(qb0 + l, sq1 - 1);             // clamped: unconditional loads
+        const bool first = PREF && set == 0 && qb0 == sq0;
+        const float qv = (first ? qv0 : qseg[qi]) + qshift;
         const uint32_t mq = first ? mq0 : qpseg[qi];
         const int t = range_rank<RK>(kl, nk, qv);
         const float kpv = __shfl(kl, max(t - 1, 0), WAVE);
@@ -1338,14 +1353,15 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
             }
         }
     }
+    }   // set
 }
 
-template <int NV, int RK, int MODE>
+template <int NV, int RK, int MODE, int NS = 1>
 static void launch_abs_walk(const AbsWalkArgs& a, RangeArrays ra, int G, hipStream_t st) {
     const long waves = (long)a.P * a.D * G;
     const unsigned blocks = (unsigned)((waves + WPB - 1) / WPB);
     StageTimer t("abs_range_walk", st);
-    hipLaunchKernelGGL((abs_range_walk<NV, RK, MODE>), dim3(blocks), dim3(WPB * WAVE), 0, st, a, ra.ta, ra.tb,
+    hipLaunchKernelGGL((abs_range_walk<NV, RK, MODE, NS>), dim3(blocks), dim3(WPB * WAVE), 0, st, a, ra.ta, ra.tb,
                        ra.qb, G);
 }
 
@@ -1379,6 +1395,16 @@ template <int NV, int RK>
 static int abs_emit_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
     const int G = (a.Ns + RK - 1) / RK;
     if (((mode & ABS_KEEP) != 0) != (a.keep != nullptr)) return (int)hipErrorInvalidValue;   // sums and walk agree
+    if (a.nsets == 3) {
+        switch (mode) {
+            case ABS_ROW | ABS_ONES:            launch_abs_walk<NV, RK, ABS_ROW | ABS_ONES, 3>(a, ra, G, st); break;
+            case ABS_ROW | ABS_ONES | ABS_KEEP: launch_abs_walk<NV, RK, ABS_ROW | ABS_ONES | ABS_KEEP, 3>(a, ra, G, st);
+                                                break;
+            default: return (int)hipErrorInvalidValue;
+        }
+        return (int)hipGetLastError();
+    }
+    if (a.nsets > 1) return (int)hipErrorInvalidValue;
     switch (mode) {
         case ABS_ROW:                         launch_abs_walk<NV, RK, ABS_ROW>(a, ra, G, st); break;
         case ABS_ROW | ABS_ONES:              launch_abs_walk<NV, RK, ABS_ROW | ABS_ONES>(a, ra, G, st); break;
