@@ -148,12 +148,15 @@ int for_chunks(int P, int pc, F f) {
     return QLKA_OK;
 }
 
+// k and q sorted; in one launch when N == M (a hipError_t value, 0 on success)
+int sort_pair(const float* q, const float* k, SortedWs& w, int S, int N, int M, hipStream_t st) {
+    if (N == M) return seg_sort2(k, w.ks, w.kp, q, w.qs, w.qp, S, N, w.sort_scratch, st);
+    if (int e = seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st)) return e;
+    return seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, st);
+}
+
 int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, hipStream_t st) {
-    int e = seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st);
-    if (e) return hip_status(e, "segmented sort of k");
-    e = seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, st);
-    if (e) return hip_status(e, "segmented sort of q");
-    return QLKA_OK;
+    return hip_status(sort_pair(q, k, w, S, N, M, st), "segmented sort of k and q");
 }
 
 // The query side of a forward walk that keeps no sorts: q grouped by key chunk, with the range bounds, in one pass
@@ -436,12 +439,14 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         SortedWs w; AbsWalkArgs a;
         view(p0, np, buf, w, a);
         const size_t p = (size_t)p0;
+        if (keep_sorts) {
+            if (int e = hip_status(sort_pair(q + p * D * M, k + p * D * N, w, np * D, N, M, s), "segmented sorts"))
+                return e;
+            return hip_status(range_bounds(a, w.ra.qb, s), "query bounds");
+        }
         if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s), "segmented sort of k"))
             return e;
-        if (!keep_sorts) return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
-        if (int e = seg_sort(q + p * D * M, w.qs, w.qp, np * D, M, w.sort_scratch, s))
-            return hip_status(e, "segmented sort of q");
-        return hip_status(range_bounds(a, w.ra.qb, s), "query bounds");
+        return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
     };
     auto main = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w; AbsWalkArgs a;
@@ -841,17 +846,11 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
         chunk_in(p0, qc, kc, vc, npc, keepc, outc);
         LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
-        if (bump) {
+        if (bump) {   // one launch per step, so that the prep's kernels start together beside a reduce
             SortedWs& w = L.op;
-            if (int e = hip_status(seg_sort(kc, w.ks, w.kp, np * D, N, w.sort_scratch, s), "segmented sort of k"))
-                return e;
-            if (int e = hip_status(seg_sort(qc, w.qs, w.qp, np * D, M, w.sort_scratch, s), "segmented sort of q"))
-                return e;
-            int* qbs[3] = {w.ra.qb, L.qb[0], L.qb[1]};
-            for (int ev = 0; ev < 3; ++ev)
-                if (int e = query_bounds(w.ks, w.qs, qbs[ev], shift[ev], np * D, N, M, C, s))
-                    return hip_status(e, "query bounds");
-            return QLKA_OK;
+            if (int e = hip_status(sort_pair(qc, kc, w, np * D, N, M, s), "segmented sort of k and q")) return e;
+            int* const qbs[3] = {w.ra.qb, L.qb[0], L.qb[1]};
+            return hip_status(query_bounds_sets(w.ks, w.qs, qbs, shift, 3, np * D, N, M, C, s), "query bounds");
         }
         // masked add_laplace: masked keys become FLT_MAX (terms exactly 0, sorted last) and the unmasked walk runs
         const bool lap_masked = kind == LAYER_ADD_LAPLACE && masked;

@@ -32,6 +32,10 @@ size_t seg_sort_scratch_bytes(int S, int L);
 // Stable ascending sort of S contiguous segments of length L. Returns a hipError_t value (0 on success).
 int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch,
              hipStream_t st);
+// seg_sort of two arrays of S segments of length L, in one launch when the segments fit one LDS sort (so that the
+// two sorts start together when they run beside other work); scratch as seg_sort's, reused in turn otherwise
+int seg_sort2(const float* a, float* a_keys, uint32_t* a_perm, const float* b, float* b_keys, uint32_t* b_perm,
+              int S, int L, void* scratch, hipStream_t st);
 
 // ---- walks.hip ----
 // Keys per key range (one wave per range) for a channel count C.
@@ -165,6 +169,9 @@ int range_bounds(const AbsWalkArgs& a, int* qb, hipStream_t st);
 // queries qs (S segments of Mq), ranges of range_keys(C) keys
 int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S, int Ns, int Mq, int C,
                  hipStream_t st);
+// query_bounds for nsets <= 3 shifts in one launch: qb[i] for shift[i]
+int query_bounds_sets(const float* ks, const float* qs, int* const qb[], const float shift[], int nsets, int S,
+                      int Ns, int Mq, int C, hipStream_t st);
 // The queries of every segment (shifted by qshift) grouped by key chunk, a quarter of a key range: qs / qp (S segments
 // of Mq) get the values and original indices of chunk 0's queries, then chunk 1's, ... (a query's chunk holds the first
 // key >= q + qshift), so each range's queries are contiguous and come chunk by chunk; the order inside a chunk is not

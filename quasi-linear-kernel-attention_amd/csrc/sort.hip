@@ -18,10 +18,19 @@ namespace qlka {
 
 template <int WAVES, int ITEMS>
 __global__ __launch_bounds__(WAVES * WAVE)
-void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int run_len, const int runs_per_seg,
-                    float* __restrict__ out_keys, uint32_t* __restrict__ out_perm,        // direct output (1 run)
-                    uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_idx)       // run output (merging)
+void lds_radix_sort(const float* __restrict__ in1, const int seg_len, const int run_len, const int runs_per_seg,
+                    float* __restrict__ out_keys1, uint32_t* __restrict__ out_perm1,      // direct output (1 run)
+                    uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_idx,       // run output (merging)
+                    const int blocks1, const float* __restrict__ in2, float* __restrict__ out_keys2,
+                    uint32_t* __restrict__ out_perm2)                                     // second array (1 run)
 {
+    // blocks [0, blocks1) sort the segments of in1, the blocks after them those of in2 (same segment length), so that
+    // two arrays are sorted by one launch
+    const bool second = (int)blockIdx.x >= blocks1;
+    const int bid = second ? (int)blockIdx.x - blocks1 : (int)blockIdx.x;
+    const float* in = second ? in2 : in1;
+    float* out_keys = second ? out_keys2 : out_keys1;
+    uint32_t* out_perm = second ? out_perm2 : out_perm1;
     constexpr int THREADS = WAVES * WAVE;
     constexpr int CAP     = THREADS * ITEMS;
     __shared__ uint32_t skey[CAP];
@@ -29,8 +38,8 @@ void lds_radix_sort(const float* __restrict__ in, const int seg_len, const int r
     __shared__ uint32_t hist[WAVES * 256];
     __shared__ uint32_t dbase[256];
 
-    const int seg   = blockIdx.x / runs_per_seg;
-    const int run   = blockIdx.x - seg * runs_per_seg;
+    const int seg   = bid / runs_per_seg;
+    const int run   = bid - seg * runs_per_seg;
     const int start = run * run_len;
     const int len   = min(run_len, seg_len - start);
     const size_t seg_off = (size_t)seg * seg_len;
@@ -243,10 +252,12 @@ void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__
 
 template <int WAVES, int ITEMS>
 static void launch_lds(const float* in, int S, int L, int run_len, int runs, float* ok, uint32_t* op,
-                       uint32_t* rk, uint32_t* ri, hipStream_t st) {
+                       uint32_t* rk, uint32_t* ri, hipStream_t st, const float* in2 = nullptr, float* ok2 = nullptr,
+                       uint32_t* op2 = nullptr) {
     StageTimer t("lds_radix_sort", st);
-    hipLaunchKernelGGL((lds_radix_sort<WAVES, ITEMS>), dim3(S * runs), dim3(WAVES * WAVE), 0, st,
-                       in, L, run_len, runs, ok, op, rk, ri);
+    const int blocks1 = S * runs;
+    hipLaunchKernelGGL((lds_radix_sort<WAVES, ITEMS>), dim3(in2 ? 2 * blocks1 : blocks1), dim3(WAVES * WAVE), 0, st,
+                       in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
 }
 
 size_t seg_sort_scratch_bytes(int S, int L) {
@@ -254,22 +265,37 @@ size_t seg_sort_scratch_bytes(int S, int L) {
     return 4 * (size_t)S * (size_t)L * sizeof(uint32_t);   // two (key, idx) ping-pong buffers
 }
 
+// One launch of the LDS sort over the S segments of `in` (and, with in2, those of in2) of length L <= LDS_SORT_MAX.
+static int lds_sort(const float* in, float* out_keys, uint32_t* out_perm, const float* in2, float* out_keys2,
+                    uint32_t* out_perm2, int S, int L, hipStream_t st) {
+    // smallest (waves, items) whose capacity covers L; more waves for long runs keep 16 items per thread max
+#define QLKA_LDS(W, I) launch_lds<W, I>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st, in2, out_keys2, \
+                                        out_perm2)
+    if      (L <= 64)    QLKA_LDS(1, 1);
+    else if (L <= 128)   QLKA_LDS(1, 2);
+    else if (L <= 256)   QLKA_LDS(1, 4);
+    else if (L <= 512)   QLKA_LDS(2, 4);
+    else if (L <= 1024)  QLKA_LDS(4, 4);
+    else if (L <= 2048)  QLKA_LDS(8, 4);
+    else if (L <= 4096)  QLKA_LDS(16, 4);
+    else if (L <= 8192)  QLKA_LDS(16, 8);
+    else                 QLKA_LDS(16, 16);
+#undef QLKA_LDS
+    return (int)hipGetLastError();
+}
+
+int seg_sort2(const float* a, float* a_keys, uint32_t* a_perm, const float* b, float* b_keys, uint32_t* b_perm,
+              int S, int L, void* scratch, hipStream_t st) {
+    if (S <= 0 || L <= 0) return 0;
+    if (L <= LDS_SORT_MAX) return lds_sort(a, a_keys, a_perm, b, b_keys, b_perm, S, L, st);
+    if (int e = seg_sort(a, a_keys, a_perm, S, L, scratch, st)) return e;
+    return seg_sort(b, b_keys, b_perm, S, L, scratch, st);
+}
+
 int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch,
              hipStream_t st) {
     if (S <= 0 || L <= 0) return 0;
-    if (L <= LDS_SORT_MAX) {
-        // smallest (waves, items) whose capacity covers L; more waves for long runs keep 16 items per thread max
-        if      (L <= 64)    launch_lds<1, 1>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else if (L <= 128)   launch_lds<1, 2>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else if (L <= 256)   launch_lds<1, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else if (L <= 512)   launch_lds<2, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else if (L <= 1024)  launch_lds<4, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else if (L <= 2048)  launch_lds<8, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else if (L <= 4096)  launch_lds<16, 4>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else if (L <= 8192)  launch_lds<16, 8>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        else                 launch_lds<16, 16>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st);
-        return (int)hipGetLastError();
-    }
+    if (L <= LDS_SORT_MAX) return lds_sort(in, out_keys, out_perm, nullptr, nullptr, nullptr, S, L, st);
     const size_t n = (size_t)S * (size_t)L;
     uint32_t* k0 = (uint32_t*)scratch;
     uint32_t* i0 = k0 + n;

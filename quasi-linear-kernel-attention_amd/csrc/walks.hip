@@ -735,13 +735,20 @@ constexpr int RB_T = 1024;         // threads per workgroup
 constexpr int RB_Q = 4;            // consecutive queries per thread
 constexpr int RB_MAXG = 4096;      // ranges per segment: N <= 131072 keys in ranges of >= 32
 
+// Up to three query shifts in one launch: blocks [i * S * chunks, (i + 1) * S * chunks) write qb[i] for shift[i].
+struct BoundSets { int* qb[3]; float shift[3]; };
+
 template <int RK>
 __global__ __launch_bounds__(RB_T)
-void query_bounds_kernel(const float* __restrict__ ks, const float* __restrict__ qs, int* __restrict__ qb,
-                         const float qshift, const int Ns, const int Mq, const int G, const int chunks)
+void query_bounds_kernel(const float* __restrict__ ks, const float* __restrict__ qs, const BoundSets sets,
+                         const int S, const int Ns, const int Mq, const int G, const int chunks)
 {
     __shared__ float bnd[RB_MAXG];
-    const int s = blockIdx.x / chunks, ch = blockIdx.x - s * chunks;
+    const int set = blockIdx.x / (S * chunks);
+    const int blk = blockIdx.x - set * S * chunks;
+    const int s = blk / chunks, ch = blk - s * chunks;
+    int* __restrict__ qb = sets.qb[set];
+    const float qshift = sets.shift[set];
     const float* kseg = ks + (size_t)s * Ns;
     for (int g = threadIdx.x; g < G; g += RB_T) bnd[g] = kseg[min(Ns, (g + 1) * RK) - 1];
     __syncthreads();
@@ -775,19 +782,28 @@ void query_bounds_kernel(const float* __restrict__ ks, const float* __restrict__
     }
 }
 
-int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S, int Ns, int Mq, int C,
-                 hipStream_t st) {
+int query_bounds_sets(const float* ks, const float* qs, int* const qb[], const float shift[], int nsets, int S,
+                      int Ns, int Mq, int C, hipStream_t st) {
     const int RK = range_keys(C);
     const int G = (Ns + RK - 1) / RK;
-    if (G > RB_MAXG) return (int)hipErrorInvalidValue;
+    if (G > RB_MAXG || nsets < 1 || nsets > 3) return (int)hipErrorInvalidValue;
+    BoundSets sets{};
+    for (int i = 0; i < nsets; ++i) { sets.qb[i] = qb[i]; sets.shift[i] = shift[i]; }
     const int chunks = (Mq + RB_T * RB_Q - 1) / (RB_T * RB_Q);
-    const dim3 grid((unsigned)((long)S * chunks));
+    const dim3 grid((unsigned)((long)nsets * S * chunks));
     StageTimer t("query_bounds", st);
     if (RK == 64)
-        hipLaunchKernelGGL((query_bounds_kernel<64>), grid, dim3(RB_T), 0, st, ks, qs, qb, qshift, Ns, Mq, G, chunks);
+        hipLaunchKernelGGL((query_bounds_kernel<64>), grid, dim3(RB_T), 0, st, ks, qs, sets, S, Ns, Mq, G, chunks);
     else
-        hipLaunchKernelGGL((query_bounds_kernel<32>), grid, dim3(RB_T), 0, st, ks, qs, qb, qshift, Ns, Mq, G, chunks);
+        hipLaunchKernelGGL((query_bounds_kernel<32>), grid, dim3(RB_T), 0, st, ks, qs, sets, S, Ns, Mq, G, chunks);
     return (int)hipGetLastError();
+}
+
+int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S, int Ns, int Mq, int C,
+                 hipStream_t st) {
+    int* const qbs[1] = {qb};
+    const float sh[1] = {qshift};
+    return query_bounds_sets(ks, qs, qbs, sh, 1, S, Ns, Mq, C, st);
 }
 
 // Queries grouped by key chunk, the forward walks' alternative to sorting them. The sorted keys of a segment fall into

@@ -111,8 +111,12 @@ def test_layer_workspace_and_validation(lib):
     one_eval = 16384 * 64 * 4 + 16384 * 4                      # out_w + out_u of one op evaluation
     assert lap >= lib.qlka_laplace_fwd_ws_bytes(*dims) + one_eval
     assert riesz >= op + one_eval
-    assert bump >= op + 3 * one_eval                          # three shifted evaluations, one shared slab
-    assert bump < 2 * op
+    slab = 64 * 16384 * 64 * 4                                 # one p's contribution rows
+    assert bump >= op + 2 * slab                               # three query sets walked at once: three slabs
+    assert bump < 3 * op
+    # without a foldable epilogue (C / 4 not a power of two) the three evaluations share one slab in turn
+    odd = (1, 64, 16384, 16384, 63)
+    assert lib.qlka_layer_fwd_ws_bytes(2, *odd) < 2 * lib.qlka_abs_fwd_ws_bytes(*odd)
     assert lib.qlka_layer_fwd_ws_bytes(3, *dims) == 0
     dummy = ctypes.c_void_p(16)     # never dereferenced: validation fails first
     rc = lib.qlka_layer_fwd(3, dummy, dummy, dummy, None, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
