@@ -256,6 +256,9 @@ def main():
     ap.add_argument("--profile-config", type=int, default=None, choices=sorted(CONFIGS),
                     help="only time this configuration's workload (--steps calls) and print its config_ms entry, "
                          "e.g. under rocprofv3")
+    ap.add_argument("--ws-budget-gib", type=float, default=None,
+                    help="libqlka workspace budget (qlka_set_workspace_budget) for every timed call, in GiB; "
+                         "default: the library's")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -269,6 +272,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 3}), flush=True)
         return
+    if args.ws_budget_gib is not None:
+        from qlka import _lib as _l
+        _l.load().qlka_set_workspace_budget(int(args.ws_budget_gib * (1 << 30)))
     if args.profile_config is not None:
         dev = torch.device("cuda", 0)
         print(json.dumps(config_timings(dev, reps=args.steps, only=args.profile_config)), flush=True)

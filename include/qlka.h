@@ -40,7 +40,7 @@ int qlka_version(void);
  */
 int qlka_set_direct_max(int n);
 /*
- * Workspace budget in bytes (default 8 GiB). Every operator below runs its whole pipeline on chunks of consecutive
+ * Workspace budget in bytes (default 16 GiB). Every operator below runs its whole pipeline on chunks of consecutive
  * p = (batch, head) indices (every stage works on each p alone), taking the largest chunk the workspace it is given
  * holds (at least one p), so the caller bounds device memory by the workspace it passes. The *_ws_bytes() queries
  * report the workspace of the largest chunk within this budget (one p when even one p exceeds it); results do not

@@ -67,6 +67,7 @@ struct SortedWs {
     float* ks; uint32_t* kp; float* qs; uint32_t* qp;
     void* sort_scratch; RangeArrays ra;
     float* slab; float* uslab; float* uq;
+    int* group;          // query grouping scratch (long segments)
 };
 
 struct WsSpec {
@@ -86,26 +87,30 @@ size_t ws_part(const WsSpec& w, int i) {
         case 6: return w.slab_rows ? align256(S * slab_rows(w.slab_rows) * (size_t)slab_stride(w.C) * 4) : 0;
         case 7: return (w.slab_rows && w.want_u) ? align256(S * w.slab_rows * 4) : 0;
         case 8: return (w.slab_rows && w.want_u) ? align256(S * w.M * 4) : 0;   // v == 1 terms in query order
+        case 9: return align256(group_scratch_bytes((int)S, w.N, w.M, w.C));        // query grouping counts
     }
     return 0;
 }
 
+constexpr int WS_PARTS = 10;
+
 size_t ws_bytes(const WsSpec& w) {
     size_t b = 0;
-    for (int i = 0; i < 9; ++i) b += ws_part(w, i);
+    for (int i = 0; i < WS_PARTS; ++i) b += ws_part(w, i);
     return b;
 }
 
 SortedWs carve(void* ws, const WsSpec& w) {
     char* b = (char*)ws;
-    char* part[9];
-    for (int i = 0; i < 9; ++i) { part[i] = b; b += ws_part(w, i); }
+    char* part[WS_PARTS];
+    for (int i = 0; i < WS_PARTS; ++i) { part[i] = b; b += ws_part(w, i); }
     SortedWs r;
     r.ks = (float*)part[0]; r.kp = (uint32_t*)part[1]; r.qs = (float*)part[2]; r.qp = (uint32_t*)part[3];
     r.sort_scratch = part[4];
     r.ra = carve_range_arrays(part[5], w.P * w.D, w.range_stream_max, w.C);
     r.slab = (float*)part[6]; r.uslab = (float*)part[7];
     r.uq = ws_part(w, 8) ? (float*)part[8] : nullptr;
+    r.group = ws_part(w, 9) ? (int*)part[9] : nullptr;
     return r;
 }
 
@@ -119,7 +124,7 @@ int check_ws(void* ws, size_t have, size_t need) {
 // whole pipeline (sorts, range passes, walks, reduce, epilogue) on a chunk of pc consecutive p at a time, with a
 // workspace sized for pc. An operator takes the largest chunk that the workspace it is given holds; the *_ws_bytes()
 // queries size the workspace for the largest chunk within the process-wide budget (qlka_set_workspace_budget).
-std::atomic<size_t> g_ws_budget{size_t(8) << 30};
+std::atomic<size_t> g_ws_budget{size_t(16) << 30};
 
 // largest pc in [1, P] with bytes(pc) <= cap, or 1 when even one p does not fit (bytes() grows with pc)
 template <class Bytes>
@@ -162,7 +167,7 @@ int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, 
 // The query side of a forward walk that keeps no sorts: q grouped by key chunk, with the range bounds, in one pass
 // (the walks take grouped queries as well as sorted ones).
 static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int M, int C, hipStream_t st) {
-    return hip_status(group_queries(w.ks, q, w.qs, w.qp, w.ra.qb, qshift, S, N, M, C, st), "query grouping");
+    return hip_status(group_queries(w.ks, q, w.qs, w.qp, w.ra.qb, qshift, S, N, M, C, w.group, st), "query grouping");
 }
 
 // ---- overlap of the query side (q sort, range boundaries) with the key side (range summaries, scan)

@@ -52,6 +52,7 @@ struct RangeArrays {
     float* ta;   // [S][G+1][stride] range states (written by the scan)
     float* tb;   // [S][G+1][stride]
     int*   qb;   // [S][G]
+    float* aggs; // per-workgroup scan aggregates of segments longer than one scan workgroup (else nullptr)
 };
 size_t range_arrays_bytes(int S, int Nstream, int C);
 RangeArrays carve_range_arrays(void* base, int S, int Nstream, int C);
@@ -177,7 +178,9 @@ int query_bounds_sets(const float* ks, const float* qs, int* const qb[], const f
 // key >= q + qshift), so each range's queries are contiguous and come chunk by chunk; the order inside a chunk is not
 // fixed. qb as query_bounds writes it. The forward walks accept these grouped queries as well as sorted ones.
 int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int* qb, float qshift, int S, int Ns,
-                  int Mq, int C, hipStream_t st);
+                  int Mq, int C, int* scratch, hipStream_t st);
+// scratch of group_queries (per-tile bucket counts of segments too long to stage in LDS; 0 when every segment fits)
+size_t group_scratch_bytes(int S, int Ns, int Mq, int C);
 int range_count(int Ns, int C);          // key ranges per segment
 
 // Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null

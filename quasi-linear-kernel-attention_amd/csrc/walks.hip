@@ -41,11 +41,14 @@ constexpr int WPB = 4;             // waves per workgroup for the range kernels
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
+size_t scan_agg_bytes(int S, int Ns, int C);
+
 size_t range_arrays_bytes(int S, int Ns, int C) {
     const int RK = range_keys(C);
     const size_t G = (size_t)((Ns + RK - 1) / RK);
     const size_t rows = (size_t)S * (G + 1);
-    return 4 * align256(rows * range_stride(C) * sizeof(float)) + align256((size_t)S * G * sizeof(int));
+    return 4 * align256(rows * range_stride(C) * sizeof(float)) + align256((size_t)S * G * sizeof(int)) +
+           align256(scan_agg_bytes(S, Ns, C));
 }
 
 RangeArrays carve_range_arrays(void* base, int S, int Ns, int C) {
@@ -58,7 +61,8 @@ RangeArrays carve_range_arrays(void* base, int S, int Ns, int C) {
     r.sb = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
     r.ta = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
     r.tb = (float*)b; b += align256(rows * range_stride(C) * sizeof(float));
-    r.qb = (int*)b;
+    r.qb = (int*)b; b += align256((size_t)S * G * sizeof(int));
+    r.aggs = scan_agg_bytes(S, Ns, C) ? (float*)b : nullptr;
     return r;
 }
 
@@ -248,24 +252,51 @@ __device__ __forceinline__ void store_scan_row(float* __restrict__ row, const in
     if (lane_id() == 0) row[C] = r[NV];
 }
 
+// Long segments are scanned by several workgroups of SCAN_BLOCK ranges each, in two launches: phase 1 runs every wave's
+// piece from a zero state and writes the wave aggregates and, composed in order, the workgroup's aggregate; phase 2
+// composes the aggregates of the workgroups before (and, for a suffix, after) its own into its incoming state, then
+// the waves of its own before (after) theirs, and reruns each piece from the true state, writing the range states.
+// Segments of up to SCAN_BLOCK ranges (N <= 16384 at 64-key ranges) run both phases in one workgroup (phase 0).
+constexpr int SCAN_BLOCK = 256;
+__host__ __device__ inline int scan_blocks(int G) { return (G + SCAN_BLOCK - 1) / SCAN_BLOCK; }
+// floats of one workgroup's aggregate record: SCAN_W wave aggregates + the workgroup aggregate, each two (state,
+// link) pairs of NV + 1 lane vectors and one lane vector
+template <int NV> __host__ __device__ constexpr int scan_rec_floats() { return (SCAN_W + 1) * 2 * (NV + 2) * WAVE; }
+size_t scan_agg_bytes(int S, int Ns, int C) {
+    const int G = (Ns + range_keys(C) - 1) / range_keys(C);
+    const int nb = scan_blocks(G);
+    if (nb <= 1) return 0;
+    return (size_t)S * nb * (C <= WAVE ? scan_rec_floats<1>() : scan_rec_floats<2>()) * sizeof(float);
+}
+
+// one aggregate (two lane-vector sets of NV + 1 values plus one lane vector) in a record: slot i of SCAN_W + 1
+template <int NV>
+__device__ __forceinline__ float* agg_slot(float* rec, int i, int part) {
+    return rec + ((size_t)i * 2 + part) * (NV + 2) * WAVE;
+}
+
 // Laplace: entry L state of every range (relative to the last key before the range) and exit R state (relative to
 // the first key after it). Forward: L <- a_g + e^{-(klast_g - klast_{g-1})} L; backward: R <- b_g +
 // e^{-(kfirst_{g+1} - kfirst_g)} R. A piece composes to  out = local + (product of its decays) in.
-template <int NV, int RK>
+template <int NV, int RK, int PHASE>
 __global__ __launch_bounds__(SCAN_W * WAVE)
 void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ ta,
-                    float* __restrict__ tb, const int S, const int C, const int G)
+                    float* __restrict__ tb, float* __restrict__ aggs, const int S, const int C, const int G)
 {
     __shared__ float agg[2][SCAN_W][NV + 1][WAVE];
     __shared__ float span[2][SCAN_W];
-    const int s = blockIdx.x, w = wave_in_block(), l = lane_id();
+    const int nb = PHASE == 0 ? 1 : scan_blocks(G);
+    const int s = blockIdx.x / nb, blk = blockIdx.x - s * nb;
+    const int w = wave_in_block(), l = lane_id();
     const int CS = range_stride(C);
     const float* SA = sa + (size_t)s * (G + 1) * CS;
     const float* SB = sb + (size_t)s * (G + 1) * CS;
     float* A = ta + (size_t)s * (G + 1) * CS;
     float* B = tb + (size_t)s * (G + 1) * CS;
-    const int per = (G + SCAN_W - 1) / SCAN_W;
-    const int glo = min(G, w * per), ghi = min(G, w * per + per);
+    const int b0 = PHASE == 0 ? 0 : blk * SCAN_BLOCK, b1 = PHASE == 0 ? G : min(G, b0 + SCAN_BLOCK);
+    const int per = (b1 - b0 + SCAN_W - 1) / SCAN_W;
+    const int glo = min(b1, b0 + w * per), ghi = min(b1, b0 + w * per + per);
+    float* seg_aggs = PHASE == 0 ? nullptr : aggs + (size_t)s * nb * scan_rec_floats<NV>();
 
     // forward piece walk from state cur; writes entry states when OUT; returns the product of the piece's decays
     auto fwd = [&](float (&cur)[NV + 1], const bool out) {
@@ -306,19 +337,75 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
         return prod;
     };
 
-    float cf[NV + 1], cb[NV + 1];
+    float cf[NV + 1], cb[NV + 1], pf = 1.f, pb = 1.f;
+    if constexpr (PHASE <= 1) {
+        // pass 1: every piece from a zero state; empty pieces have product 1 and aggregate 0
 #pragma unroll
-    for (int j = 0; j <= NV; ++j) { cf[j] = 0.f; cb[j] = 0.f; }
-    const float pf = fwd(cf, false), pb = bwd(cb, false);
+        for (int j = 0; j <= NV; ++j) { cf[j] = 0.f; cb[j] = 0.f; }
+        pf = fwd(cf, false);
+        pb = bwd(cb, false);
 #pragma unroll
-    for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = cf[j]; agg[1][w][j][l] = cb[j]; }
-    if (l == 0) { span[0][w] = pf; span[1][w] = pb; }
+        for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = cf[j]; agg[1][w][j][l] = cb[j]; }
+        if (l == 0) { span[0][w] = pf; span[1][w] = pb; }
+    }
+    if constexpr (PHASE == 1) {
+        // the wave aggregates, and wave 0 (forward) / wave 1 (backward) composes the workgroup's
+        float* rec = seg_aggs + (size_t)blk * scan_rec_floats<NV>();
+        for (int part = 0; part < 2; ++part) {
+            float* ws_ = agg_slot<NV>(rec, w, part);
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) ws_[j * WAVE + l] = part ? cb[j] : cf[j];
+            ws_[(NV + 1) * WAVE + l] = part ? pb : pf;
+        }
+        __syncthreads();
+        if (w < 2) {
+            const int part = w;
+            float c[NV + 1], d = 1.f;
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) c[j] = 0.f;
+            for (int k = 0; k < SCAN_W; ++k) {
+                const int ww = part == 0 ? k : SCAN_W - 1 - k;    // forward: left to right; backward: right to left
+                const float dd = span[part][ww];
+#pragma unroll
+                for (int j = 0; j <= NV; ++j) c[j] = agg[part][ww][j][l] + dd * c[j];
+                d *= dd;
+            }
+            float* bs = agg_slot<NV>(rec, SCAN_W, part);
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) bs[j * WAVE + l] = c[j];
+            bs[(NV + 1) * WAVE + l] = d;
+        }
+        return;
+    }
+    if constexpr (PHASE == 2) {
+        // this workgroup's wave aggregates, from phase 1
+        const float* rec = seg_aggs + (size_t)blk * scan_rec_floats<NV>();
+        for (int part = 0; part < 2; ++part) {
+            const float* ws_ = agg_slot<NV>(const_cast<float*>(rec), w, part);
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) agg[part][w][j][l] = ws_[j * WAVE + l];
+            if (l == 0) span[part][w] = ws_[(NV + 1) * WAVE];
+        }
+    }
     __syncthreads();
 
-    // incoming states: compose the aggregates of the pieces to the left (forward) and to the right (backward);
-    // empty pieces have product 1 and aggregate 0
+    // incoming states: the workgroups before (forward) / after (backward) this one, then its waves before / after
 #pragma unroll
     for (int j = 0; j <= NV; ++j) { cf[j] = 0.f; cb[j] = 0.f; }
+    if constexpr (PHASE == 2) {
+        for (int bb = 0; bb < blk; ++bb) {
+            const float* bs = agg_slot<NV>(seg_aggs + (size_t)bb * scan_rec_floats<NV>(), SCAN_W, 0);
+            const float d = bs[(NV + 1) * WAVE + l];
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) cf[j] = bs[j * WAVE + l] + d * cf[j];
+        }
+        for (int bb = nb - 1; bb > blk; --bb) {
+            const float* bs = agg_slot<NV>(seg_aggs + (size_t)bb * scan_rec_floats<NV>(), SCAN_W, 1);
+            const float d = bs[(NV + 1) * WAVE + l];
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) cb[j] = bs[j * WAVE + l] + d * cb[j];
+        }
+    }
     for (int ww = 0; ww < w; ++ww) {
         const float d = span[0][ww];
 #pragma unroll
@@ -616,8 +703,17 @@ static int laplace_prepare_t(const float* ks, const uint32_t* kp, const float* v
     }
     {
         StageTimer t("lap_range_scan", st);
-        hipLaunchKernelGGL((lap_range_scan<NV, RK>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
-                           ra.sa, ra.sb, ra.ta, ra.tb, S, C, G);
+        const int nb = scan_blocks(G);
+        if (nb <= 1) {
+            hipLaunchKernelGGL((lap_range_scan<NV, RK, 0>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
+                               ra.sa, ra.sb, ra.ta, ra.tb, nullptr, S, C, G);
+        } else {
+            if (ra.aggs == nullptr) return (int)hipErrorInvalidValue;
+            hipLaunchKernelGGL((lap_range_scan<NV, RK, 1>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st,
+                               ra.sa, ra.sb, ra.ta, ra.tb, ra.aggs, S, C, G);
+            hipLaunchKernelGGL((lap_range_scan<NV, RK, 2>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st,
+                               ra.sa, ra.sb, ra.ta, ra.tb, ra.aggs, S, C, G);
+        }
     }
     return (int)hipGetLastError();
 }
@@ -942,98 +1038,183 @@ void group_queries_staged(const float* __restrict__ ks, const float* __restrict_
     }
 }
 
-// Any segment length: two passes over the queries (the second searches again) and direct scattered stores.
-template <int CH>
-__global__ __launch_bounds__(GQ_T)
-void group_queries_global(const float* __restrict__ ks, const float* __restrict__ q, float* __restrict__ qs,
-                          uint32_t* __restrict__ qp, int* __restrict__ qb, const float qshift, const int Ns,
-                          const int Mq, const int G, const int Gc)
-{
-    __shared__ GroupLds<GQ_MAXB, 1> sm;
-    const int s = blockIdx.x, tid = threadIdx.x;
-    const float* kseg = ks + (size_t)s * Ns;
-    const float* qseg = q + (size_t)s * Mq;
-    for (int c = tid; c < Gc; c += GQ_T) {
+// Segments too long to stage (more than GQ_STAGE queries, or more than GQ_STAGE_MAXB buckets): three passes with tiles
+// of GT_Q queries, so that a segment is spread over many workgroups. group_count: each (segment, tile) counts its
+// queries per bucket into counts[s][tile][bucket]. group_offsets: per segment, the exclusive scan of the counts in
+// (bucket, tile) order gives every (tile, bucket) its first slot, and the range bounds. group_scatter: each (segment,
+// tile) buckets its queries again and places them with returning LDS atomics on its slots (direct scattered stores).
+constexpr int GT_Q = 16384;        // queries per tile (16 per thread)
+
+template <int MAXB>
+struct BucketLds {
+    float bnd[MAXB];
+    float rb[MAXB / 4];
+    int off[MAXB + 1];
+};
+
+// the segment's Gc chunk boundaries (and the range boundaries) into LDS
+template <int CH, int MAXB>
+__device__ __forceinline__ void load_bounds(BucketLds<MAXB>& sm, const float* kseg, const int Ns, const int Gc) {
+    for (int c = threadIdx.x; c < Gc; c += GQ_T) {
         const float y = kseg[min(Ns, (c + 1) * CH) - 1];
         sm.bnd[c] = y;
         if ((c & 3) == 3 || c == Gc - 1) sm.rb[c >> 2] = y;
     }
+}
+
+template <int CH>
+__global__ __launch_bounds__(GQ_T)
+void group_count(const float* __restrict__ ks, const float* __restrict__ q, int* __restrict__ counts,
+                 const float qshift, const int Ns, const int Mq, const int Gc, const int tiles)
+{
+    __shared__ BucketLds<GQ_MAXB> sm;
+    const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles, tid = threadIdx.x;
+    const float* qseg = q + (size_t)s * Mq;
+    const int i0 = tile * GT_Q;
+    constexpr int NI = GT_Q / GQ_T;
+    float x[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)] + qshift;   // clamped: all in flight
+    load_bounds<CH>(sm, ks + (size_t)s * Ns, Ns, Gc);
     for (int c = tid; c <= Gc; c += GQ_T) sm.off[c] = 0;
     __syncthreads();
-    constexpr int NI = 4;
-    for (int i0 = 0; i0 < Mq; i0 += NI * GQ_T) {
-        float x[NI];
-        int b[NI];
+    int b[NI];
+    buckets<NI>(sm.bnd, sm.rb, Gc, x, b);
 #pragma unroll
-        for (int j = 0; j < NI; ++j) x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)] + qshift;
-        buckets<NI>(sm.bnd, sm.rb, Gc, x, b);
-#pragma unroll
-        for (int j = 0; j < NI; ++j)
-            if (i0 + tid + j * GQ_T < Mq) atomicAdd(&sm.off[b[j]], 1);
-    }
+    for (int j = 0; j < NI; ++j)
+        if (i0 + tid + j * GQ_T < Mq) atomicAdd(&sm.off[b[j]], 1);
     __syncthreads();
-    group_scan(sm.off, sm.wsum, Gc + 1, qb + (size_t)s * G);
-    float* qso = qs + (size_t)s * Mq;
-    uint32_t* qpo = qp + (size_t)s * Mq;
-    for (int i0 = 0; i0 < Mq; i0 += NI * GQ_T) {
-        float x[NI], xs[NI];
-        int b[NI];
+    int* out = counts + ((size_t)s * tiles + tile) * (Gc + 1);
+    for (int c = tid; c <= Gc; c += GQ_T) out[c] = sm.off[c];
+}
+
+__global__ __launch_bounds__(GQ_T)
+void group_offsets(int* __restrict__ counts, int* __restrict__ qb, const int Gc, const int tiles, const int G)
+{
+    __shared__ int wsum[GQ_T / WAVE];
+    const int s = blockIdx.x, tid = threadIdx.x;
+    const int n = Gc + 1;
+    int* cs = counts + (size_t)s * tiles * n;
+    // thread t owns buckets [e0, e1); a bucket's total is the sum over the tiles
+    const int E = (n + GQ_T - 1) / GQ_T;
+    const int e0 = min(tid * E, n), e1 = min(e0 + E, n);
+    int own = 0;
+    for (int c = e0; c < e1; ++c)
+        for (int t = 0; t < tiles; ++t) own += cs[(size_t)t * n + c];
+    int incl = own;
 #pragma unroll
-        for (int j = 0; j < NI; ++j) { x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)]; xs[j] = x[j] + qshift; }
-        buckets<NI>(sm.bnd, sm.rb, Gc, xs, b);
-#pragma unroll
-        for (int j = 0; j < NI; ++j) {
-            const int i = i0 + tid + j * GQ_T;
-            if (i < Mq) {
-                const int pos = atomicAdd(&sm.off[b[j]], 1);
-                qso[pos] = x[j];
-                qpo[pos] = (uint32_t)i;
-            }
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const int y = __shfl_up(incl, d, WAVE);
+        if (lane_id() >= d) incl += y;
+    }
+    if (lane_id() == WAVE - 1) wsum[tid / WAVE] = incl;
+    __syncthreads();
+    int base = incl - own;
+    for (int w = 0; w < tid / WAVE; ++w) base += wsum[w];
+    int* qbs = qb + (size_t)s * G;
+    for (int c = e0; c < e1; ++c) {
+        if (c > 0 && ((c & 3) == 0 || c == n - 1)) qbs[(c - 1) >> 2] = base;
+        for (int t = 0; t < tiles; ++t) {                 // in place: count -> first slot of (tile, bucket)
+            const int cnt = cs[(size_t)t * n + c];
+            cs[(size_t)t * n + c] = base;
+            base += cnt;
         }
     }
 }
 
+template <int CH>
+__global__ __launch_bounds__(GQ_T)
+void group_scatter(const float* __restrict__ ks, const float* __restrict__ q, const int* __restrict__ offsets,
+                   float* __restrict__ qs, uint32_t* __restrict__ qp, const float qshift, const int Ns, const int Mq,
+                   const int Gc, const int tiles)
+{
+    __shared__ BucketLds<GQ_MAXB> sm;
+    const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles, tid = threadIdx.x;
+    const float* qseg = q + (size_t)s * Mq;
+    const int i0 = tile * GT_Q;
+    constexpr int NI = GT_Q / GQ_T;
+    float x[NI], xs[NI];
+#pragma unroll
+    for (int j = 0; j < NI; ++j) { x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)]; xs[j] = x[j] + qshift; }
+    load_bounds<CH>(sm, ks + (size_t)s * Ns, Ns, Gc);
+    const int* off = offsets + ((size_t)s * tiles + tile) * (Gc + 1);
+    for (int c = tid; c <= Gc; c += GQ_T) sm.off[c] = off[c];
+    __syncthreads();
+    int b[NI];
+    buckets<NI>(sm.bnd, sm.rb, Gc, xs, b);
+    float* qso = qs + (size_t)s * Mq;
+    uint32_t* qpo = qp + (size_t)s * Mq;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+        const int i = i0 + tid + j * GQ_T;
+        if (i < Mq) {
+            const int pos = atomicAdd(&sm.off[b[j]], 1);
+            qso[pos] = x[j];
+            qpo[pos] = (uint32_t)i;
+        }
+    }
+}
+
+size_t group_scratch_bytes(int S, int Ns, int Mq, int C) {
+    const int RK = range_keys(C), CH = RK / 4;
+    const int Gc = (Ns + CH - 1) / CH;
+    if (Mq <= GQ_STAGE && Gc <= GQ_STAGE_MAXB) return 0;
+    const int tiles = (Mq + GT_Q - 1) / GT_Q;
+    return (size_t)S * tiles * (Gc + 1) * sizeof(int);
+}
+
 int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int* qb, float qshift, int S, int Ns,
-                  int Mq, int C, hipStream_t st) {
+                  int Mq, int C, int* scratch, hipStream_t st) {
     const int RK = range_keys(C), CH = RK / 4;
     const int G = (Ns + RK - 1) / RK, Gc = (Ns + CH - 1) / CH;
     if (Gc > GQ_MAXB) return (int)hipErrorInvalidValue;
-    const bool staged = Mq <= GQ_STAGE && Gc <= GQ_STAGE_MAXB;
     StageTimer t("group_queries", st);
-    if (CH == 16) {
-        if (staged) hipLaunchKernelGGL((group_queries_staged<16>), dim3(S), dim3(GQ_T), 0, st,
-                                       ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
-        else hipLaunchKernelGGL((group_queries_global<16>), dim3(S), dim3(GQ_T), 0, st,
+    if (Mq <= GQ_STAGE && Gc <= GQ_STAGE_MAXB) {
+        if (CH == 16) hipLaunchKernelGGL((group_queries_staged<16>), dim3(S), dim3(GQ_T), 0, st,
+                                         ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
+        else hipLaunchKernelGGL((group_queries_staged<8>), dim3(S), dim3(GQ_T), 0, st,
                                 ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
-    } else {
-        if (staged) hipLaunchKernelGGL((group_queries_staged<8>), dim3(S), dim3(GQ_T), 0, st,
-                                       ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
-        else hipLaunchKernelGGL((group_queries_global<8>), dim3(S), dim3(GQ_T), 0, st,
-                                ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
+        return (int)hipGetLastError();
     }
+    if (scratch == nullptr) return (int)hipErrorInvalidValue;
+    const int tiles = (Mq + GT_Q - 1) / GT_Q;
+    const dim3 grid((unsigned)((long)S * tiles));
+    if (CH == 16) hipLaunchKernelGGL((group_count<16>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qshift, Ns, Mq, Gc,
+                                     tiles);
+    else hipLaunchKernelGGL((group_count<8>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qshift, Ns, Mq, Gc, tiles);
+    hipLaunchKernelGGL(group_offsets, dim3(S), dim3(GQ_T), 0, st, scratch, qb, Gc, tiles, G);
+    if (CH == 16) hipLaunchKernelGGL((group_scatter<16>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qs, qp, qshift, Ns,
+                                     Mq, Gc, tiles);
+    else hipLaunchKernelGGL((group_scatter<8>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qs, qp, qshift, Ns, Mq, Gc,
+                            tiles);
     return (int)hipGetLastError();
 }
 
 // Abs: entry prefix state of every range and the segment totals (row G). State (PW, B) with B relative to the last
 // key absorbed: at range g, B <- b_g + B + gap_g PW, PW <- PW + a_g for every slot, slot C included (gap_g = klast_g -
-// klast_{g-1}). A piece composes to  PW = PW_in + sum a,  B = B_in + B_local + (sum of its gaps) PW_in.
-template <int NV, int RK>
+// klast_{g-1}). A piece composes to  PW = PW_in + sum a,  B = B_in + B_local + (sum of its gaps) PW_in. Long segments
+// take two launches over workgroups of SCAN_BLOCK ranges, as the Laplace scan (the record's part 0 holds PW with the
+// gap sum in its link vector, part 1 holds B).
+template <int NV, int RK, int PHASE>
 __global__ __launch_bounds__(SCAN_W * WAVE)
 void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ ta,
-                    float* __restrict__ tb, const int S, const int Ns, const int C, const int G)
+                    float* __restrict__ tb, float* __restrict__ aggs, const int S, const int Ns, const int C,
+                    const int G)
 {
     __shared__ float agg[2][SCAN_W][NV + 1][WAVE];
     __shared__ float span[SCAN_W];
-    const int s = blockIdx.x, w = wave_in_block(), l = lane_id();
+    const int nb = PHASE == 0 ? 1 : scan_blocks(G);
+    const int s = blockIdx.x / nb, blk = blockIdx.x - s * nb;
+    const int w = wave_in_block(), l = lane_id();
     const int CS = range_stride(C);
     const float* SA = sa + (size_t)s * (G + 1) * CS;
     const float* SB = sb + (size_t)s * (G + 1) * CS;
     float* A = ta + (size_t)s * (G + 1) * CS;
     float* B = tb + (size_t)s * (G + 1) * CS;
-    const int per = (G + SCAN_W - 1) / SCAN_W;
-    auto lo_of = [&](int ww) { return min(G, ww * per); };
-    auto hi_of = [&](int ww) { return min(G, ww * per + per); };
-    const int glo = lo_of(w), ghi = hi_of(w);
+    const int b0 = PHASE == 0 ? 0 : blk * SCAN_BLOCK, b1 = PHASE == 0 ? G : min(G, b0 + SCAN_BLOCK);
+    const int per = (b1 - b0 + SCAN_W - 1) / SCAN_W;
+    const int glo = min(b1, b0 + w * per), ghi = min(b1, b0 + w * per + per);
+    float* seg_aggs = PHASE == 0 ? nullptr : aggs + (size_t)s * nb * scan_rec_floats<NV>();
 
     // piece walk from (pw, bb); writes entry states when OUT; returns the sum of the piece's gaps. Slot NV (slot C
     // of the rows) runs the same recurrence: its B state (the v == 1 channel) is weighted by its PW state, the count of
@@ -1065,17 +1246,65 @@ void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
     };
 
     float pw[NV + 1], bb[NV + 1];
+    if constexpr (PHASE <= 1) {
+        // pass 1: every piece from a zero state (empty pieces: all zero)
 #pragma unroll
-    for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
-    const float gs = walk(pw, bb, false);
+        for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
+        const float gs = walk(pw, bb, false);
 #pragma unroll
-    for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = pw[j]; agg[1][w][j][l] = bb[j]; }
-    if (l == 0) span[w] = gs;
+        for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = pw[j]; agg[1][w][j][l] = bb[j]; }
+        if (l == 0) span[w] = gs;
+    }
+    if constexpr (PHASE == 1) {
+        // the wave aggregates, and wave 0 composes the workgroup's from left to right
+        float* rec = seg_aggs + (size_t)blk * scan_rec_floats<NV>();
+        float* w0 = agg_slot<NV>(rec, w, 0);
+        float* w1 = agg_slot<NV>(rec, w, 1);
+#pragma unroll
+        for (int j = 0; j <= NV; ++j) { w0[j * WAVE + l] = pw[j]; w1[j * WAVE + l] = bb[j]; }
+        __syncthreads();
+        w0[(NV + 1) * WAVE + l] = span[w];
+        if (w == 0) {
+            float cp[NV + 1], cb[NV + 1], gsum = 0.f;
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) { cp[j] = 0.f; cb[j] = 0.f; }
+            for (int ww = 0; ww < SCAN_W; ++ww) {
+                const float sp = span[ww];
+#pragma unroll
+                for (int j = 0; j <= NV; ++j) { cb[j] += agg[1][ww][j][l] + sp * cp[j]; cp[j] += agg[0][ww][j][l]; }
+                gsum += sp;
+            }
+            float* b0_ = agg_slot<NV>(rec, SCAN_W, 0);
+            float* b1_ = agg_slot<NV>(rec, SCAN_W, 1);
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) { b0_[j * WAVE + l] = cp[j]; b1_[j * WAVE + l] = cb[j]; }
+            b0_[(NV + 1) * WAVE + l] = gsum;
+        }
+        return;
+    }
+    if constexpr (PHASE == 2) {
+        // this workgroup's wave aggregates, from phase 1
+        const float* rec = seg_aggs + (size_t)blk * scan_rec_floats<NV>();
+        const float* w0 = agg_slot<NV>(const_cast<float*>(rec), w, 0);
+        const float* w1 = agg_slot<NV>(const_cast<float*>(rec), w, 1);
+#pragma unroll
+        for (int j = 0; j <= NV; ++j) { agg[0][w][j][l] = w0[j * WAVE + l]; agg[1][w][j][l] = w1[j * WAVE + l]; }
+        if (l == 0) span[w] = w0[(NV + 1) * WAVE];
+    }
     __syncthreads();
 
-    // incoming state: compose the aggregates of the pieces to the left (empty pieces: all zero)
+    // incoming state: the workgroups before this one, then its waves before this wave
 #pragma unroll
     for (int j = 0; j <= NV; ++j) { pw[j] = 0.f; bb[j] = 0.f; }
+    if constexpr (PHASE == 2) {
+        for (int k = 0; k < blk; ++k) {
+            const float* r0 = agg_slot<NV>(seg_aggs + (size_t)k * scan_rec_floats<NV>(), SCAN_W, 0);
+            const float* r1 = agg_slot<NV>(seg_aggs + (size_t)k * scan_rec_floats<NV>(), SCAN_W, 1);
+            const float sp = r0[(NV + 1) * WAVE + l];
+#pragma unroll
+            for (int j = 0; j <= NV; ++j) { bb[j] += r1[j * WAVE + l] + sp * pw[j]; pw[j] += r0[j * WAVE + l]; }
+        }
+    }
     for (int ww = 0; ww < w; ++ww) {
         const float sp = span[ww];
 #pragma unroll
@@ -1401,8 +1630,17 @@ static int abs_prepare_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStre
     }
     {
         StageTimer t("abs_range_scan", st);
-        hipLaunchKernelGGL((abs_range_scan<NV, RK>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
-                           ra.sa, ra.sb, ra.ta, ra.tb, S, a.Ns, a.C, G);
+        const int nb = scan_blocks(G);
+        if (nb <= 1) {
+            hipLaunchKernelGGL((abs_range_scan<NV, RK, 0>), dim3(S), dim3(SCAN_W * WAVE), 0, st,
+                               ra.sa, ra.sb, ra.ta, ra.tb, nullptr, S, a.Ns, a.C, G);
+        } else {
+            if (ra.aggs == nullptr) return (int)hipErrorInvalidValue;
+            hipLaunchKernelGGL((abs_range_scan<NV, RK, 1>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st,
+                               ra.sa, ra.sb, ra.ta, ra.tb, ra.aggs, S, a.Ns, a.C, G);
+            hipLaunchKernelGGL((abs_range_scan<NV, RK, 2>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st,
+                               ra.sa, ra.sb, ra.ta, ra.tb, ra.aggs, S, a.Ns, a.C, G);
+        }
     }
     return (int)hipGetLastError();
 }

@@ -10,7 +10,10 @@ becomes the key mask of every attention layer (inside the sums for the additive 
 pareto.py's per-sequence RoPE base (an embedding-quality fix) does not change the work and is left out.
 
     python -m qlka.harness [--kernel add_bump] [--seq_len 8192] [--batch_size 16] [--docs 32] [--layers 12]
+                           [--ws_budget_gb 4]
 
+The library's workspace budget (qlka_set_workspace_budget) is set for the run (default 4 GB): every attention call
+then runs its B * heads p in chunks whose workspace stays within it, which bounds the model's peak memory.
 Prints one JSON line: ms_per_doc, peak_mem_gb and the configuration.
 """
 
@@ -61,8 +64,18 @@ def encode_time(model, batches):
     return gpu_ms, torch.cat(pooled)
 
 
-def run(kernel="add_bump", seq_len=8192, batch_size=16, docs=32, layers=12, device="cuda:0", **model_kw):
+def run(kernel="add_bump", seq_len=8192, batch_size=16, docs=32, layers=12, device="cuda:0", ws_budget_gb=4.0,
+        **model_kw):
     device = torch.device(device)
+    from . import _lib
+    prev = _lib.load().qlka_set_workspace_budget(int(ws_budget_gb * 1e9))
+    try:
+        return _run(kernel, seq_len, batch_size, docs, layers, device, ws_budget_gb, **model_kw)
+    finally:
+        _lib.load().qlka_set_workspace_budget(prev)
+
+
+def _run(kernel, seq_len, batch_size, docs, layers, device, ws_budget_gb, **model_kw):
     model = build_encoder(layers, kernel, device, max_positions=seq_len, **model_kw)
     if seq_len > model.config.max_position_embeddings:
         raise ValueError(f"seq_len {seq_len} exceeds the encoder's {model.config.max_position_embeddings} positions")
@@ -75,7 +88,7 @@ def run(kernel="add_bump", seq_len=8192, batch_size=16, docs=32, layers=12, devi
     return {"kernel": kernel, "seq_len": seq_len, "batch_size": batch_size, "num_docs": docs, "layers": layers,
             "hidden": model.config.hidden_size, "heads": model.config.num_attention_heads,
             "ms_per_doc": round(gpu_ms / docs, 3), "gpu_s": round(gpu_ms / 1000, 3),
-            "peak_mem_gb": round(torch.cuda.max_memory_allocated(device) / 1e9, 2),
+            "peak_mem_gb": round(torch.cuda.max_memory_allocated(device) / 1e9, 2), "ws_budget_gb": ws_budget_gb,
             "weights": "random (NomicBertConfig defaults)", "data": "synthetic token ids, padded"}
 
 
@@ -86,8 +99,10 @@ def main(argv=None):
     ap.add_argument("--batch_size", type=int, default=16)
     ap.add_argument("--docs", type=int, default=32)
     ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--ws_budget_gb", type=float, default=4.0)
     a = ap.parse_args(argv)
-    print(json.dumps(run(a.kernel, a.seq_len, a.batch_size, a.docs, a.layers)), flush=True)
+    print(json.dumps(run(a.kernel, a.seq_len, a.batch_size, a.docs, a.layers, ws_budget_gb=a.ws_budget_gb)),
+          flush=True)
 
 
 if __name__ == "__main__":
