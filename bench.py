@@ -259,6 +259,9 @@ def main():
     ap.add_argument("--ws-budget-gib", type=float, default=None,
                     help="libqlka workspace budget (qlka_set_workspace_budget) for every timed call, in GiB; "
                          "default: the library's")
+    ap.add_argument("--op", choices=("laplace", "abs"), default=None,
+                    help="only run --warmup + --steps calls of this one headline op and print the call count (for "
+                         "per-op rocprofv3 counter runs: traffic per call = the sum over its dispatches / calls)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -297,6 +300,15 @@ def main():
     def step():
         weighted_laplace_sum(q, k, v)
         weighted_abs_sum_full(q, k, v, backend="cuda")
+
+    if args.op is not None:
+        fn = (lambda: weighted_laplace_sum(q, k, v)) if args.op == "laplace" else \
+            (lambda: weighted_abs_sum_full(q, k, v, backend="cuda"))
+        for _ in range(args.warmup + args.steps):
+            fn()
+        torch.cuda.synchronize()
+        print(json.dumps({"op": args.op, "calls": args.warmup + args.steps}), flush=True)
+        return
 
     for _ in range(args.warmup):
         step()
