@@ -87,10 +87,39 @@ def config_inputs(c, dev, seed=0):
     return q, k, v, g_w, g_u
 
 
-def config_timings(dev, reps=3, only=None):
-    """ms per call of each configuration's workload (median of reps after one warmup); only: one config index."""
+FP32_PEAK_TFLOPS = 157.3     # MI355X dense fp32 (matrix and vector with packed math)
+
+
+def dense_flops(i, c):
+    """Algorithmic flops of configuration i's workload on the dense route (configs[0], [1]): forming
+    A[m, n] = sum_d f(q_d - k_d) costs a subtract and an add per (m, n, d) (|x| is a free operand modifier) plus the
+    exponential for the Laplace kernel, the contraction A^T [v, 1] 2 (C + 1) per (m, n); each sign sum of the backward
+    forms G = X Y^T (2 C per (i, j)) and adds a selected +-G per (d, i, j) (2); grad_v is the forward with q and k
+    swapped (no row sums)."""
+    P, D, N, C = c["P"], c["D"], c["N"], c["C"]
+    M = N
+    fwd_abs = 2.0 * P * M * N * D + 2.0 * P * M * N * (C + 1)
+    if i == 0:
+        sign = 2.0 * P * M * N * C + 2.0 * P * D * M * N
+        grad_v = 2.0 * P * M * N * D + 2.0 * P * M * N * C
+        return fwd_abs + 2 * sign + grad_v
+    if i == 1:
+        fwd_lap = 3.0 * P * M * N * D + 2.0 * P * M * N * (C + 1)
+        return fwd_lap + fwd_abs
+    return None
+
+
+def config_timings(dev, reps=None, only=None):
+    """ms per call of each configuration's workload: the mean over `reps` calls (default 20; 3 for configs[4]), each
+    bracketed by events after a synchronisation, following warmup calls (5; 1 for configs[4]), as the reference's
+    speed bench times a step (Experiments/speed_and_memory/bench.py:106-118). For the dense-route configurations [0]
+    and [1] also the library kernels' own time per call (libqlka's stage timer, a separate pass), the share of the
+    call that is not kernel time (`host_frac`) and the flop rate against the fp32 peak (`flop_frac`, over the whole
+    call; `flop_frac_kernels` over the kernels' time). only: one config index."""
+    from qlka import _lib
     from weighted_abs_sum import weighted_abs_sum_full
     from weighted_laplace_sum import weighted_laplace_sum
+    lib = _lib.load()
     out = {}
     for i, c in CONFIGS.items():
         if only is not None and i != only:
@@ -115,9 +144,11 @@ def config_timings(dev, reps=3, only=None):
             def fn():
                 fwd_bwd()
                 weighted_laplace_sum(q, k, v)
-        fn()
+        n_rep = reps or (3 if i == 4 else 20)
+        for _ in range(1 if i == 4 else 5):
+            fn()
         ts = []
-        for _ in range(reps):
+        for _ in range(n_rep):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             e0.record()
@@ -125,8 +156,23 @@ def config_timings(dev, reps=3, only=None):
             e1.record()
             torch.cuda.synchronize()
             ts.append(e0.elapsed_time(e1))
-        out[f"configs[{i}]"] = {"ms": round(statistics.median(ts), 4), "work": c["work"],
-                                "shape": f"P={c['P']} D={c['D']} N=M={c['N']} C={c['C']}"}
+        ms = statistics.fmean(ts)
+        entry = {"ms": round(ms, 4), "ms_median": round(statistics.median(ts), 4), "calls": n_rep,
+                 "work": c["work"], "shape": f"P={c['P']} D={c['D']} N=M={c['N']} C={c['C']}"}
+        flops = dense_flops(i, c)
+        if flops is not None:
+            lib.qlka_timing_reset()
+            lib.qlka_timing_enable(1)
+            for _ in range(n_rep):
+                fn()
+            torch.cuda.synchronize()
+            lib.qlka_timing_enable(0)
+            kms = sum(_lib.stage_time(name)[0] for name in STAGES + DENSE_STAGES) / n_rep
+            entry.update({"kernel_ms": round(kms, 4), "host_frac": round(max(ms - kms, 0.0) / ms, 4),
+                          "gflop": round(flops / 1e9, 3), "flop_peak_tflops": FP32_PEAK_TFLOPS,
+                          "flop_frac": round(flops / (ms / 1e3) / 1e12 / FP32_PEAK_TFLOPS, 4),
+                          "flop_frac_kernels": round(flops / (kms / 1e3) / 1e12 / FP32_PEAK_TFLOPS, 4)})
+        out[f"configs[{i}]"] = entry
         del q, k, v, g_w, g_u
         torch.cuda.empty_cache()
     return out
@@ -175,6 +221,7 @@ def _cpu_model():
 STAGES = ("lds_radix_sort", "merge_runs", "group_queries", "query_bounds", "fill_zero", "lap_range_sums",
           "lap_range_scan", "lap_range_walk", "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_to_query",
           "u_sum", "slab_reduce")
+DENSE_STAGES = ("direct_fwd", "direct_sign")
 
 
 def kernel_algorithmic_bytes(name):

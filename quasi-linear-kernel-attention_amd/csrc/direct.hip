@@ -172,12 +172,15 @@ void direct_fwd_small_kernel(const float* __restrict__ q, const float* __restric
 
 // Longer segments: one workgroup of 256 threads per (p, tile of IT queries) walks the keys in tiles of 64. Per key
 // tile and 64-feature chunk the k values ([d][n]) come from registers loaded during the previous step, and each thread
-// adds the chunk to its 4-key x (IT / 16)-query block of A; after the last chunk the A tile goes to LDS ([n][m], zero
-// at keys past N) and each thread adds A^T v to its 2-query x 4-channel blocks (and the row sums), with the tile's v
-// rows, loaded while A was formed, in LDS ([n][c]). IT = 64 for C <= 32 (CM = 32), else 32 (CM = 64 or 128), so that
-// the blocks of A and of A^T v are (a multiple of) one per thread. Staging as in the tiled sign sums: raw buffer
-// descriptors that end at the segment's end (rows past it read 0), fixed LDS row strides; columns past the tile (keys
-// past N, queries past M, channels past C) may read the next row and never reach an output or A.
+// adds the chunk to its 4-key x (IT / 16)-query block of A on the VALU; after the last chunk the A tile goes to LDS
+// ([n][m], zero at keys past N) and the contraction A^T [v, 1] runs on the matrix cores: the IT x CM output tile is
+// 16 x 16 blocks, each wave owns BW of them (one query block, BW channel blocks) and adds the tile's 64 keys to them
+// with 16 v_mfma_f32_16x16x4_f32 per block (fp32 products and sums, as the VALU form), the tile's v rows, loaded while
+// A was formed, in LDS ([n][c]). The waves whose first channel block is 0 also run one MFMA per step against a
+// column of ones: the row sums out_u. IT = 64 for C <= 32 (CM = 32), else 32 (CM = 64 or 128). Staging as in the
+// tiled sign sums: raw buffer descriptors that end at the segment's end (rows past it read 0), fixed LDS row strides;
+// columns past the tile (keys past N, queries past M, channels past C) may read the next row and never reach an
+// output or A (an MFMA output column depends only on its own column of v).
 template <int KIND, int IT, int CM>
 __global__ __launch_bounds__(ST_T)
 void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
@@ -188,7 +191,8 @@ void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restric
     constexpr int QM = IT / 16;                           // queries per thread in the A phase (4 keys x QM)
     constexpr int KS = ST_JT + 4, VS = CM + 4;            // LDS row strides
     constexpr int KK = ST_JT / 4, KV = CM / 4, KQ = IT / 4;   // staged elements per thread (4 threads per row)
-    constexpr int NAV = (IT / 2) * (CM / 4) / ST_T;       // A^T v blocks per thread (1 or 2)
+    constexpr int NBC = CM / 16, BW = (IT / 16) * NBC / 4;   // 16-channel blocks; 16 x 16 output blocks per wave
+    static_assert(BW >= 1 && NBC % BW == 0, "a wave's output blocks share one query block");
     __shared__ float qs[DCK * IT];                        // [d][m]
     __shared__ float ks[DCK * KS];                        // [d][n]
     __shared__ float vs[ST_JT * VS];                      // [n][c]
@@ -223,17 +227,17 @@ void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restric
     load_v(0);
     if (chunks == 1) stage_q(0);
     const int an = (tid / (IT / QM)) * 4, am = (tid - (tid / (IT / QM)) * (IT / QM)) * QM;   // A block
-    float a[4][QM], acc[NAV][2][4], us[2] = {0.f, 0.f};
+    const int wv = wave_in_block(), ln = lane_id();
+    const int mi = (wv * BW) / NBC, cb0 = (wv * BW) % NBC;  // this wave's query block and first channel block
+    const bool uw = cb0 == 0;                              // it also forms the row sums
+    float a[4][QM];
+    f4_t acc[BW], accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int u = 0; u < QM; ++u) a[r][u] = 0.f;
 #pragma unroll
-    for (int w = 0; w < NAV; ++w)
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[w][u][c] = 0.f;
+    for (int t = 0; t < BW; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < steps; ++s) {
         const int t = s / chunks, h = s - t * chunks, n0 = t * ST_JT, d0 = h * DCK;
         __syncthreads();                                  // readers of ks (and of vs / At / qs) are done
@@ -279,35 +283,31 @@ void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restric
                 a[r][u] = 0.f;
             }
         __syncthreads();
-#pragma unroll
-        for (int w = 0; w < NAV; ++w) {
-            const int tv = tid + w * ST_T, c0 = (tv / (IT / 2)) * 4, m0 = (tv - (tv / (IT / 2)) * (IT / 2)) * 2;
+        // A^T [v, 1] on the matrix cores: lane ln supplies A^T[m][n] and v[n][c] at m, c = block base + ln % 16,
+        // n = 4 kk + ln / 16 (keys past N: A = 0 and v = 0)
+        const float* Ap = At + (ln >> 4) * IT + mi * 16 + (ln & 15);
+        const float* Vp = vs + (ln >> 4) * VS + cb0 * 16 + (ln & 15);
 #pragma unroll 4
-            for (int n = 0; n < Nl; ++n) {
-                const f2_t ar = *reinterpret_cast<const f2_t*>(At + n * IT + m0);
-                const f4_t vr = *reinterpret_cast<const f4_t*>(vs + n * VS + c0);
+        for (int kk = 0; kk < ST_JT / 4; ++kk) {
+            const float av = Ap[kk * 4 * IT];
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    if (w == 0) us[u] += ar[u];
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) acc[w][u][c] += ar[u] * vr[c];
-                }
-            }
+            for (int t = 0; t < BW; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, Vp[kk * 4 * VS + t * 16], acc[t], 0, 0, 0);
+            if (uw) accu = __builtin_amdgcn_mfma_f32_16x16x4f32(av, 1.f, accu, 0, 0, 0);
         }
     }
+    // lane ln holds rows m = 16 mi + 4 (ln / 16) + r, r < 4, of column ln % 16 of each of its blocks
 #pragma unroll
-    for (int w = 0; w < NAV; ++w) {
-        const int tv = tid + w * ST_T, c0 = (tv / (IT / 2)) * 4, m0 = (tv - (tv / (IT / 2)) * (IT / 2)) * 2;
+    for (int r = 0; r < 4; ++r) {
+        const int m = mi * 16 + 4 * (ln >> 4) + r;
+        if (m >= Ml) continue;
+        float* o = out_w + ((size_t)p * M + mb + m) * C;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int m = m0 + u;
-            if (m >= Ml) continue;
-            float* o = out_w + ((size_t)p * M + mb + m) * C;
-#pragma unroll
-            for (int c = 0; c < 4; ++c)
-                if (c0 + c < C) o[c0 + c] = acc[w][u][c];
-            if (w == 0 && c0 == 0 && out_u != nullptr) out_u[(size_t)p * M + mb + m] = us[u];
+        for (int t = 0; t < BW; ++t) {
+            const int c = (cb0 + t) * 16 + (ln & 15);
+            if (c < C) o[c] = acc[t][r];
         }
+        if (uw && (ln & 15) == 0 && out_u != nullptr) out_u[(size_t)p * M + mb + m] = accu[r];
     }
 }
 
@@ -518,8 +518,9 @@ static bool sign_small_fits(int D, int I, int J, int C) {
 
 // Longer segments: one workgroup of 256 threads per (p, tile of IT outputs) walks the j in tiles of 64. The x rows
 // of the tile sit in LDS feature-major for the whole walk; per j tile the y rows ([j][c]), the b values of a chunk of
-// DCM features ([d][j]) and g_u come from registers loaded during the previous tile, G[j][i] (zero at padded i, j) is
-// formed 4 j x 2 i per thread from four-float reads, and each thread adds 64 j to its block of 4 features x 2 outputs
+// DCM features ([d][j]) and g_u come from registers loaded during the previous tile, G[j][i] = <x_i, y_j> (+ g_u, zero
+// at padded i, j) is formed on the matrix cores (v_mfma_f32_16x16x4_f32, one 16-j block per wave, fp32 products and
+// sums) and stored to LDS, and each thread adds 64 j to its block of 4 features x 2 outputs
 // with the same sign step as the small kernel. IT = 32 (DCM = 64) in general, IT = 64 (DCM = 32) for D <= 32, so that
 // the 256 blocks of a feature chunk are one per thread; more features take further chunks (G formed again per chunk).
 // Staging: each thread owns one row of a tile and loads its columns part, part + TPR, ... through a raw buffer
@@ -534,6 +535,7 @@ void direct_sign_tiled_kernel(const float* __restrict__ a, const float* __restri
                               const float tie, const float scale, const int D, const int I, const int J, const int C,
                               const int itiles)
 {
+    static_assert(ST_JT / 16 == ST_T / WAVE, "one 16-j block of G per wave");
     constexpr int DCM = 2048 / IT;                        // features per chunk
     constexpr int NI2 = IT / 2;                           // output pairs per tile
     constexpr int YS = CM + 4, BS = ST_JT + 4;            // LDS row strides of y and b
@@ -605,33 +607,32 @@ void direct_sign_tiled_kernel(const float* __restrict__ a, const float* __restri
         if (s + 1 < steps) load_step(s + 1);
         __syncthreads();
         const int Jl = min(ST_JT, J - j0);
-        for (int t = tid; t < (ST_JT / 4) * NI2; t += ST_T) {
-            const int jq = (t / NI2) * 4, ip = (t - (t / NI2) * NI2) * 2;
-            float g[4][2];
+        {
+            // G = Y X^T on the matrix cores: wave w owns the 16 j of block w and all IT / 16 blocks of i; lane ln
+            // supplies y[j][c] and x[i][c] at j, i = block base + ln % 16, c = 4 kk + ln / 16 (columns C .. Cp-1 of
+            // xs and ys are 0)
+            const int wv = wave_in_block(), ln = lane_id();
+            const float* Yp = ys + (wv * 16 + (ln & 15)) * YS + (ln >> 4);
+            const float* Xp = xs + (ln >> 4) * IT + (ln & 15);
+            f4_t g[IT / 16];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) { g[u][0] = 0.f; g[u][1] = 0.f; }
-            for (int c = 0; c < Cp; c += 4) {             // columns C .. Cp-1 of xs are 0
-                f4_t yr[4];
-                f2_t xr[4];
+            for (int t = 0; t < IT / 16; ++t) g[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+            for (int kk = 0; kk < Cp / 4; ++kk) {
+                const float yv_ = Yp[kk * 4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) yr[u] = *reinterpret_cast<const f4_t*>(ys + (jq + u) * YS + c);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) xr[k] = *reinterpret_cast<const f2_t*>(xs + (c + k) * IT + ip);
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) { g[u][0] += yr[u][k] * xr[k][0]; g[u][1] += yr[u][k] * xr[k][1]; }
+                for (int t = 0; t < IT / 16; ++t)
+                    g[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(yv_, Xp[kk * 4 * IT + t * 16], g[t], 0, 0, 0);
             }
+            // lane ln holds rows j = 16 wv + 4 (ln / 16) + r of column i = 16 t + ln % 16 of each block
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int j = jq + u;
-                f2_t row;
+            for (int t = 0; t < IT / 16; ++t) {
+                const int i = t * 16 + (ln & 15);
 #pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const int i = ip + q;
-                    row[q] = (i < Il && j < Jl) ? g[u][q] + (GU_OWN ? gi[i] : gj[j]) : 0.f;
+                for (int r = 0; r < 4; ++r) {
+                    const int j = wv * 16 + 4 * (ln >> 4) + r;
+                    G[j * IT + i] = (i < Il && j < Jl) ? g[t][r] + (GU_OWN ? gi[i] : gj[j]) : 0.f;
                 }
-                *reinterpret_cast<f2_t*>(G + j * IT + ip) = row;
             }
         }
         __syncthreads();
