@@ -1,16 +1,20 @@
-"""ctypes binding of libqlka.so (the C ABI declared in include/qlka.h).
+"""Loading of libqlka.so (the C ABI declared in include/qlka.h): a ctypes binding, and the PyTorch C++ extension
+_qlka_torch.so built over the same library (the operators' entry points and autograd).
 
 PyTorch is only plumbing here: it owns device memory (outputs and workspace come from its caching allocator) and the
 current stream; every computation runs in the HIP kernels of libqlka.so. There is no CPU or PyTorch fallback: if the
-library is missing or cannot be loaded, loading raises.
+library or the extension is missing or cannot be loaded, loading raises.
 """
 
 import ctypes
+import importlib.machinery
+import importlib.util
 import os
 
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libqlka.so")
+EXT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_qlka_torch.so")
 
 _c_int = ctypes.c_int
 _c_size = ctypes.c_size_t
@@ -69,6 +73,26 @@ def load():
             fn.argtypes = args
         _lib = lib
     return _lib
+
+
+_ext = None
+
+
+def torch_ext():
+    """Import the in-tree _qlka_torch.so once (after libqlka.so, which it links) and return the module."""
+    global _ext
+    if _ext is None:
+        load()
+        if not os.path.exists(EXT_PATH):
+            raise RuntimeError(
+                f"_qlka_torch.so not found at {EXT_PATH}; build it with "
+                "`python quasi-linear-kernel-attention_amd/qlka/build.py`")
+        loader = importlib.machinery.ExtensionFileLoader("_qlka_torch", EXT_PATH)
+        spec = importlib.util.spec_from_file_location("_qlka_torch", EXT_PATH, loader=loader)
+        mod = importlib.util.module_from_spec(spec)
+        loader.exec_module(mod)
+        _ext = mod
+    return _ext
 
 
 def check(rc):

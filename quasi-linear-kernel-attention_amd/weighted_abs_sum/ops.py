@@ -17,7 +17,7 @@ import torch
 from weighted_abs_sum import _ext as _C
 
 _BACKENDS = ("auto", "keops", "cuda", "cuda-fused", "cuda-global")
-_DIRECT = "direct"      # forward of the keops route: dense evaluation
+_DIRECT = 2             # the keops route: dense evaluation (the extension's DIRECT path code)
 _PATH = {"cuda": -1, "cuda-fused": 1, "cuda-global": 0, "keops": _DIRECT}
 
 # "auto" uses the keops route strictly below this max(N,M)
@@ -55,61 +55,16 @@ def _resolve(backend, q, k, v):
     return "cuda"
 
 
-def _forward(ctx, q, k, v, path, full):
-    """Shared forward of the two Functions: the dense route for "keops", else the native ops, keeping the sorts
-    for the backward when a gradient is wanted and KEEP_SORTS is set."""
-    if path == _DIRECT:
-        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
-    ctx.set_materialize_grads(False)
-    ctx.direct = path == _DIRECT
-    srt = None
-    if ctx.direct:
-        out, out_u = _C.weighted_abs_sum_direct_forward(q, k, v, full=full)
-    elif KEEP_SORTS and any(ctx.needs_input_grad[:3]):
-        out, out_u, srt = _C.weighted_abs_sum_forward_keep(q, k, v, path, full)
-    elif full:
-        out, out_u = _C.weighted_abs_sum_full_forward(q, k, v, path)
-    else:
-        out, out_u = _C.weighted_abs_sum_forward(q, k, v, path), None
-    ctx.sorted = srt is not None
-    ctx.save_for_backward(q, k, v, *(srt or ()))
-    return out, out_u
+def _keep(q, k, v):
+    """Keep the forward's sorts: KEEP_SORTS and a gradient will be wanted from this call."""
+    return KEEP_SORTS and torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
 
 
-def _backward(ctx, g_w, g_u):
-    q, k, v = ctx.saved_tensors[:3]
-    if ctx.direct:          # the KeOps gradient: sign(0) = 0
-        return _C.weighted_abs_sum_direct_backward(q, k, v, g_w, g_u, tie=0.0)
-    if ctx.sorted:
-        return _C.weighted_abs_sum_backward_sorted(q, k, v, g_w, g_u, ctx.saved_tensors[3:])
-    if g_u is None:         # out_u unused -> the cheaper plain backward
-        return _C.weighted_abs_sum_backward(q, k, v, g_w)
-    return _C.weighted_abs_sum_full_backward(q, k, v, g_w, g_u)
-
-
-class _WeightedAbsSum(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, v, path):
-        return _forward(ctx, q, k, v, path, full=False)[0]
-
-    @staticmethod
-    def backward(ctx, g_w):
-        grad_q, grad_k, grad_v = _backward(ctx, g_w.contiguous(), None)
-        return grad_q, grad_k, grad_v, None
-
-
-class _WeightedAbsSumFull(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, v, path):
-        return _forward(ctx, q, k, v, path, full=True)
-
-    @staticmethod
-    def backward(ctx, g_w, g_u):
-        q, v = ctx.saved_tensors[0], ctx.saved_tensors[2]
-        if g_w is None:
-            g_w = torch.zeros(q.shape[0], q.shape[2], v.shape[2], device=q.device, dtype=q.dtype)
-        grad_q, grad_k, grad_v = _backward(ctx, g_w.contiguous(), None if g_u is None else g_u.contiguous())
-        return grad_q, grad_k, grad_v, None
+# The two differentiable ops are one C++ autograd Function of the extension (csrc/torch_ext.cpp, AbsSumFn), the
+# counterpart of the reference's _WeightedAbsSum / _WeightedAbsSumFull (ops.py:72-104): its forward runs the dense
+# route for "keops" (on contiguous copies) or the native ops, keeping the sorted k and q for the backward when asked;
+# its backward is the dense gradient with sign(0) = 0 for "keops", else the native backward over the kept sorts
+# (or sorting again), the plain one when out_u gets no gradient. Neither direction runs Python.
 
 
 def weighted_abs_sum(q, k, v, backend="auto"):
@@ -118,7 +73,7 @@ def weighted_abs_sum(q, k, v, backend="auto"):
     q: (P, D, M), k: (P, D, N), v: (P, N, C) -> (P, M, C). Differentiable.
     """
     b = _resolve(backend, q, k, v)
-    return _WeightedAbsSum.apply(q, k, v, _PATH[b])
+    return _C.abs_sum_autograd(q, k, v, _PATH[b], False, _keep(q, k, v))[0]
 
 
 def weighted_abs_sum_full(q, k, v, backend="auto"):
@@ -126,7 +81,8 @@ def weighted_abs_sum_full(q, k, v, backend="auto"):
     out_u[p,m] = sum_{n,d} |k[p,d,n] - q[p,d,m]| (P, M), from one pass. Differentiable in both outputs.
     """
     b = _resolve(backend, q, k, v)
-    return _WeightedAbsSumFull.apply(q, k, v, _PATH[b])
+    out_w, out_u = _C.abs_sum_autograd(q, k, v, _PATH[b], True, _keep(q, k, v))
+    return out_w, out_u
 
 
 def weighted_sgn_sum(q, k, v, g, backend="auto"):

@@ -1,7 +1,7 @@
 """MI355X drop-in for the reference's weighted_laplace_sum package
 (Weighted_Laplace_Sum/weighted_laplace_sum/__init__.py:1-16)."""
 
-from ._ext import weighted_laplace_sum_forward as _forward
+from . import _ext
 
 
 def weighted_laplace_sum(q, k, v):
@@ -13,7 +13,7 @@ def weighted_laplace_sum(q, k, v):
         out_u[p, m]    = sum_{d, n} exp(-|k[p, d, n] - q[p, d, m]|)                 (P, M)
     No autograd. Padded keys: zero k and v there and subtract n_pad * sum_d exp(-|q_d|) from out_u.
     """
-    return _forward(q, k, v)
+    return _ext.weighted_laplace_sum_forward(q, k, v)
 
 
 __all__ = ["weighted_laplace_sum"]

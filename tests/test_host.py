@@ -54,3 +54,22 @@ def test_cpu_tensors_raise_reference_messages():
         weighted_abs_sum.weighted_sgn_sum(q, q, v, torch.zeros(1, 4, 3))
     with pytest.raises(RuntimeError, match="q, k and v must be CUDA tensors"):
         weighted_laplace_sum.weighted_laplace_sum(q, q, v)
+
+
+def test_torch_extension_is_the_boundary():
+    """The drop-in packages' entry points are the C++ extension's (no Python in the call or its backward): every
+    name of the reference's pybind modules and the differentiable op resolve to _qlka_torch.so built in-tree."""
+    from qlka import _lib
+    import weighted_laplace_sum._ext as lext
+    ext = _lib.torch_ext()
+    assert ext.__file__ == _lib.EXT_PATH
+    for name in _ext._NAMES:
+        assert getattr(_ext, name) is getattr(ext, name)
+    assert lext.weighted_laplace_sum_forward is ext.weighted_laplace_sum_forward
+    assert ops._DIRECT == ext.DIRECT
+    # errors from C++ keep the reference's types and texts, also for the shape and argument checks
+    q = torch.zeros(1, 2, 4)
+    with pytest.raises(RuntimeError, match="q, k, and v must be CUDA tensors"):
+        ext.abs_sum_autograd(q, q, torch.zeros(1, 4, 3), -1, True, False)
+    with pytest.raises(TypeError):
+        ext.weighted_abs_sum_forward(q, q)
