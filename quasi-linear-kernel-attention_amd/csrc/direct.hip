@@ -529,7 +529,8 @@ static bool sign_small_fits(int D, int I, int J, int C) {
 // so stores need no bounds. Columns of b past J read the next row: harmless, as G is 0 there and the sign step selects
 // rather than multiplies.
 template <bool GU_OWN, int TIE, int IT, int CM>      // CM: padded C at most (64 or 128)
-__global__ __launch_bounds__(ST_T)
+// grad_k's variant (GU_OWN false) is held to 168 VGPRs, 3 waves per SIMD (left alone it takes 172, 2 waves, 30% slower)
+__global__ __launch_bounds__(ST_T) __attribute__((amdgpu_waves_per_eu(GU_OWN ? 1 : 3)))
 void direct_sign_tiled_kernel(const float* __restrict__ a, const float* __restrict__ b, const float* __restrict__ x,
                               const float* __restrict__ y, const float* __restrict__ gu, float* __restrict__ out,
                               const float tie, const float scale, const int D, const int I, const int J, const int C,
