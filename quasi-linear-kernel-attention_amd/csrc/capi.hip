@@ -272,9 +272,15 @@ size_t plan_bytes(const Plan& pl, Bytes bytes1) { return (size_t)pl.nbuf * bytes
 // the per-chunk launch tails outweigh the overlap).
 inline bool pipelined(int P, int D, int M) { return P >= 2 && (int64_t)P * D * M >= (int64_t(1) << 22); }
 
-// prep / main / back: int(p0, np, buf, stream) for the chunk [p0, p0 + np) over workspace copy `buf`.
-template <class Prep, class Main, class Back>
-int run_pipeline(int P, const Plan& pl, void* ws, size_t copy, hipStream_t st, Prep prep, Main main, Back back) {
+// prep / main / back: int(p0, np, buf, stream) for the chunk [p0, p0 + np) over workspace copy `buf`. `early`, the
+// same, runs after prep and before main's wait for the previous chunk's reduce: the part of main that may share the
+// GPU with that reduce (add_bump's range passes beside its three-slab reduce, 0.55 ms: 4.43 -> 4.42 ms; making that
+// reduce wait for the next chunk's sort, which it slows from 0.12 to 0.64 ms, cost 0.1 ms instead).
+inline int no_early(int, int, void*, hipStream_t) { return QLKA_OK; }
+
+template <class Prep, class Main, class Back, class Early = decltype(&no_early)>
+int run_pipeline(int P, const Plan& pl, void* ws, size_t copy, hipStream_t st, Prep prep, Main main, Back back,
+                 Early early = &no_early) {
     SideStream* sd = nullptr;
     if (pl.nbuf == 2 && (P + pl.pc - 1) / pl.pc > 1) {
         if (hipError_t e = side_stream(st, &sd)) return hip_status((int)e, "side stream");
@@ -282,6 +288,7 @@ int run_pipeline(int P, const Plan& pl, void* ws, size_t copy, hipStream_t st, P
     if (sd == nullptr) {
         return for_chunks(P, pl.pc, [&](int p0, int np) {
             if (int e = prep(p0, np, ws, st)) return e;
+            if (int e = early(p0, np, ws, st)) return e;
             if (int e = main(p0, np, ws, st)) return e;
             return back(p0, np, ws, st); });
     }
@@ -294,6 +301,7 @@ int run_pipeline(int P, const Plan& pl, void* ws, size_t copy, hipStream_t st, P
         void* buf = (char*)ws + (size_t)(j % 2) * copy;
         if (j >= 2) err = hipc(hipStreamWaitEvent(st, sd->reduced[j % 2], 0), "pipeline");
         if (!err) err = prep(p0, np, buf, st);
+        if (!err) err = early(p0, np, buf, st);
         if (!err && j >= 1) err = hipc(hipStreamWaitEvent(st, sd->reduced[(j - 1) % 2], 0), "pipeline");
         if (!err) err = main(p0, np, buf, st);
         if (!err) err = hipc(hipEventRecord(sd->walked, st), "pipeline");
@@ -866,6 +874,25 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
             return e;
         return group_q(qc, L.op, 0.f, np * D, N, M, C, s);
     };
+    // the abs walk's arguments of a chunk (add_riesz, add_bump)
+    auto abs_args = [&](const SortedWs& w, const float* vc, const uint8_t* keepc, int np) {
+        AbsWalkArgs a{};
+        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = vc; a.u = nullptr; a.keep = keepc;
+        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
+        a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
+        a.out_dot = nullptr; a.out_rank = nullptr;
+        a.sign = 1.f; a.P = np; a.D = D; a.C = C; a.qshift = 0.f;
+        return a;
+    };
+    const int abs_mode = ABS_ROW | ABS_ONES | (masked ? ABS_KEEP : 0);
+    // add_bump: the range passes beside the previous chunk's reduce
+    auto early = [&](int p0, int np, void* buf, hipStream_t s) {
+        if (!bump) return (int)QLKA_OK;
+        const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
+        chunk_in(p0, qc, kc, vc, npc, keepc, outc);
+        LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
+        return hip_status(abs_prepare(abs_args(L.op, vc, keepc, np), abs_mode, L.op.ra, s), "abs ranges");
+    };
     auto main = [&](int p0, int np, void* buf, hipStream_t s) {
         const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
         chunk_in(p0, qc, kc, vc, npc, keepc, outc);
@@ -878,17 +905,12 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
             order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
             return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
         }
-        AbsWalkArgs a{};
-        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = vc; a.u = nullptr; a.keep = keepc;
-        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
-        a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
-        a.out_dot = nullptr; a.out_rank = nullptr;
-        a.sign = 1.f; a.P = np; a.D = D; a.C = C; a.qshift = 0.f;
-        const int mode = ABS_ROW | ABS_ONES | (masked ? ABS_KEEP : 0);
-        if (int e = abs_prepare(a, mode, w.ra, s)) return hip_status(e, "abs ranges");
-        if (!bump)
+        AbsWalkArgs a = abs_args(w, vc, keepc, np);
+        const int mode = abs_mode;
+        if (!bump) {
+            if (int e = abs_prepare(a, mode, w.ra, s)) return hip_status(e, "abs ranges");
             if (int e = riesz_prefix(kc, vc, keepc, L.pre, np, D, N, C, s)) return hip_status(e, "riesz prefixes");
-        if (bump) {
+        } else {
             a.nsets = 3;
             for (int ev = 1; ev < 3; ++ev) {
                 a.set_shift[ev] = shift[ev];
@@ -898,9 +920,13 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
             }
         }
         if (int e = hip_status(abs_emit(a, mode, w.ra, s), "abs walk")) return e;
-        order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
-        if (bump)
-            for (int ev = 0; ev < 2; ++ev) order_u_terms(L.uslab2[ev], w.qp, L.uq2[ev], np, D, M, s);
+        if (bump) {
+            const float* us[3] = {w.uslab, L.uslab2[0], L.uslab2[1]};
+            float* uqs[3] = {w.uq, L.uq2[0], L.uq2[1]};
+            order_u_terms_sets(us, w.qp, uqs, 3, np, D, M, s);
+        } else {
+            order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
+        }
         return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
     };
     auto back = [&](int p0, int np, void* buf, hipStream_t s) {
@@ -926,7 +952,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         return hip_status(layer_epilogue(kind, masked, qc, npc, L.w[0], L.u[0], nullptr, nullptr, nullptr, nullptr,
                                          L.pre, L.qt, outc, np, D, N, M, C, s), "layer epilogue");
     };
-    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back);
+    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back, early);
 }
 
 int qlka_layer_fwd(int kind, const float* q, const float* k, const float* v, const float* n_pad, float* out,

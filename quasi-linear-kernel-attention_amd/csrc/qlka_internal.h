@@ -118,6 +118,9 @@ int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, f
 // The v == 1 terms in query order: uslab itself when the walks wrote them so, else uq after the transpose through
 // LDS by the permutation qperm (launched on st).
 const float* order_u_terms(const float* uslab, const uint32_t* qperm, float* uq, int P, int D, int M, hipStream_t st);
+// the same for nsets (<= 3) sets of terms sorted alike, in one launch
+void order_u_terms_sets(const float* const* uslab, const uint32_t* qperm, float* const* uq, int nsets, int P, int D,
+                        int M, hipStream_t st);
 
 // Emission modes of the abs-family walk (bit set).
 enum AbsMode : int {

@@ -18,14 +18,19 @@ namespace qlka {
 constexpr int RT = 256;        // threads per block
 
 // uq[s][qperm[s][i]] = uslab[s][i] for every segment s (M <= U_LDS_CAP): one workgroup per segment, through LDS.
+// Up to three sets of terms sorted alike (add_bump's q, q + 1, q - 1) go in one launch: block b does segment b % S
+// of set b / S.
 constexpr int UT_T = 1024;
+struct USets { const float* uslab[3]; float* uq[3]; };
 __global__ __launch_bounds__(UT_T)
-void u_to_query(const float* __restrict__ uslab, const uint32_t* __restrict__ qperm, float* __restrict__ uq,
-                const int M)
+void u_to_query(const USets sets, const uint32_t* __restrict__ qperm, const int S, const int M)
 {
     constexpr int UT_I = U_LDS_CAP / UT_T;          // items per thread; all of a thread's loads are issued at once
     __shared__ float buf[U_LDS_CAP];
-    const size_t base = (size_t)blockIdx.x * M;
+    const int set = blockIdx.x / S, seg = blockIdx.x - set * S;
+    const float* __restrict__ uslab = sets.uslab[set];
+    float* __restrict__ uq = sets.uq[set];
+    const size_t base = (size_t)seg * M;
     const int tid = threadIdx.x;
     float x[UT_I];
     uint32_t dst[UT_I];
@@ -139,8 +144,7 @@ int reduce_slabs(const float* slab, const float* uslab, const uint32_t* qperm, f
     const int cq = C / 4;
     const bool fused_u = out_u && v4 && (cq & (cq - 1)) == 0;     // row lanes aligned within a wave
     if (out_u && qperm && !u_query_order(M)) {
-        StageTimer t("u_to_query", st);
-        hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
+        order_u_terms_sets(&uslab, qperm, &uq, 1, P, D, M, st);
     } else if (out_u) {
         uq = const_cast<float*>(uslab);                   // already in query order
     }
@@ -242,10 +246,19 @@ int reduce_slabs_bump(bool masked, const ReduceEpilogue& ep, const float* const 
 }
 
 const float* order_u_terms(const float* uslab, const uint32_t* qperm, float* uq, int P, int D, int M, hipStream_t st) {
-    if (u_query_order(M)) return uslab;
+    const float* u[1] = {uslab};
+    float* q[1] = {uq};
+    order_u_terms_sets(u, qperm, q, 1, P, D, M, st);
+    return u_query_order(M) ? uslab : uq;
+}
+
+void order_u_terms_sets(const float* const* uslab, const uint32_t* qperm, float* const* uq, int nsets, int P, int D,
+                        int M, hipStream_t st) {
+    if (u_query_order(M) || nsets < 1 || nsets > 3) return;
+    USets sets{};
+    for (int i = 0; i < nsets; ++i) { sets.uslab[i] = uslab[i]; sets.uq[i] = uq[i]; }
     StageTimer t("u_to_query", st);
-    hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
-    return uq;
+    hipLaunchKernelGGL(u_to_query, dim3((unsigned)(nsets * P * D)), dim3(UT_T), 0, st, sets, qperm, P * D, M);
 }
 
 bool reduce_folds_epilogue(int M, int C) {
@@ -259,8 +272,7 @@ int reduce_slabs_layer(int kind, bool masked, const ReduceEpilogue& ep, const fl
         return (int)hipErrorInvalidValue;
     const int CR = slab_stride(C);
     if (qperm && !u_query_order(M)) {
-        StageTimer t("u_to_query", st);
-        hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, uslab, qperm, uq, M);
+        order_u_terms_sets(&uslab, qperm, &uq, 1, P, D, M, st);
     } else {
         uq = const_cast<float*>(uslab);                   // already in query order
     }
