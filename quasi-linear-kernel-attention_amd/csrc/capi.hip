@@ -67,7 +67,6 @@ struct SortedWs {
     float* ks; uint32_t* kp; float* qs; uint32_t* qp;
     void* sort_scratch; RangeArrays ra;
     float* slab; float* uslab; float* uq;
-    int* group;          // query grouping scratch (long segments)
 };
 
 struct WsSpec {
@@ -87,12 +86,11 @@ size_t ws_part(const WsSpec& w, int i) {
         case 6: return w.slab_rows ? align256(S * slab_rows(w.slab_rows) * (size_t)slab_stride(w.C) * 4) : 0;
         case 7: return (w.slab_rows && w.want_u) ? align256(S * w.slab_rows * 4) : 0;
         case 8: return (w.slab_rows && w.want_u) ? align256(S * w.M * 4) : 0;   // v == 1 terms in query order
-        case 9: return align256(group_scratch_bytes((int)S, w.N, w.M, w.C));        // query grouping counts
     }
     return 0;
 }
 
-constexpr int WS_PARTS = 10;
+constexpr int WS_PARTS = 9;
 
 size_t ws_bytes(const WsSpec& w) {
     size_t b = 0;
@@ -110,7 +108,6 @@ SortedWs carve(void* ws, const WsSpec& w) {
     r.ra = carve_range_arrays(part[5], w.P * w.D, w.range_stream_max, w.C);
     r.slab = (float*)part[6]; r.uslab = (float*)part[7];
     r.uq = ws_part(w, 8) ? (float*)part[8] : nullptr;
-    r.group = ws_part(w, 9) ? (int*)part[9] : nullptr;
     return r;
 }
 
@@ -164,10 +161,16 @@ int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, 
     return hip_status(sort_pair(q, k, w, S, N, M, st), "segmented sort of k and q");
 }
 
-// The query side of a forward walk that keeps no sorts: q grouped by key chunk, with the range bounds, in one pass
-// (the walks take grouped queries as well as sorted ones).
+// The query side of a forward walk that keeps no sorts, after the k sort: q grouped by key chunk, with the range
+// bounds, in one pass (the walks take grouped queries as well as sorted ones) where a segment's queries and chunk
+// bounds fit one workgroup's LDS; longer segments sort q instead and search the bounds (at N = M = 131072 the
+// multi-workgroup grouping's scattered 4-byte stores wrote 6.8x their bytes: 1.19 ms a chunk of 3 p, against 0.86
+// for the q sort and the bounds).
 static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int M, int C, hipStream_t st) {
-    return hip_status(group_queries(w.ks, q, w.qs, w.qp, w.ra.qb, qshift, S, N, M, C, w.group, st), "query grouping");
+    if (group_fits(N, M, C))
+        return hip_status(group_queries(w.ks, q, w.qs, w.qp, w.ra.qb, qshift, S, N, M, C, st), "query grouping");
+    if (int e = hip_status(seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, st), "segmented sort of q")) return e;
+    return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, qshift, S, N, M, C, st), "query bounds");
 }
 
 // ---- overlap of the query side (q sort, range boundaries) with the key side (range summaries, scan)

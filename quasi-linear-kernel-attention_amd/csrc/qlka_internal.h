@@ -179,11 +179,11 @@ int query_bounds_sets(const float* ks, const float* qs, int* const qb[], const f
 // The queries of every segment (shifted by qshift) grouped by key chunk, a quarter of a key range: qs / qp (S segments
 // of Mq) get the values and original indices of chunk 0's queries, then chunk 1's, ... (a query's chunk holds the first
 // key >= q + qshift), so each range's queries are contiguous and come chunk by chunk; the order inside a chunk is not
-// fixed. qb as query_bounds writes it. The forward walks accept these grouped queries as well as sorted ones.
+// fixed. qb as query_bounds writes it. The forward walks accept these grouped queries as well as sorted ones. Only for
+// segments that group_fits (one workgroup stages them in LDS); longer ones are sorted.
 int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int* qb, float qshift, int S, int Ns,
-                  int Mq, int C, int* scratch, hipStream_t st);
-// scratch of group_queries (per-tile bucket counts of segments too long to stage in LDS; 0 when every segment fits)
-size_t group_scratch_bytes(int S, int Ns, int Mq, int C);
+                  int Mq, int C, hipStream_t st);
+bool group_fits(int Ns, int Mq, int C);
 int range_count(int Ns, int C);          // key ranges per segment
 
 // Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null

@@ -917,7 +917,6 @@ int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S,
 constexpr int GQ_T = 1024;         // threads per workgroup
 constexpr int GQ_STAGE = 16384;    // longest segment staged in LDS (its values and indices: 128 KB)
 constexpr int GQ_STAGE_MAXB = 2048;        // most chunk buckets of a staged segment
-constexpr int GQ_MAXB = 4 * RB_MAXG;       // most chunk buckets
 
 template <int MAXB, int STAGE>
 struct GroupLds {
@@ -1038,155 +1037,21 @@ void group_queries_staged(const float* __restrict__ ks, const float* __restrict_
     }
 }
 
-// Segments too long to stage (more than GQ_STAGE queries, or more than GQ_STAGE_MAXB buckets): three passes with tiles
-// of GT_Q queries, so that a segment is spread over many workgroups. group_count: each (segment, tile) counts its
-// queries per bucket into counts[s][tile][bucket]. group_offsets: per segment, the exclusive scan of the counts in
-// (bucket, tile) order gives every (tile, bucket) its first slot, and the range bounds. group_scatter: each (segment,
-// tile) buckets its queries again and places them with returning LDS atomics on its slots (direct scattered stores).
-constexpr int GT_Q = 16384;        // queries per tile (16 per thread)
-
-template <int MAXB>
-struct BucketLds {
-    float bnd[MAXB];
-    float rb[MAXB / 4];
-    int off[MAXB + 1];
-};
-
-// the segment's Gc chunk boundaries (and the range boundaries) into LDS
-template <int CH, int MAXB>
-__device__ __forceinline__ void load_bounds(BucketLds<MAXB>& sm, const float* kseg, const int Ns, const int Gc) {
-    for (int c = threadIdx.x; c < Gc; c += GQ_T) {
-        const float y = kseg[min(Ns, (c + 1) * CH) - 1];
-        sm.bnd[c] = y;
-        if ((c & 3) == 3 || c == Gc - 1) sm.rb[c >> 2] = y;
-    }
-}
-
-template <int CH>
-__global__ __launch_bounds__(GQ_T)
-void group_count(const float* __restrict__ ks, const float* __restrict__ q, int* __restrict__ counts,
-                 const float qshift, const int Ns, const int Mq, const int Gc, const int tiles)
-{
-    __shared__ BucketLds<GQ_MAXB> sm;
-    const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles, tid = threadIdx.x;
-    const float* qseg = q + (size_t)s * Mq;
-    const int i0 = tile * GT_Q;
-    constexpr int NI = GT_Q / GQ_T;
-    float x[NI];
-#pragma unroll
-    for (int j = 0; j < NI; ++j) x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)] + qshift;   // clamped: all in flight
-    load_bounds<CH>(sm, ks + (size_t)s * Ns, Ns, Gc);
-    for (int c = tid; c <= Gc; c += GQ_T) sm.off[c] = 0;
-    __syncthreads();
-    int b[NI];
-    buckets<NI>(sm.bnd, sm.rb, Gc, x, b);
-#pragma unroll
-    for (int j = 0; j < NI; ++j)
-        if (i0 + tid + j * GQ_T < Mq) atomicAdd(&sm.off[b[j]], 1);
-    __syncthreads();
-    int* out = counts + ((size_t)s * tiles + tile) * (Gc + 1);
-    for (int c = tid; c <= Gc; c += GQ_T) out[c] = sm.off[c];
-}
-
-__global__ __launch_bounds__(GQ_T)
-void group_offsets(int* __restrict__ counts, int* __restrict__ qb, const int Gc, const int tiles, const int G)
-{
-    __shared__ int wsum[GQ_T / WAVE];
-    const int s = blockIdx.x, tid = threadIdx.x;
-    const int n = Gc + 1;
-    int* cs = counts + (size_t)s * tiles * n;
-    // thread t owns buckets [e0, e1); a bucket's total is the sum over the tiles
-    const int E = (n + GQ_T - 1) / GQ_T;
-    const int e0 = min(tid * E, n), e1 = min(e0 + E, n);
-    int own = 0;
-    for (int c = e0; c < e1; ++c)
-        for (int t = 0; t < tiles; ++t) own += cs[(size_t)t * n + c];
-    int incl = own;
-#pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        const int y = __shfl_up(incl, d, WAVE);
-        if (lane_id() >= d) incl += y;
-    }
-    if (lane_id() == WAVE - 1) wsum[tid / WAVE] = incl;
-    __syncthreads();
-    int base = incl - own;
-    for (int w = 0; w < tid / WAVE; ++w) base += wsum[w];
-    int* qbs = qb + (size_t)s * G;
-    for (int c = e0; c < e1; ++c) {
-        if (c > 0 && ((c & 3) == 0 || c == n - 1)) qbs[(c - 1) >> 2] = base;
-        for (int t = 0; t < tiles; ++t) {                 // in place: count -> first slot of (tile, bucket)
-            const int cnt = cs[(size_t)t * n + c];
-            cs[(size_t)t * n + c] = base;
-            base += cnt;
-        }
-    }
-}
-
-template <int CH>
-__global__ __launch_bounds__(GQ_T)
-void group_scatter(const float* __restrict__ ks, const float* __restrict__ q, const int* __restrict__ offsets,
-                   float* __restrict__ qs, uint32_t* __restrict__ qp, const float qshift, const int Ns, const int Mq,
-                   const int Gc, const int tiles)
-{
-    __shared__ BucketLds<GQ_MAXB> sm;
-    const int s = blockIdx.x / tiles, tile = blockIdx.x - s * tiles, tid = threadIdx.x;
-    const float* qseg = q + (size_t)s * Mq;
-    const int i0 = tile * GT_Q;
-    constexpr int NI = GT_Q / GQ_T;
-    float x[NI], xs[NI];
-#pragma unroll
-    for (int j = 0; j < NI; ++j) { x[j] = qseg[min(i0 + tid + j * GQ_T, Mq - 1)]; xs[j] = x[j] + qshift; }
-    load_bounds<CH>(sm, ks + (size_t)s * Ns, Ns, Gc);
-    const int* off = offsets + ((size_t)s * tiles + tile) * (Gc + 1);
-    for (int c = tid; c <= Gc; c += GQ_T) sm.off[c] = off[c];
-    __syncthreads();
-    int b[NI];
-    buckets<NI>(sm.bnd, sm.rb, Gc, xs, b);
-    float* qso = qs + (size_t)s * Mq;
-    uint32_t* qpo = qp + (size_t)s * Mq;
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-        const int i = i0 + tid + j * GQ_T;
-        if (i < Mq) {
-            const int pos = atomicAdd(&sm.off[b[j]], 1);
-            qso[pos] = x[j];
-            qpo[pos] = (uint32_t)i;
-        }
-    }
-}
-
-size_t group_scratch_bytes(int S, int Ns, int Mq, int C) {
-    const int RK = range_keys(C), CH = RK / 4;
-    const int Gc = (Ns + CH - 1) / CH;
-    if (Mq <= GQ_STAGE && Gc <= GQ_STAGE_MAXB) return 0;
-    const int tiles = (Mq + GT_Q - 1) / GT_Q;
-    return (size_t)S * tiles * (Gc + 1) * sizeof(int);
+bool group_fits(int Ns, int Mq, int C) {
+    const int CH = range_keys(C) / 4;
+    return Mq <= GQ_STAGE && (Ns + CH - 1) / CH <= GQ_STAGE_MAXB;
 }
 
 int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int* qb, float qshift, int S, int Ns,
-                  int Mq, int C, int* scratch, hipStream_t st) {
+                  int Mq, int C, hipStream_t st) {
     const int RK = range_keys(C), CH = RK / 4;
     const int G = (Ns + RK - 1) / RK, Gc = (Ns + CH - 1) / CH;
-    if (Gc > GQ_MAXB) return (int)hipErrorInvalidValue;
+    if (!group_fits(Ns, Mq, C)) return (int)hipErrorInvalidValue;
     StageTimer t("group_queries", st);
-    if (Mq <= GQ_STAGE && Gc <= GQ_STAGE_MAXB) {
-        if (CH == 16) hipLaunchKernelGGL((group_queries_staged<16>), dim3(S), dim3(GQ_T), 0, st,
-                                         ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
-        else hipLaunchKernelGGL((group_queries_staged<8>), dim3(S), dim3(GQ_T), 0, st,
-                                ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
-        return (int)hipGetLastError();
-    }
-    if (scratch == nullptr) return (int)hipErrorInvalidValue;
-    const int tiles = (Mq + GT_Q - 1) / GT_Q;
-    const dim3 grid((unsigned)((long)S * tiles));
-    if (CH == 16) hipLaunchKernelGGL((group_count<16>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qshift, Ns, Mq, Gc,
-                                     tiles);
-    else hipLaunchKernelGGL((group_count<8>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qshift, Ns, Mq, Gc, tiles);
-    hipLaunchKernelGGL(group_offsets, dim3(S), dim3(GQ_T), 0, st, scratch, qb, Gc, tiles, G);
-    if (CH == 16) hipLaunchKernelGGL((group_scatter<16>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qs, qp, qshift, Ns,
-                                     Mq, Gc, tiles);
-    else hipLaunchKernelGGL((group_scatter<8>), grid, dim3(GQ_T), 0, st, ks, q, scratch, qs, qp, qshift, Ns, Mq, Gc,
-                            tiles);
+    if (CH == 16) hipLaunchKernelGGL((group_queries_staged<16>), dim3(S), dim3(GQ_T), 0, st,
+                                     ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
+    else hipLaunchKernelGGL((group_queries_staged<8>), dim3(S), dim3(GQ_T), 0, st,
+                            ks, q, qs, qp, qb, qshift, Ns, Mq, G, Gc);
     return (int)hipGetLastError();
 }
 
