@@ -146,8 +146,10 @@ void lds_radix_sort(const float* __restrict__ in1, const int seg_len, const int 
 
 // One stable merge pass: runs of `width` become runs of 2*width (A = the left run wins ties). A workgroup owns
 // MERGE_TILE consecutive outputs of one pair of runs:
-//  1. two waves find where the tile starts and ends on the merge path (the number of A elements before each
-//     boundary) with a 64-way search per round (3 rounds for 64K-key runs instead of 16 dependent steps);
+//  1. merge_partition, a launch before, finds where every tile starts on the merge path (the number of A elements
+//     before its first output) with one wave per tile and a 64-way search per round (3 rounds for 64K-key runs
+//     instead of 16 dependent steps); a tile ends where the next one of its pair starts (each boundary is searched
+//     once: searched by both of its tiles, the scattered search reads were 2x the merge's own);
 //  2. the tile's A and B slices (MERGE_TILE keys + indices in total) are loaded into LDS, coalesced;
 //  3. each thread finds its MERGE_ITEMS outputs' start on the merge path inside LDS and merges them;
 //  4. the merged tile goes back through LDS and out coalesced (the final pass writes floats and perm).
@@ -174,15 +176,32 @@ __device__ int merge_path_wave(const uint32_t* __restrict__ A, const uint32_t* _
     return lo;
 }
 
+// splits[seg * blocks_per_seg + blk]: A elements before tile blk's first output within its pair (one wave per tile)
+__global__ __launch_bounds__(MERGE_THREADS)
+void merge_partition(const uint32_t* __restrict__ src_k, int* __restrict__ splits, const int seg_len, const int width,
+                     const int blocks_per_seg, const int tiles)
+{
+    const int t = blockIdx.x * (MERGE_THREADS / WAVE) + wave_in_block();
+    if (t >= tiles) return;                               // whole wave
+    const int seg = t / blocks_per_seg, blk = t - seg * blocks_per_seg;
+    const int o0 = blk * MERGE_TILE;
+    const size_t so = (size_t)seg * seg_len;
+    const int pair0 = (o0 / (2 * width)) * (2 * width);
+    const int la    = min(width, seg_len - pair0);
+    const int lb    = max(0, min(width, seg_len - pair0 - la));
+    const int ob    = o0 - pair0;
+    const int i = merge_path_wave(src_k + so + pair0, src_k + so + pair0 + la, ob, max(0, ob - lb), min(ob, la));
+    if (lane_id() == 0) splits[t] = i;
+}
+
 __global__ __launch_bounds__(MERGE_THREADS)
 void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__ src_i,
                 uint32_t* __restrict__ dst_k, uint32_t* __restrict__ dst_i,
-                float* __restrict__ out_keys, uint32_t* __restrict__ out_perm,
+                float* __restrict__ out_keys, uint32_t* __restrict__ out_perm, const int* __restrict__ splits,
                 const int seg_len, const int width, const int final_pass, const int blocks_per_seg)
 {
     __shared__ uint32_t sk[MERGE_TILE];
     __shared__ uint32_t si[MERGE_TILE];
-    __shared__ int split[2];
     const int seg = blockIdx.x / blocks_per_seg;
     const int blk = blockIdx.x - seg * blocks_per_seg;
     const int o0  = blk * MERGE_TILE;                     // tile start within the segment
@@ -198,20 +217,20 @@ void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__
     const uint32_t* Ai = src_i + so + pair0;
     const uint32_t* Bi = src_i + so + b0;
     const int ob = o0 - pair0, oe = min(ob + MERGE_TILE, la + lb);   // tile outputs [ob, oe) of the pair
-    const int w = tid / WAVE;
-    if (w < 2) {
-        const int o = w == 0 ? ob : oe;
-        const int i = merge_path_wave(A, B, o, max(0, o - lb), min(o, la));
-        if (lane_id() == 0) split[w] = i;
-    }
-    __syncthreads();
-    const int ia = split[0], na = split[1] - split[0];
-    const int jb = ob - ia, nb = (oe - split[1]) - jb;
+    // the next tile of the same pair starts where this one ends; the pair's last tile ends with all of A
+    const int* sp = splits + (size_t)seg * blocks_per_seg + blk;
+    const int ia = sp[0], iend = oe < la + lb ? sp[1] : la;
+    const int na = iend - ia;
+    const int jb = ob - ia, nb = (oe - iend) - jb;
     const int n = na + nb;                                // == oe - ob
-    for (int e = tid; e < n; e += MERGE_THREADS) {
-        const bool fa = e < na;
-        sk[e] = fa ? A[ia + e] : B[jb + e - na];
-        si[e] = fa ? Ai[ia + e] : Bi[jb + e - na];
+    // two loops, not one with a select: the select form loads both sources for every element (2x the reads)
+    for (int e = tid; e < na; e += MERGE_THREADS) {
+        sk[e] = A[ia + e];
+        si[e] = Ai[ia + e];
+    }
+    for (int e = tid; e < nb; e += MERGE_THREADS) {
+        sk[na + e] = B[jb + e];
+        si[na + e] = Bi[jb + e];
     }
     __syncthreads();
     // this thread's outputs d .. d + MERGE_ITEMS - 1 of the tile: A part sk[0, na), B part sk[na, n)
@@ -260,9 +279,12 @@ static void launch_lds(const float* in, int S, int L, int run_len, int runs, flo
                        in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
 }
 
+static inline int merge_tiles(int L) { return (L + MERGE_TILE - 1) / MERGE_TILE; }
+
 size_t seg_sort_scratch_bytes(int S, int L) {
     if (L <= LDS_SORT_MAX) return 0;
-    return 4 * (size_t)S * (size_t)L * sizeof(uint32_t);   // two (key, idx) ping-pong buffers
+    // two (key, idx) ping-pong buffers and the merge pass's tile splits
+    return 4 * (size_t)S * (size_t)L * sizeof(uint32_t) + (size_t)S * merge_tiles(L) * sizeof(int);
 }
 
 // One launch of the LDS sort over the S segments of `in` (and, with in2, those of in2) of length L <= LDS_SORT_MAX.
@@ -305,12 +327,15 @@ int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L,
     launch_lds<16, 16>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
     int err = (int)hipGetLastError();
     if (err) return err;
-    const int bps = (L + MERGE_TILE - 1) / MERGE_TILE;
-    dim3 grid((unsigned)((long)bps * S));
+    const int bps = merge_tiles(L);
+    int* splits = (int*)(i1 + n);
+    const int tiles = bps * S;
+    const dim3 grid((unsigned)tiles), pgrid((unsigned)((tiles + MERGE_THREADS / WAVE - 1) / (MERGE_THREADS / WAVE)));
     for (int width = LDS_SORT_MAX; width < L; width *= 2) {
         const int fin = (2 * width >= L);
         StageTimer t("merge_runs", st);
-        hipLaunchKernelGGL(merge_runs, grid, dim3(MERGE_THREADS), 0, st, k0, i0, k1, i1, out_keys, out_perm,
+        hipLaunchKernelGGL(merge_partition, pgrid, dim3(MERGE_THREADS), 0, st, k0, splits, L, width, bps, tiles);
+        hipLaunchKernelGGL(merge_runs, grid, dim3(MERGE_THREADS), 0, st, k0, i0, k1, i1, out_keys, out_perm, splits,
                            L, width, fin, bps);
         err = (int)hipGetLastError();
         if (err) return err;
