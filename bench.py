@@ -178,6 +178,51 @@ def config_timings(dev, reps=None, only=None):
     return out
 
 
+def sort_compare(dev, reps=10):
+    """ms per call of libqlka's segmented stable sort (qlka_seg_sort: LDS radix runs + merge passes) and of
+    torch.sort(dim=1, stable=True) (rocPRIM's segmented radix sort) on (a) 192 segments of 131072 keys, a configs[4]
+    chunk of 3 p, half of the keys on 256 exact levels, and (b) 1536 segments of 16384 N(0,1) keys; both sorts must
+    give the same permutation."""
+    from qlka import _lib
+    lib = _lib.load()
+    out = {}
+    g = torch.Generator(device=dev).manual_seed(0)
+    for name, S, L, ties in (("192x131072", 192, 131072, True), ("1536x16384", 1536, 16384, False)):
+        x = torch.randn(S, L, device=dev, generator=g)
+        if ties:
+            x[:, ::2] = torch.round(x[:, ::2] * 16) / 16
+        keys = torch.empty_like(x)
+        perm = torch.empty(S, L, dtype=torch.int32, device=dev)
+        ws = _lib.workspace(lib.qlka_seg_sort_ws_bytes(S, L), dev)
+
+        def ours():
+            _lib.check(lib.qlka_seg_sort(_lib.ptr(x), _lib.ptr(keys), _lib.ptr(perm), S, L, _lib.ptr(ws), ws.numel(),
+                                         _lib.stream_of(dev)))
+
+        def theirs():
+            return torch.sort(x, dim=1, stable=True)
+
+        def tm(fn):
+            for _ in range(2):
+                fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            return round(e0.elapsed_time(e1) / reps, 4)
+
+        t_ours, t_theirs = tm(ours), tm(theirs)
+        ref = theirs()
+        same = bool(torch.equal(ref.indices.int(), perm)) and bool(torch.equal(ref.values, keys))
+        if not same:
+            raise SystemExit(f"bench: qlka_seg_sort and torch.sort disagree on {name}")
+        out[name] = {"qlka_seg_sort_ms": t_ours, "torch_sort_ms": t_theirs, "same_permutation": same}
+    return {"sort_compare": out}
+
+
 def cpu_baseline(seed=0, mq=256, reps=3):
     """The reference's dense PyTorch path (kernels.py:73,81 restated in oracle/dense.py), torch-CPU fp32 eager, on a
     seeded sample of mq queries per p against all N keys of the headline workload. Cost is linear in the number of
@@ -306,6 +351,10 @@ def main():
     ap.add_argument("--ws-budget-gib", type=float, default=None,
                     help="libqlka workspace budget (qlka_set_workspace_budget) for every timed call, in GiB; "
                          "default: the library's")
+    ap.add_argument("--sort-compare", action="store_true",
+                    help="only time libqlka's segmented sort against torch.sort(stable=True) (rocPRIM's segmented "
+                         "radix sort) on a configs[4]-sized chunk and on headline-length segments, check that the two "
+                         "permutations agree, and print one JSON line")
     ap.add_argument("--op", choices=("laplace", "abs"), default=None,
                     help="only run --warmup + --steps calls of this one headline op and print the call count (for "
                          "per-op rocprofv3 counter runs: traffic per call = the sum over its dispatches / calls)")
@@ -321,6 +370,9 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": x.numel() * 4, "launches": 3}), flush=True)
+        return
+    if args.sort_compare:
+        print(json.dumps(sort_compare(torch.device("cuda", 0), reps=args.steps)), flush=True)
         return
     if args.ws_budget_gib is not None:
         from qlka import _lib as _l
