@@ -8,9 +8,9 @@ Prints ONE JSON line (rank 0, N=1), only after both ops' outputs on the bench in
 query subsample (`parity`). `value` = query-feature sums per second over the whole step (2 * P*M*D units per step),
 timed with events around the steps only. `roofline.frac` = B_scan of the step's two op calls / step time / 8 TB/s
 (the op-level figure the north-star target is set on, also per op in `op_frac`); `roofline.kernel` is the kernel
-with the most GPU time on its own algorithmic bytes per launch, its launch time taken in a second, instrumented pass (libqlka's hipEvent stage
-timer on the kernel's own stream). `cpu_baseline` times the reference's dense PyTorch path (restated in
-oracle/dense.py) on the host CPU on a bounded query sample of the same workload.
+with the most GPU time on its own algorithmic bytes per launch, its launch time taken in a second, instrumented pass
+(libqlka's hipEvent stage timer on the kernel's own stream). `cpu_baseline` times the reference's dense PyTorch path
+(restated in oracle/dense.py) on the host CPU on a bounded query sample of the same workload.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline] [--no-layers] [--no-configs]
     python bench.py --profile-config I [--steps K]     (one other configuration alone, e.g. under rocprofv3)
@@ -383,7 +383,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py runs on exactly one GPU (got --gpus {args.gpus}); this build has no multi-GPU path "
-              "(the ops would shard over P = B*H, or over the features d with one reduce-scatter of the partial outputs).",
+              "(the ops would shard over P = B*H, or over the features d with one reduce-scatter of the partial "
+              "outputs).",
               file=sys.stderr)
         sys.exit(2)
 

@@ -86,7 +86,8 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
 
 /*
  * weighted_abs_sum backward; g_u == NULL gives the plain backward, g_u != NULL the _full backward.
- *   grad_q[p,d,m] = sum_n s(q_m - k_n) (<v_n, g_w[m]> + g_u[m]),  grad_k[p,d,n] = sum_m s(k_n - q_m) (<g_w[m], v_n> + g_u[m]),
+ *   grad_q[p,d,m] = sum_n s(q_m - k_n) (<v_n, g_w[m]> + g_u[m]),
+ *   grad_k[p,d,n] = sum_m s(k_n - q_m) (<g_w[m], v_n> + g_u[m]),
  *   grad_v[p,n,c] = sum_{d,m} |k_n - q_m| g_w[p,m,c];  s(x) = +1 for x > 0, -1 otherwise (a tie counts -1).
  * Replaces _ext.weighted_abs_sum_backward / weighted_abs_sum_full_backward (Weighted_Abs_Sum/csrc/binding.cpp:242-380).
  */

@@ -359,7 +359,8 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
         const size_t p = (size_t)p0;
-        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s), "segmented sort of k"))
+        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s),
+                               "segmented sort of k"))
             return e;
         return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
     };
@@ -460,7 +461,8 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
                 return e;
             return hip_status(range_bounds(a, w.ra.qb, s), "query bounds");
         }
-        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s), "segmented sort of k"))
+        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s),
+                               "segmented sort of k"))
             return e;
         return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
     };
@@ -736,8 +738,8 @@ static bool layer_pipelined(int kind, int P, int D, int M, int C) {
 size_t qlka_layer_fwd_ws_bytes(int kind, int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || kind < 0 || kind > 2) return 0;
     auto b1 = [&](int pc) { return layer_ws_bytes(kind, WsSpec{pc, D, N, M, C, N, M, true}); };
-    return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), layer_pipelined(kind, P, D, M, C), b1),
-                      b1);
+    const size_t cap = g_ws_budget.load(std::memory_order_relaxed);
+    return plan_bytes(plan_chunks(P, cap, layer_pipelined(kind, P, D, M, C), b1), b1);
 }
 
 // Both layer entry points: keep == null is the reference's composition over pre-masked k, v and n_pad; keep != null
@@ -753,80 +755,48 @@ static int layer_reduce_folded(int kind, bool masked, const float* q, const floa
                       "layer reduce");
 }
 
-// One chunk of P p of a layer (pointers offset to its first p).
-static int layer_chunk(int kind, const float* q, const float* k, const float* v, const float* n_pad,
-                       const uint8_t* keep, float* out, int P, int D, int N, int M, int C, void* ws, hipStream_t st) {
+// add_bump over one chunk of P p (pointers offset to its first p) when its reduce cannot take the epilogue (C / 4 not
+// a power of two): one sort of k and q, one set of range summaries and one scan serve the three query shifts (q + s
+// has the sorted order of q, and the key side does not depend on the queries); per shift a walk and a reduce over
+// the one slab, then the epilogue.
+static int bump_chunk_unfolded(const float* q, const float* k, const float* v, const float* n_pad,
+                               const uint8_t* keep, float* out, int P, int D, int N, int M, int C, void* ws,
+                               hipStream_t st) {
     const WsSpec spec{P, D, N, M, C, N, M, true};
     const int S = P * D;
-    LayerWs L = carve_layer(kind, ws, spec);
+    LayerWs L = carve_layer(LAYER_ADD_BUMP, ws, spec);
     SortedWs& w = L.op;
-    // Masked add_laplace: masked keys become FLT_MAX (terms exactly 0, sorted last) and the unmasked walk runs.
-    const bool lap_masked = kind == LAYER_ADD_LAPLACE && keep != nullptr;
-    if (lap_masked)
-        if (int e = hip_status(mask_keys(k, keep, L.kmask, P, D, N, st), "masked keys")) return e;
-    const float* ksrc = lap_masked ? L.kmask : k;
-    if (int e = hip_status(seg_sort(ksrc, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
-    auto sort_q = [&](hipStream_t s) {
-        return hip_status(seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s), "segmented sort of q");
-    };
-    int e = 0;
-    if (kind == LAYER_ADD_LAPLACE) {
-        e = group_q(q, w, 0.f, S, N, M, C, st);
-        if (!e) e = hip_status(laplace_prepare(w.ks, w.kp, v, P, D, N, C, w.ra, st), "laplace ranges");
-        if (e) return e;
-        e = laplace_emit(w.ks, w.kp, w.qs, w.qp, v, w.slab, w.uslab, P, D, N, M, C, w.ra, st);
-        if (e) return hip_status(e, "laplace walk");
-        if (reduce_folds_epilogue(M, C))
-            return layer_reduce_folded(kind, keep != nullptr, q, n_pad, L, out, P, D, M, C, st);
-        e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[0], L.u[0], P, D, M, C, st);
-        if (e) return hip_status(e, "laplace reduce");
-    } else {
-        AbsWalkArgs a{};
-        a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr; a.keep = keep;
-        a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
-        a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
-        a.out_dot = nullptr; a.out_rank = nullptr;
-        a.sign = 1.f; a.P = P; a.D = D; a.C = C; a.qshift = 0.f;
-        const int mode = ABS_ROW | ABS_ONES | (keep ? ABS_KEEP : 0);
-        // one sort of k and q, one set of range summaries and one scan serve every query shift of add_bump: q + s has
-        // the sorted order of q, and the key side does not depend on the queries (one shift: q grouped instead)
-        const int nev = (kind == LAYER_ADD_BUMP) ? 3 : 1;
-        const float shift[3] = {0.f, 1.f, -1.f};
-        int* qbs[3] = {w.ra.qb, L.qb[0], L.qb[1]};
-        auto key_side = [&](hipStream_t s) {
-            if (int r = abs_prepare(a, mode, w.ra, s)) return hip_status(r, "abs ranges");
-            if (kind == LAYER_ADD_RIESZ)
-                return hip_status(riesz_prefix(k, v, keep, L.pre, P, D, N, C, s), "riesz prefixes");
-            return QLKA_OK; };
-        if (nev == 1) {
-            e = group_q(q, w, 0.f, S, N, M, C, st);
-            if (!e) e = key_side(st);
-        } else e = fork_join(st, key_side,
-            [&](hipStream_t s) {
-                if (int r = sort_q(s)) return r;
-                for (int ev = 0; ev < nev; ++ev) {
-                    AbsWalkArgs b = a;
-                    b.qshift = shift[ev];
-                    if (int r = range_bounds(b, qbs[ev], s)) return hip_status(r, "query bounds");
-                }
-                return QLKA_OK; });
-        if (e) return e;
-        for (int ev = 0; ev < nev; ++ev) {
-            RangeArrays ra = w.ra;
-            a.qshift = shift[ev];
-            ra.qb = qbs[ev];
-            e = abs_emit(a, mode, ra, st);
-            if (e) return hip_status(e, "abs walk");
-            if (kind == LAYER_ADD_RIESZ && reduce_folds_epilogue(M, C))
-                return layer_reduce_folded(kind, keep != nullptr, q, n_pad, L, out, P, D, M, C, st);
-            e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[ev], L.u[ev], P, D, M, C, st);
-            if (e) return hip_status(e, "abs reduce");
-        }
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    AbsWalkArgs a{};
+    a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v; a.u = nullptr; a.keep = keep;
+    a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = nullptr; a.uq = nullptr;
+    a.slab = w.slab; a.uslab = w.uslab; a.CR = slab_stride(C);
+    a.out_dot = nullptr; a.out_rank = nullptr;
+    a.sign = 1.f; a.P = P; a.D = D; a.C = C; a.qshift = 0.f;
+    const int mode = ABS_ROW | ABS_ONES | (keep ? ABS_KEEP : 0);
+    const float shift[3] = {0.f, 1.f, -1.f};
+    int* qbs[3] = {w.ra.qb, L.qb[0], L.qb[1]};
+    int e = fork_join(st,
+        [&](hipStream_t s) { return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges"); },
+        [&](hipStream_t s) {
+            if (int r = hip_status(seg_sort(q, w.qs, w.qp, S, M, w.sort_scratch, s), "segmented sort of q")) return r;
+            for (int ev = 0; ev < 3; ++ev) {
+                AbsWalkArgs b = a;
+                b.qshift = shift[ev];
+                if (int r = range_bounds(b, qbs[ev], s)) return hip_status(r, "query bounds");
+            }
+            return QLKA_OK; });
+    if (e) return e;
+    for (int ev = 0; ev < 3; ++ev) {
+        RangeArrays ra = w.ra;
+        a.qshift = shift[ev];
+        ra.qb = qbs[ev];
+        if ((e = abs_emit(a, mode, ra, st))) return hip_status(e, "abs walk");
+        if ((e = reduce_slabs(w.slab, w.uslab, w.qp, w.uq, L.w[ev], L.u[ev], P, D, M, C, st)))
+            return hip_status(e, "abs reduce");
     }
-    const bool bump = kind == LAYER_ADD_BUMP;
-    e = layer_epilogue(kind, keep != nullptr, q, n_pad, L.w[0], L.u[0], bump ? L.w[1] : nullptr,
-                       bump ? L.u[1] : nullptr, bump ? L.w[2] : nullptr, bump ? L.u[2] : nullptr, L.pre, L.qt, out,
-                       P, D, N, M, C, st);
+    e = layer_epilogue(LAYER_ADD_BUMP, keep != nullptr, q, n_pad, L.w[0], L.u[0], L.w[1], L.u[1], L.w[2], L.u[2],
+                       L.pre, L.qt, out, P, D, N, M, C, st);
     return hip_status(e, "layer epilogue");
 }
 
@@ -851,7 +821,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         return for_chunks(P, pl.pc, [&](int p0, int np) {
             const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
             chunk_in(p0, qc, kc, vc, npc, keepc, outc);
-            return layer_chunk(kind, qc, kc, vc, npc, keepc, outc, np, D, N, M, C, ws, st); });
+            return bump_chunk_unfolded(qc, kc, vc, npc, keepc, outc, np, D, N, M, C, ws, st); });
     // Per chunk: (mask keys,) sort k, group q (add_bump: sort q and find the range bounds of q, q + 1, q - 1); range
     // passes (+ riesz prefixes) and the walk (add_bump: one walk over the three query sets into three slabs); the
     // reduce with the epilogue. fp32 addition of a constant is monotone, so q + 1 and q - 1 keep the sorted order of q,

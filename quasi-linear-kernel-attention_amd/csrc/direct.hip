@@ -28,9 +28,9 @@ constexpr size_t DS_LDS_MAX = 64 * 1024;
 
 static inline int pad4(int x) { return (x + 3) & ~3; }
 
-// One round of a zero-padded copy of the row-major [R][K] block at src (row stride K) into LDS: the thread's SU elements
-// e = e0 + u * nt of the padded [Rp][Kp] index space (row e / Kp, column e % Kp, e < n = Rp * Kp). All loads of a
-// round are issued before any LDS store, so a round costs one global-memory latency, not SU of them.
+// One round of a zero-padded copy of the row-major [R][K] block at src (row stride K) into LDS: the thread's SU
+// elements e = e0 + u * nt of the padded [Rp][Kp] index space (row e / Kp, column e % Kp, e < n = Rp * Kp). All loads
+// of a round are issued before any LDS store, so a round costs one global-memory latency, not SU of them.
 template <int SU>
 struct StageRound {
     float v[SU];
@@ -513,7 +513,8 @@ static void launch_sign_small(const float* a, const float* b, const float* x, co
 }
 
 static bool sign_small_fits(int D, int I, int J, int C) {
-    return pad4(I) <= DS_MAX && pad4(J) <= DS_MAX && pad4(C) <= DS_CMAX && direct_sign_small_lds(D, I, J, C) <= DS_LDS_MAX;
+    return pad4(I) <= DS_MAX && pad4(J) <= DS_MAX && pad4(C) <= DS_CMAX &&
+           direct_sign_small_lds(D, I, J, C) <= DS_LDS_MAX;
 }
 
 // Longer segments: one workgroup of 256 threads per (p, tile of IT outputs) walks the j in tiles of 64. The x rows

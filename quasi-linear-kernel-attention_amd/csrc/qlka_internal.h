@@ -97,7 +97,8 @@ __host__ __device__ inline int slab_row_off(int m, int G, int CR) {
 // v[p,n,c] (row stride slab_stride(C)) and the v == 1 sums into uslab. laplace_prepare is the key side (range summaries
 // and scan into ra.ta / ra.tb) and needs only the sorted keys; laplace_emit is the walk, which also needs the sorted
 // queries and their range boundaries (query_bounds into ra.qb). A key of value FLT_MAX adds exactly 0 to the sums
-// of every query below FLT_MAX (its decay factor e^{-(FLT_MAX - q)} is 0): that is how masked keys drop out (mask_keys).
+// of every query below FLT_MAX (its decay factor e^{-(FLT_MAX - q)} is 0): that is how masked keys drop out
+// (mask_keys).
 int laplace_prepare(const float* ks, const uint32_t* kp, const float* v, int P, int D, int N, int C, RangeArrays ra,
                     hipStream_t st);
 int laplace_emit(const float* ks, const uint32_t* kp, const float* qs, const uint32_t* qp, const float* v,

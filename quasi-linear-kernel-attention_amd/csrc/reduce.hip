@@ -2,9 +2,10 @@
 //
 // The walks leave one contribution row per (p, d, query) in a slab (row stride slab_stride(C), whole 128-byte lines;
 // blocked by 64 queries within pairs of features, see slab_group), written with plain row stores. Summing over the
-// D features of a p here reads, per block of 64 queries, G * 64 contiguous rows per feature group, so the D-fold accumulation costs one HBM write and one HBM read per contribution
-// instead of one fp32 atomic per channel (the L2 atomic units of the chip sustain about one 4-byte atomic per
-// channel per clock, which bounds an atomic emission at P*D*M*C atomics well above the slab's traffic time).
+// D features of a p here reads, per block of 64 queries, G * 64 contiguous rows per feature group, so the D-fold
+// accumulation costs one HBM write and one HBM read per contribution instead of one fp32 atomic per channel (the L2
+// atomic units of the chip sustain about one 4-byte atomic per channel per clock, which bounds an atomic emission at
+// P*D*M*C atomics well above the slab's traffic time).
 //
 // The v == 1 sums (out_u) are one scalar per (p, d, query). For segments of up to U_LDS_CAP queries the walks write
 // them in sorted-query order (coalesced) and u_to_query puts each segment's scalars in query order through LDS

@@ -304,7 +304,8 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
         for (int g0 = glo; g0 < ghi; g0 += SCAN_BATCH) {
             float a[SCAN_BATCH][NV + 1], dec[SCAN_BATCH];
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b) load_scan_row<NV>(SA + (size_t)min(g0 + b, ghi - 1) * CS, C, a[b], dec[b]);
+            for (int b = 0; b < SCAN_BATCH; ++b)
+                load_scan_row<NV>(SA + (size_t)min(g0 + b, ghi - 1) * CS, C, a[b], dec[b]);
 #pragma unroll
             for (int b = 0; b < SCAN_BATCH; ++b) {
                 const int g = g0 + b;
@@ -323,7 +324,8 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
         for (int g0 = ghi - 1; g0 >= glo; g0 -= SCAN_BATCH) {
             float b_[SCAN_BATCH][NV + 1], dec[SCAN_BATCH];
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b) load_scan_row<NV>(SB + (size_t)max(g0 - b, glo) * CS, C, b_[b], dec[b]);
+            for (int b = 0; b < SCAN_BATCH; ++b)
+                load_scan_row<NV>(SB + (size_t)max(g0 - b, glo) * CS, C, b_[b], dec[b]);
 #pragma unroll
             for (int b = 0; b < SCAN_BATCH; ++b) {
                 const int g = g0 - b;
@@ -658,8 +660,8 @@ void lap_range_walk(const float* __restrict__ ks, const uint32_t* __restrict__ k
                             sm.b[CH * RS + l + WAVE * j] = 0.f;
                         }
                     }
-                    // Branch-free batches of EU iterations: every lane reads a record and two rows (indices clamped into
-                    // the buffers), and only the stores of queries j0 .. j1-1 (ranks in [t0, t0 + CH]) are kept.
+                    // Branch-free batches of EU iterations: every lane reads a record and two rows (indices clamped
+                    // into the buffers), and only the stores of queries j0 .. j1-1 (ranks in [t0, t0 + CH]) are kept.
                     constexpr int EU = 4;
                     const int rlo = t0 * RS * 4, rhi = (t0 + CH) * RS * 4;
                     for (int jb = j0; jb < j1; jb += EU * el_.qpi) {
@@ -824,9 +826,10 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 
 // Query bounds of every key range, from the sorted queries in one pass: qb[s, g] = #{i : q_i + qshift <= klast_g},
 // klast_g the largest key of range g. A workgroup (segment, RB_T * RB_Q queries) stages the segment's G range
-// boundaries in LDS; query i finds its bucket b_i = #{g : klast_g < q_i + qshift} by binary search there. The b_i do not decrease with i,
-// so qb[g] = i + 1 for every g in [b_i, b_{i+1}) (b_M = G), and qb[g] = 0 below b_0: every bound is written exactly
-// once, by the query it follows. (One search per query instead of a dependent search chain per range.)
+// boundaries in LDS; query i finds its bucket b_i = #{g : klast_g < q_i + qshift} by binary search there. The b_i do
+// not decrease with i, so qb[g] = i + 1 for every g in [b_i, b_{i+1}) (b_M = G), and qb[g] = 0 below b_0: every bound
+// is written exactly once, by the query it follows. (One search per query instead of a dependent search chain per
+// range.)
 constexpr int RB_T = 1024;         // threads per workgroup
 constexpr int RB_Q = 4;            // consecutive queries per thread
 constexpr int RB_MAXG = 4096;      // ranges per segment: N <= 131072 keys in ranges of >= 32

@@ -327,7 +327,8 @@ def test_gpu_validation_errors(dev):
         _ext.weighted_abs_sum_forward(torch.randn(1, 1, 4, device=dev), torch.randn(1, 1, 131073, device=dev),
                                       torch.randn(1, 131073, 1, device=dev))
     with pytest.raises(RuntimeError, match="must be contiguous"):
-        _ext.weighted_abs_sum_forward(q.transpose(1, 2).contiguous().transpose(1, 2), k, torch.randn(1, 8, 4, device=dev))
+        qt = q.transpose(1, 2).contiguous().transpose(1, 2)
+        _ext.weighted_abs_sum_forward(qt, k, torch.randn(1, 8, 4, device=dev))
     with pytest.raises(RuntimeError, match="must be float32"):
         weighted_laplace_sum(q.double(), k, torch.randn(1, 8, 4, device=dev))
     with pytest.raises(RuntimeError, match="fused path pinned but unavailable"):
