@@ -113,9 +113,10 @@ def config_timings(dev, reps=None, only=None):
     """ms per call of each configuration's workload: the mean over `reps` calls (default 20; 3 for configs[4]), each
     bracketed by events after a synchronisation, following warmup calls (5; 1 for configs[4]), as the reference's
     speed bench times a step (Experiments/speed_and_memory/bench.py:106-118). For the dense-route configurations [0]
-    and [1] also the library kernels' own time per call (libqlka's stage timer, a separate pass), the share of the
-    call that is not kernel time (`host_frac`) and the flop rate against the fp32 peak (`flop_frac`, over the whole
-    call; `flop_frac_kernels` over the kernels' time). only: one config index."""
+    and [1] also the library kernels' own time per call (libqlka's stage timer, a separate pass: `kernel_ms` is the
+    time in which at least one library kernel ran, the union over both streams; `kernel_sum_ms` the sum of the
+    launches' durations), the share of the call that is not kernel time (`host_frac`) and the flop rate against the
+    fp32 peak (`flop_frac`, over the whole call; `flop_frac_kernels` over `kernel_ms`). only: one config index."""
     from qlka import _lib
     from weighted_abs_sum import weighted_abs_sum_full
     from weighted_laplace_sum import weighted_laplace_sum
@@ -167,8 +168,10 @@ def config_timings(dev, reps=None, only=None):
                 fn()
             torch.cuda.synchronize()
             lib.qlka_timing_enable(0)
-            kms = sum(_lib.stage_time(name)[0] for name in STAGES + DENSE_STAGES) / n_rep
-            entry.update({"kernel_ms": round(kms, 4), "host_frac": round(max(ms - kms, 0.0) / ms, 4),
+            ksum = sum(_lib.stage_time(name)[0] for name in STAGES + DENSE_STAGES) / n_rep
+            kms = _lib.stage_time("busy")[0] / n_rep
+            entry.update({"kernel_ms": round(kms, 4), "kernel_sum_ms": round(ksum, 4),
+                          "host_frac": round(max(ms - kms, 0.0) / ms, 4),
                           "gflop": round(flops / 1e9, 3), "flop_peak_tflops": FP32_PEAK_TFLOPS,
                           "flop_frac": round(flops / (ms / 1e3) / 1e12 / FP32_PEAK_TFLOPS, 4),
                           "flop_frac_kernels": round(flops / (kms / 1e3) / 1e12 / FP32_PEAK_TFLOPS, 4)})

@@ -44,7 +44,8 @@ int qlka_set_direct_max(int n);
  * p = (batch, head) indices (every stage works on each p alone), taking the largest chunk the workspace it is given
  * holds (at least one p), so the caller bounds device memory by the workspace it passes. The *_ws_bytes() queries
  * report the workspace of the largest chunk within this budget (one p when even one p exceeds it); results do not
- * depend on the chunking. Process-wide; returns the previous value. The reference has no counterpart: its
+ * depend on the chunking. They report 0 for a call that takes the dense route at the current cutoff (qlka_laplace_fwd,
+ * qlka_abs_bwd, qlka_abs_bwd_sorted, qlka_sgn_fwd): such a call takes no workspace, and ws may be null. Process-wide; returns the previous value. The reference has no counterpart: its
  * workspace is O(P*D*(N+M)) (Weighted_Abs_Sum/csrc/binding.cpp:101-111), where this build's per-feature slab of
  * contribution rows is O(P*D*M*C).
  */
@@ -54,7 +55,7 @@ size_t qlka_set_workspace_budget(size_t bytes);
  * weighted_laplace_sum forward.
  *   out_w[p,m,c] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|) v[p,n,c],  out_u[p,m] = sum_{d,n} exp(-|k[p,d,n] - q[p,d,m]|)
  * max(N, M) <= B (the dense cutoff, default 512; see qlka_set_direct_max) runs the dense evaluation of
- * qlka_direct_fwd (the workspace is then unused).
+ * qlka_direct_fwd (no workspace: qlka_laplace_fwd_ws_bytes reports 0).
  * Replaces _ext.weighted_laplace_sum_forward (Weighted_Laplace_Sum/csrc/binding.cpp:63-100).
  */
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C);
@@ -200,6 +201,8 @@ int qlka_merge_rank(const float* q, const float* k, int32_t* rank, int num_segs,
  * Optional per-stage timing (no reference counterpart; measurement aid for bench.py). When enabled, every kernel
  * launch is bracketed by hipEvents on its own stream; qlka_timing_read() synchronises them and reports the
  * accumulated milliseconds and launch count of one stage ("lap_range_walk", "abs_range_walk", "lds_radix_sort", ...).
+ * The stage "busy" is the union of all bracketed intervals since the last reset (time in which at least one library
+ * kernel ran; launches on the side stream overlap those on the caller's stream).
  */
 int qlka_timing_enable(int on);
 int qlka_timing_reset(void);

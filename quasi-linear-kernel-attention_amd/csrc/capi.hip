@@ -239,6 +239,39 @@ int fork_join(hipStream_t st, KeySide key_side, QuerySide query_side) {
     return w == hipSuccess ? QLKA_OK : hip_status((int)w, "join");
 }
 
+// Dense abs backward with sign(0) = tie (0: KeOps, -1: the walks' convention), g_u nullable. Its three products are
+// independent and none fills the GPU at the sizes the dense route takes (608 workgroups each at P = 32, N = M = 600),
+// so grad_k runs on the side stream beside grad_q and then grad_v on the caller's stream: 0.355 -> 0.313 ms for a
+// forward + backward at that size. grad_q is launched before the side stream's wait (12-16 us of host time), so the
+// GPU does not wait for it.
+int dense_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+              float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, hipStream_t st) {
+    // grad_q[d, m] = sum_n s(q - k) (<g_w[m], v[n]> + g_u[m])
+    auto gq = [&](hipStream_t s) { return direct_sign(true, q, k, g_w, v, g_u, grad_q, tie, 1.f, P, D, M, N, C, s); };
+    // grad_k[d, n] = sum_m s(k - q) (<v[n], g_w[m]> + g_u[m])
+    auto gk = [&](hipStream_t s) { return direct_sign(false, k, q, v, g_w, g_u, grad_k, tie, 1.f, P, D, N, M, C, s); };
+    // grad_v[n, :] = sum_m A[m, n] g_w[m, :]: the dense abs sum with the roles of q and k swapped
+    auto gv = [&](hipStream_t s) { return direct_fwd(0, k, q, g_w, grad_v, nullptr, P, D, M, N, C, s); };
+    SideStream* sd = nullptr;
+    if (hipError_t e = side_stream(st, &sd)) return hip_status((int)e, "side stream");
+    int e = QLKA_OK;
+    if (sd == nullptr) {
+        if (!(e = gq(st)) && !(e = gk(st))) e = gv(st);
+        return hip_status(e, "dense backward");
+    }
+    if (hipError_t r = hipEventRecord(sd->fork, st)) return hip_status((int)r, "fork");
+    e = gq(st);
+    const hipError_t w = hipStreamWaitEvent(sd->s, sd->fork, 0);
+    if (w != hipSuccess) return e ? hip_status(e, "dense backward") : hip_status((int)w, "fork");
+    const int ek = e ? QLKA_OK : gk(sd->s);
+    if (!e) e = gv(st);
+    // join whatever happened, so that nothing later on st can overtake work issued on the side stream
+    const hipError_t r = hipEventRecord(sd->join, sd->s);
+    const hipError_t j = r == hipSuccess ? hipStreamWaitEvent(st, sd->join, 0) : r;
+    if (e || ek) return hip_status(e ? e : ek, "dense backward");
+    return j == hipSuccess ? QLKA_OK : hip_status((int)j, "join");
+}
+
 // ---- pipelined p-chunks
 // A chunk's work falls in three parts: prep (the sorts and the query grouping: LDS- and VALU-bound), main (the range
 // passes and the walk) and back (the reduce of the chunk's slab: an HBM-bound stream). With two workspace copies the
@@ -295,15 +328,16 @@ int run_pipeline(int P, const Plan& pl, void* ws, size_t copy, hipStream_t st, P
             if (int e = main(p0, np, ws, st)) return e;
             return back(p0, np, ws, st); });
     }
+    // The side stream needs no fork: its first work waits for `walked` of chunk 0, recorded on st after everything
+    // before it. Copy j % 2 is free for the prep of chunk j >= 2 because main of chunk j - 1 already waited on st for
+    // the reduce of chunk j - 2. (A stream wait costs 12-16 us of host time here, a record about 1 us.)
     auto hipc = [](hipError_t e, const char* what) { return e == hipSuccess ? QLKA_OK : hip_status((int)e, what); };
-    int err = hipc(hipEventRecord(sd->fork, st), "fork");
-    if (!err) err = hipc(hipStreamWaitEvent(sd->s, sd->fork, 0), "fork");
+    int err = QLKA_OK;
     int j = 0;
     for (int p0 = 0; p0 < P && !err; p0 += pl.pc, ++j) {
         const int np = std::min(pl.pc, P - p0);
         void* buf = (char*)ws + (size_t)(j % 2) * copy;
-        if (j >= 2) err = hipc(hipStreamWaitEvent(st, sd->reduced[j % 2], 0), "pipeline");
-        if (!err) err = prep(p0, np, buf, st);
+        err = prep(p0, np, buf, st);
         if (!err) err = early(p0, np, buf, st);
         if (!err && j >= 1) err = hipc(hipStreamWaitEvent(st, sd->reduced[(j - 1) % 2], 0), "pipeline");
         if (!err) err = main(p0, np, buf, st);
@@ -340,6 +374,7 @@ static WsSpec laplace_spec(int P, int D, int N, int M, int C) { return WsSpec{P,
 
 size_t qlka_laplace_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    if (dense_laplace_fwd(N, M)) return 0;        // the dense route takes no workspace
     auto b1 = [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); };
     return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, M), b1), b1);
 }
@@ -349,12 +384,12 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !out_w || !out_u) return fail(QLKA_EINVAL, "q, k, v, out_w and out_u must be non-null");
-    auto b1 = [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); };
-    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, M), b1);
-    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     hipStream_t st = (hipStream_t)stream;
     if (dense_laplace_fwd(N, M))
         return hip_status(direct_fwd(1, q, k, v, out_w, out_u, P, D, N, M, C, st), "laplace direct sum");
+    auto b1 = [&](int pc) { return ws_bytes(laplace_spec(pc, D, N, M, C)); };
+    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, M), b1);
+    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     // per chunk: sort k and group q; range passes and walk; reduce
     auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
@@ -511,6 +546,7 @@ static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
 
 size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    if (dense_sign(P, N, M)) return 0;            // the dense route takes no workspace
     auto b1 = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
     return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, N), b1), b1);
 }
@@ -525,13 +561,12 @@ int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
         return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
+    hipStream_t st = (hipStream_t)stream;
+    if (dense_sign(P, N, M))     // the walks' convention: a tie counts -1 in both gradients
+        return dense_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st);
     auto b1 = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
     const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, N), b1);
     if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
-    hipStream_t st = (hipStream_t)stream;
-    if (dense_sign(P, N, M))     // the walks' convention: a tie counts -1 in both gradients
-        return hip_status(direct_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st),
-                          "dense backward");
     // the chunk's workspace view, with the forward's sorts of the chunk when given
     auto view = [&](int p0, int np, void* buf) {
         SortedWs w = carve(buf, abs_bwd_spec(np, D, N, M, C));
@@ -603,6 +638,7 @@ static WsSpec sgn_spec(int P, int D, int N, int M, int C) { return WsSpec{P, D, 
 
 size_t qlka_sgn_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    if (dense_sign(P, N, M)) return 0;            // the dense route takes no workspace
     return budget_bytes(P, [&](int pc) { return ws_bytes(sgn_spec(pc, D, N, M, C)); });
 }
 
@@ -611,12 +647,12 @@ int qlka_sgn_fwd(const float* q, const float* k, const float* v, const float* g,
     g_err.clear();
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g || !out) return fail(QLKA_EINVAL, "q, k, v, g and out must be non-null");
-    auto bytes = [&](int pc) { return ws_bytes(sgn_spec(pc, D, N, M, C)); };
-    const int pc = fit_chunk(P, ws_bytes_given, bytes);
-    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
     hipStream_t st = (hipStream_t)stream;
     if (dense_sign(P, N, M))     // sgn(k - q) with a tie counted +1 == -(s(q - k) with a tie counted -1)
         return hip_status(direct_sign(true, q, k, g, v, nullptr, out, -1.f, -1.f, P, D, M, N, C, st), "dense sgn sum");
+    auto bytes = [&](int pc) { return ws_bytes(sgn_spec(pc, D, N, M, C)); };
+    const int pc = fit_chunk(P, ws_bytes_given, bytes);
+    if (int e = check_ws(ws, ws_bytes_given, bytes(pc))) return e;
     return for_chunks(P, pc, [&](int p0, int np) {
         const size_t p = (size_t)p0;
         SortedWs w = carve(ws, sgn_spec(np, D, N, M, C));
@@ -645,8 +681,7 @@ int qlka_direct_bwd(float tie, const float* q, const float* k, const float* v, c
     if (int e = check_dims(P, D, N, M, C)) return e;
     if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v)
         return fail(QLKA_EINVAL, "q, k, v, g_w and the three gradients must be non-null");
-    return hip_status(direct_bwd(tie, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, (hipStream_t)stream),
-                      "direct backward");
+    return dense_bwd(tie, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, (hipStream_t)stream);
 }
 
 int qlka_direct_sgn(float tie, const float* q, const float* k, const float* v, const float* g, float* out,

@@ -710,14 +710,4 @@ int direct_sign(bool gu_own, const float* a, const float* b, const float* x, con
     return (int)hipGetLastError();
 }
 
-int direct_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
-               float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, hipStream_t st) {
-    // grad_q[d, m] = sum_n s(q - k) (<g_w[m], v[n]> + g_u[m])
-    if (int e = direct_sign(true, q, k, g_w, v, g_u, grad_q, tie, 1.f, P, D, M, N, C, st)) return e;
-    // grad_k[d, n] = sum_m s(k - q) (<v[n], g_w[m]> + g_u[m])
-    if (int e = direct_sign(false, k, q, v, g_w, g_u, grad_k, tie, 1.f, P, D, N, M, C, st)) return e;
-    // grad_v[n, :] = sum_m A[m, n] g_w[m, :]: the dense abs sum with the roles of q and k swapped
-    return direct_fwd(0, k, q, g_w, grad_v, nullptr, P, D, M, N, C, st);
-}
-
 }  // namespace qlka

@@ -194,9 +194,6 @@ int direct_fwd(int kind, const float* q, const float* k, const float* v, float* 
 // x (P, I, C), y (P, J, C), g_u nullable
 int direct_sign(bool gu_own, const float* a, const float* b, const float* x, const float* y, const float* gu,
                 float* out, float tie, float scale, int P, int D, int I, int J, int C, hipStream_t st);
-// dense abs backward with sign(0) = tie (0: KeOps, -1: the walk's convention); g_u nullable
-int direct_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
-               float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, hipStream_t st);
 
 // Fused attention-layer epilogues (layers.hip)
 enum LayerKind { LAYER_ADD_LAPLACE = 0, LAYER_ADD_RIESZ = 1, LAYER_ADD_BUMP = 2 };

@@ -1,9 +1,12 @@
 // Opt-in per-stage timing. When enabled (qlka_timing_enable(1)), every kernel launch of the library is bracketed by
 // two hipEvents recorded on the launch's own stream; qlka_timing_read() synchronises the recorded events and returns
 // the accumulated milliseconds and launch count of one stage. Off by default: then no event is created or recorded.
+// The pseudo-stage "busy" is the union of all bracketed intervals: the time in which at least one library kernel
+// ran, which differs from the sum over stages when launches on two streams overlap.
 #include "qlka.h"
 #include "qlka_internal.h"
 
+#include <algorithm>
 #include <atomic>
 #include <map>
 #include <mutex>
@@ -21,13 +24,33 @@ std::vector<Pending> g_pending;
 std::map<std::string, Totals> g_totals;
 
 void drain_locked() {
+    std::vector<std::pair<float, float>> spans;     // [start, end] relative to the first launch's start
     for (auto& p : g_pending) {
-        float ms = 0.f;
+        float ms = 0.f, t0 = 0.f, t1 = 0.f;
         if (hipEventSynchronize(p.b) == hipSuccess && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
             auto& t = g_totals[p.name];
             t.ms += ms;
             t.count += 1;
+            if (hipEventElapsedTime(&t0, g_pending[0].a, p.a) == hipSuccess &&
+                hipEventElapsedTime(&t1, g_pending[0].a, p.b) == hipSuccess)
+                spans.emplace_back(t0, t1);
         }
+    }
+    std::sort(spans.begin(), spans.end());
+    double busy = 0.0;
+    float lo = 0.f, hi = 0.f;
+    for (size_t i = 0; i < spans.size(); ++i) {
+        if (i == 0 || spans[i].first > hi) {
+            busy += hi - lo;
+            lo = spans[i].first;
+            hi = spans[i].second;
+        } else {
+            hi = std::max(hi, spans[i].second);
+        }
+    }
+    busy += hi - lo;
+    if (!spans.empty()) g_totals["busy"].ms += busy;
+    for (auto& p : g_pending) {
         (void)hipEventDestroy(p.a);
         (void)hipEventDestroy(p.b);
     }

@@ -41,9 +41,19 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_version_and_workspace_sizes(lib):
     assert lib.qlka_version() == 1
-    small = lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4)
+    small = lib.qlka_laplace_fwd_ws_bytes(1, 1, 800, 800, 4)
     big = lib.qlka_laplace_fwd_ws_bytes(12, 64, 16384, 16384, 64)
     assert 0 < small < big
+    # calls the dense route takes (at the default cutoff 512) need no workspace
+    assert lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4) == 0
+    assert lib.qlka_abs_bwd_ws_bytes(32, 64, 600, 600, 64) == 0
+    assert lib.qlka_sgn_fwd_ws_bytes(2, 3, 500, 500, 8) == 0
+    assert lib.qlka_abs_bwd_ws_bytes(12, 64, 600, 600, 64) > 0          # too few workgroups at L = 600: walks
+    prev = lib.qlka_set_direct_max(0)
+    try:
+        assert lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4) > 0          # cutoff 0: always sort and walk
+    finally:
+        lib.qlka_set_direct_max(prev)
     # the row-emitting ops carry one contribution row per (p, d, query) of a chunk: the D-fold slab
     assert lib.qlka_laplace_fwd_ws_bytes(1, 64, 16384, 16384, 64) >= 64 * 16384 * 64 * 4
     assert lib.qlka_abs_bwd_ws_bytes(1, 64, 16384, 16384, 64) >= 64 * 16384 * 64 * 4
@@ -98,7 +108,8 @@ def test_path_and_workspace_errors(lib):
     assert rc == 1 and "fused path pinned but unavailable" in lib.qlka_last_error().decode()
     rc = lib.qlka_abs_fwd(dummy, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, 2, dummy, 1 << 40, None)
     assert rc == 1 and "path must be -1 (auto), 0 (global) or 1 (fused)" in lib.qlka_last_error().decode()
-    rc = lib.qlka_laplace_fwd(dummy, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, dummy, 16, None)
+    # a sort + walk shape (the dense route takes no workspace): the size check fails before any launch
+    rc = lib.qlka_laplace_fwd(dummy, dummy, dummy, dummy, dummy, 1, 1, 800, 800, 4, dummy, 16, None)
     assert rc == 2 and "workspace too small" in lib.qlka_last_error().decode()
     rc = lib.qlka_laplace_fwd(None, dummy, dummy, dummy, dummy, 1, 1, 8, 8, 4, dummy, 1 << 40, None)
     assert rc == 1 and "non-null" in lib.qlka_last_error().decode()

@@ -543,3 +543,34 @@ def test_keops_route_tie_semantics(dev):
     out = weighted_sgn_sum(_t(q, dev), _t(k, dev), _t(v, dev), _t(g_w, dev), backend="keops")
     want, norm = brute.sgn_sum(q, k, v, g_w, tie=0.0)
     _assert_rel(_np(out), want, norm, "keops sgn (tie 0)")
+
+
+def test_stage_timer_busy_is_the_union(dev):
+    # the dense backward runs grad_k on the side stream beside grad_q and grad_v: the stage timer's "busy" time (the
+    # union of the launches' intervals) is positive, at most the sum of the launches' durations, and at least the
+    # longest launch
+    from qlka import _lib
+    from weighted_abs_sum import _ext
+    lib = _lib.load()
+    P, D, N, M, C = 32, 64, 600, 600, 64
+    q, k, v = _data(P, D, N, M, C, seed=5)
+    rng = np.random.default_rng(12)
+    g_w = _t(rng.standard_normal((P, M, C)).astype(np.float32), dev)
+    g_u = _t(rng.standard_normal((P, M)).astype(np.float32), dev)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    _ext.weighted_abs_sum_direct_backward(tq, tk, tv, g_w, g_u, -1.0)
+    torch.cuda.synchronize()
+    lib.qlka_timing_reset()
+    lib.qlka_timing_enable(1)
+    try:
+        _ext.weighted_abs_sum_direct_backward(tq, tk, tv, g_w, g_u, -1.0)
+        torch.cuda.synchronize()
+    finally:
+        lib.qlka_timing_enable(0)
+    sign_ms, sign_n = _lib.stage_time("direct_sign")
+    fwd_ms, fwd_n = _lib.stage_time("direct_fwd")
+    busy, _ = _lib.stage_time("busy")
+    lib.qlka_timing_reset()
+    assert (sign_n, fwd_n) == (2, 1)
+    assert 0.0 < busy <= sign_ms + fwd_ms + 1e-3
+    assert busy >= max(fwd_ms, sign_ms / 2) - 1e-3
