@@ -124,21 +124,25 @@ __device__ __forceinline__ void mask_rows(float (&x)[RK][NV], const float kw) {
 // The two weighted row sums of a 64-key range, oa = sum_t a_t x_t and ob = sum_t b_t x_t, x_t the v row of key t
 // (row index pl, weights a, b: lane t's values), for C <= 64 with C % 4 == 0; lane c returns channel c. 16 lanes
 // cover a row with one 16-byte load each and lane group r takes keys r, r + 4, ..., so the 64 rows take 16 load
-// instructions (64 with a lane per channel); each lane fetches its key's row offset and weights by a lane shuffle,
-// and the groups' partial sums meet across lanes at the end.
+// instructions (64 with a lane per channel). Each lane stages its key's row offset and weights in wave-private LDS
+// and reads those of the keys it loads 16 bytes at a time (one LDS read per row instead of three lane shuffles: range
+// sums 0.069 -> 0.064 ms at the headline shape); the groups' partial sums meet across lanes at the end.
 __device__ __forceinline__ void range_row_sums_v4(const rsrc_t vr, const int C, const uint32_t pl, const float a,
                                                   const float b, float& oa, float& ob) {
     const int l = lane_id(), grp = l >> 4, sub = l & 15;
     const int coff = min(4 * sub, C - 4) * 4;
+    __shared__ f4_t stage_all[WPB][64];
+    f4_t* stage = stage_all[wave_in_block()];
+    stage[l] = f4_t{__uint_as_float(pl * (uint32_t)C * 4u), a, b, 0.f};
+    __builtin_amdgcn_wave_barrier();
     f4_t sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int t = 4 * i + grp;
-        const uint32_t row = (uint32_t)__shfl((int)pl, t, WAVE);
-        const float at = __shfl(a, t, WAVE), bt = __shfl(b, t, WAVE);
-        const f4_t x = buf_load4(vr, (int)(row * C * 4) + coff, 0);
-        sa += at * x;
-        sb += bt * x;
+        const f4_t w = stage[t];
+        const f4_t x = buf_load4(vr, (int)__float_as_uint(w[0]) + coff, 0);
+        sa += w[1] * x;
+        sb += w[2] * x;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
