@@ -98,7 +98,9 @@ def _sgn(x, tie):
 
 def sgn_sum(q, k, v, g, tie=1.0, qidx=None):
     """(out, norm): out[p,d,m] = sum_n sgn(k[p,d,n] - q[p,d,m]) <v[p,n,:], g[p,m,:]> with sgn(0) = tie
-    (+1 for the reference's CUDA walk, 0 for its keops backend); norm[p,d,m] = sum_n |<v_n, g_m>|."""
+    (+1 for the reference's CUDA walk, 0 for its keops backend); norm[p,d,m] = sum_{n,c} |v[p,n,c] g[p,m,c]|, the sum
+    of |term| over the elementary products (a dot product's own cancellation is fp32 rounding of the sum, not of its
+    terms)."""
     qs, qidx = _select(q, qidx)
     k, v, g = _f64(k), _f64(v), _f64(g)
     P, D = qs.shape[0], qs.shape[1]
@@ -107,10 +109,11 @@ def sgn_sum(q, k, v, g, tie=1.0, qidx=None):
     for p in range(P):
         gp = g[p] if qidx is None else g[p][qidx[p]]
         Bm = gp @ v[p].T                                   # (Mq, N) = <g_m, v_n>
+        Ba = np.abs(gp) @ np.abs(v[p]).T                   # (Mq, N) = sum_c |g_mc v_nc|
         for d in range(D):
             S = _sgn(k[p, d][None, :] - qs[p, d][:, None], tie)
             out[p, d] = (S * Bm).sum(axis=1)
-            norm[p, d] = np.abs(Bm).sum(axis=1)
+            norm[p, d] = Ba.sum(axis=1)
     return out, norm
 
 
@@ -118,7 +121,8 @@ def abs_backward(q, k, v, g_w, g_u=None, tie=-1.0):
     """(grad_q, grad_k, grad_v) of weighted_abs_sum(_full): the derivative of |k - q| w.r.t. q is s(q - k) and w.r.t.
     k is s(k - q), with s(x) = sign(x) and s(0) = tie. tie = -1 is the reference CUDA extension's convention
     (sgn_kernels.cu:8-15, binding.cpp:242-245), tie = 0 the gradient of the KeOps forward (keops_backend.py:40-41).
-    Also returns the normalisers (nq, nk, nv)."""
+    Also returns the normalisers (nq, nk, nv): the sums of |term| over the elementary terms, s g_mc v_nc and s g_um for
+    grad_q / grad_k, |k - q| g_mc for grad_v."""
     q, k, v, g_w = _f64(q), _f64(k), _f64(v), _f64(g_w)
     g_u = None if g_u is None else _f64(g_u)
     P, D, M = q.shape
@@ -127,16 +131,18 @@ def abs_backward(q, k, v, g_w, g_u=None, tie=-1.0):
     gk = np.zeros((P, D, N)); nk = np.zeros_like(gk)
     for p in range(P):
         Bm = g_w[p] @ v[p].T                               # (M, N)
+        Ba = np.abs(g_w[p]) @ np.abs(v[p]).T               # sum_c |g_mc v_nc|
         if g_u is not None:
             Bm = Bm + g_u[p][:, None]
+            Ba = Ba + np.abs(g_u[p])[:, None]
         for d in range(D):
             x = q[p, d][:, None] - k[p, d][None, :]        # (M, N) = q_m - k_n
             sq = np.where(x > 0, 1.0, np.where(x < 0, -1.0, tie))     # s(q - k)
             sk = np.where(x < 0, 1.0, np.where(x > 0, -1.0, tie))     # s(k - q)
             gq[p, d] = (sq * Bm).sum(axis=1)
             gk[p, d] = (sk * Bm).sum(axis=0)
-            nq[p, d] = np.abs(Bm).sum(axis=1)
-            nk[p, d] = np.abs(Bm).sum(axis=0)
+            nq[p, d] = Ba.sum(axis=1)
+            nk[p, d] = Ba.sum(axis=0)
     gv, _, nv = abs_sum(k, q, g_w)                         # grad_v = sum_{d,m} |k_n - q_m| g_w[m, :]
     return (gq, gk, gv), (nq, nk, nv)
 
@@ -157,16 +163,20 @@ def abs_backward_sub(q, k, v, g_w, g_u, qidx, kidx):
         qi, ki = qidx[p], kidx[p]
         Bq = g_w[p][qi] @ v[p].T                          # (mq, N)
         Bk = g_w[p] @ v[p][ki].T                          # (M, nk)
+        Aq = np.abs(g_w[p][qi]) @ np.abs(v[p]).T          # elementary-term normalisers
+        Ak = np.abs(g_w[p]) @ np.abs(v[p][ki]).T
         if g_u is not None:
             Bq = Bq + g_u[p][qi][:, None]
             Bk = Bk + g_u[p][:, None]
+            Aq = Aq + np.abs(g_u[p][qi])[:, None]
+            Ak = Ak + np.abs(g_u[p])[:, None]
         for d in range(D):
             xq = q[p, d][qi][:, None] - k[p, d][None, :]  # (mq, N)
             gq[p, d] = (np.where(xq > 0, 1.0, -1.0) * Bq).sum(axis=1)
-            nq[p, d] = np.abs(Bq).sum(axis=1)
+            nq[p, d] = Aq.sum(axis=1)
             xk = k[p, d][ki][None, :] - q[p, d][:, None]  # (M, nk) = k_n - q_m
             gk[p, d] = (np.where(xk > 0, 1.0, -1.0) * Bk).sum(axis=0)
-            nk[p, d] = np.abs(Bk).sum(axis=0)
+            nk[p, d] = Ak.sum(axis=0)
             A = np.abs(xk)                                # |k_n - q_m|
             gv[p] += A.T @ g_w[p]
             nv[p] += A.T @ np.abs(g_w[p])

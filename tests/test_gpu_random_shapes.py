@@ -1,0 +1,135 @@
+"""GPU parity of every op on seeded random shapes, both routes, against the fp64 oracle (oracle/brute.py).
+
+The fixed shape lists of the other tests pick the edges by hand; these cases are drawn once from numpy PCG64(7):
+P in [1, 4], D in [1, 9], N and M log-uniform in [1, 6000] (M == N in about half of them, so both sides cross the
+dense cutoffs and the 64-key range and 16-key chunk boundaries at unplanned places), C from a list of awkward widths
+(1, odd, one below / above 32, 64 and 128's lane slots), and values N(0, s^2) with s in {0.1, 1, 8} (s = 8 underflows
+most Laplace terms) or the tie-heavy levels of the parity tests. Each case runs the Laplace and abs forwards, the abs
+backward through autograd (the kept sorts), the C-ABI backward and weighted_sgn_sum, on the library's own routing
+and with every segment walked (qlka_set_direct_max(0)). Bar: REL = 1e-5 of sum |term| per element.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import brute
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-5
+N_CASES = 32
+WIDTHS = (1, 2, 3, 5, 8, 16, 31, 32, 33, 63, 64, 65, 100, 127, 128)
+KINDS = ("s0.1", "s1", "s8", "ties")
+
+
+def _log_uniform(rng, hi):
+    return int(np.clip(np.exp(rng.uniform(0.0, np.log(hi))), 1, hi))
+
+
+def _cases():
+    rng = np.random.default_rng(np.random.PCG64(7))
+    out = []
+    while len(out) < N_CASES:
+        P, D = int(rng.integers(1, 5)), int(rng.integers(1, 10))
+        N = _log_uniform(rng, 6000)
+        M = N if rng.random() < 0.5 else _log_uniform(rng, 6000)
+        C = int(rng.choice(WIDTHS))
+        kind = str(rng.choice(KINDS))
+        if P * D * N * M <= 2e8 and P * N * M * C <= 1e9:     # the fp64 oracle stays within seconds
+            out.append((P, D, N, M, C, kind, int(rng.integers(0, 1 << 30))))
+    return out
+
+
+CASES = _cases()
+
+
+def _data(P, D, N, M, C, kind, seed):
+    rng = np.random.default_rng(np.random.PCG64(seed))
+    if kind == "ties":
+        q = (rng.integers(-4, 5, size=(P, D, M)) / 4).astype(np.float32)
+        k = (rng.integers(-4, 5, size=(P, D, N)) / 4).astype(np.float32)
+    else:
+        s = np.float32(float(kind[1:]))
+        q = rng.standard_normal((P, D, M), dtype=np.float32) * s
+        k = rng.standard_normal((P, D, N), dtype=np.float32) * s
+    v = rng.standard_normal((P, N, C), dtype=np.float32)
+    g_w = rng.standard_normal((P, M, C), dtype=np.float32)
+    g_u = rng.standard_normal((P, M), dtype=np.float32)
+    return q, k, v, g_w, g_u
+
+
+def _t(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _check(got, want, norm, what):
+    err = brute.rel_err(got, want, norm)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    worst = float(err.max()) if err.size else 0.0
+    assert worst <= REL, f"{what}: max rel err {worst:.3e} > {REL}"
+
+
+@pytest.fixture(scope="module")
+def oracle_cache():
+    return {}
+
+
+def _oracle(cache, i):
+    """fp64 results of case i, computed once for both routes."""
+    if i not in cache:
+        P, D, N, M, C, kind, seed = CASES[i]
+        q, k, v, g_w, g_u = _data(P, D, N, M, C, kind, seed)
+        cache[i] = dict(lap=brute.laplace_sum(q, k, v), abs=brute.abs_sum(q, k, v),
+                        bwd=brute.abs_backward(q, k, v, g_w, g_u, tie=-1.0),
+                        sgn=brute.sgn_sum(q, k, v, g_w, tie=1.0))
+    return cache[i]
+
+
+@pytest.mark.parametrize("route", ["auto", "walk"])
+@pytest.mark.parametrize("i", range(N_CASES), ids=[f"P{c[0]}D{c[1]}N{c[2]}M{c[3]}C{c[4]}-{c[5]}" for c in CASES])
+def test_random_shape(dev, oracle_cache, i, route):
+    from qlka import _lib
+    from weighted_abs_sum import _ext, weighted_abs_sum_full, weighted_sgn_sum
+    from weighted_laplace_sum import weighted_laplace_sum
+    P, D, N, M, C, kind, seed = CASES[i]
+    print(f"case {i}: P={P} D={D} N={N} M={M} C={C} {kind} route={route}", flush=True)
+    q, k, v, g_w, g_u = _data(P, D, N, M, C, kind, seed)
+    want = _oracle(oracle_cache, i)
+    tq, tk, tv, tgw, tgu = (_t(a, dev) for a in (q, k, v, g_w, g_u))
+    lib = _lib.load()
+    prev = lib.qlka_set_direct_max(0) if route == "walk" else None
+    try:
+        w, u = weighted_laplace_sum(tq, tk, tv)
+        ow, ou, nw = want["lap"]
+        _check(_np(w), ow, nw, "laplace out_w")
+        _check(_np(u), ou, ou, "laplace out_u")
+
+        w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+        ow, ou, nw = want["abs"]
+        _check(_np(w), ow, nw, "abs out_w")
+        _check(_np(u), ou, ou, "abs out_u")
+
+        (wq, wk, wv), (nq, nk, nv) = want["bwd"]
+        aq, ak, av = (t.clone().requires_grad_(True) for t in (tq, tk, tv))
+        w, u = weighted_abs_sum_full(aq, ak, av, backend="cuda")
+        torch.autograd.backward([w, u], [tgw, tgu])
+        _check(_np(aq.grad), wq, nq, "autograd grad_q")
+        _check(_np(ak.grad), wk, nk, "autograd grad_k")
+        _check(_np(av.grad), wv, nv, "autograd grad_v")
+
+        gq, gk, gv = _ext.weighted_abs_sum_full_backward(tq, tk, tv, tgw, tgu)
+        _check(_np(gq), wq, nq, "grad_q")
+        _check(_np(gk), wk, nk, "grad_k")
+        _check(_np(gv), wv, nv, "grad_v")
+
+        out = weighted_sgn_sum(tq, tk, tv, tgw, backend="cuda")
+        os_, ns = want["sgn"]
+        _check(_np(out), os_, ns, "sgn")
+    finally:
+        if prev is not None:
+            lib.qlka_set_direct_max(prev)
