@@ -197,6 +197,8 @@ void slab_reduce_bump(const float* __restrict__ s0, const float* __restrict__ sp
     const size_t fstride = (size_t)SLAB_QB * CR;
     const size_t off = (size_t)p * D * slab_rows(M) * CR + (size_t)slab_row_off(m, G, CR) / 4;
     f4 a0 = {0.f, 0.f, 0.f, 0.f}, ap = a0, am = a0;
+    // 4 feature groups of loads in flight per thread (12 16-byte loads): 4.38 -> 4.34 ms per add_bump call
+#pragma unroll 4
     for (int g0 = 0; g0 < D; g0 += G) {
         const size_t go = off + (size_t)(g0 / G) * gstride;
         const f4* r0 = reinterpret_cast<const f4*>(s0 + go) + c;
