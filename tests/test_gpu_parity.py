@@ -574,3 +574,41 @@ def test_stage_timer_busy_is_the_union(dev):
     assert (sign_n, fwd_n) == (2, 1)
     assert 0.0 < busy <= sign_ms + fwd_ms + 1e-3
     assert busy >= max(fwd_ms, sign_ms / 2) - 1e-3
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 131072, 70000, 128), (2, 1, 50000, 131072, 65)])
+def test_long_segments_wide_channels(dev, shape):
+    # segments past one LDS sort run on both sides (merge passes, two-launch range scans, sorted queries instead of
+    # grouped ones, v == 1 terms written in query order) with two channel slots per lane or an odd width and M != N:
+    # both forwards on 8 queries per p, the _full backward on 8 queries and 8 keys per p, against the fp64 oracle
+    from oracle import inputs
+    from weighted_abs_sum import _ext
+    from weighted_laplace_sum import weighted_laplace_sum
+    P, D, N, M, C = shape
+    print(f"long segments {shape}", flush=True)
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) % 1000 + 21)
+    rng = np.random.default_rng(23)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    qidx = inputs.query_subsample(P, M, per_p=8, seed=5)
+
+    def sub(a, idx, axis):                                   # (P, ..., X) -> the subsample along axis 1 + axis
+        return np.stack([np.take(a[p], idx[p], axis=axis) for p in range(P)])
+
+    w, u = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v, qidx=qidx)
+    _assert_rel(sub(_np(w), qidx, 0), ow, nw, "long laplace out_w")
+    _assert_rel(sub(_np(u), qidx, 0), ou, ou, "long laplace out_u")
+    w, u = _ext.weighted_abs_sum_full_forward(tq, tk, tv)
+    ow, ou, nw = brute.abs_sum(q, k, v, qidx=qidx)
+    _assert_rel(sub(_np(w), qidx, 0), ow, nw, "long abs out_w")
+    _assert_rel(sub(_np(u), qidx, 0), ou, ou, "long abs out_u")
+    del w, u
+    bq = inputs.query_subsample(P, M, per_p=8, seed=6)
+    bk = inputs.query_subsample(P, N, per_p=8, seed=7)
+    gq, gk, gv = _ext.weighted_abs_sum_full_backward(tq, tk, tv, _t(g_w, dev), _t(g_u, dev))
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward_sub(q, k, v, g_w, g_u, bq, bk)
+    _assert_rel(sub(_np(gq), bq, 1), wq, nq, "long grad_q")
+    _assert_rel(sub(_np(gk), bk, 1), wk, nk, "long grad_k")
+    _assert_rel(sub(_np(gv), bk, 0), wv, nv, "long grad_v")
