@@ -34,7 +34,9 @@ int qlka_version(void);
  * Base cutoff B of the dense evaluation (the qlka_direct_* kernels: same results to fp32 rounding, same tie
  * conventions) in qlka_laplace_fwd, qlka_abs_fwd (path -1), qlka_abs_bwd and qlka_sgn_fwd, with L = max(N, M): the
  * abs forward goes dense for L <= 2B, the Laplace forward for L <= B, the backward and the sgn sum for L <= B or for
- * L <= 5B/4 when P * ceil(L / 32) >= 512. Default 512; 0 always sorts and walks. Process-wide; returns the previous
+ * L <= 5B/4 when P * ceil(L / 32) >= 512. With B > 0 the abs forward also goes dense for N <= 16 keys, and the
+ * backward and the sgn sum for min(N, M) <= 16 (the walk's segment totals lose accuracy with a handful of keys).
+ * Default 512; 0 always sorts and walks. Process-wide; returns the previous
  * value (or -QLKA_EINVAL for n < 0). The C-level counterpart of the reference's set_keops_cutoff
  * (Weighted_Abs_Sum/weighted_abs_sum/ops.py:21-25), which picks the KeOps backend in Python.
  */

@@ -40,13 +40,20 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 //   Laplace forward  L <= B    (its exp per term: about even at L = 700 for P = 12)
 //   backward, sgn    L <= B, or L <= 5B/4 when P * ceil(L / 32) >= 512 workgroups fill the GPU (at L = 600: dense
 //                    0.30 vs 0.44 ms at P = 32, but 0.22 vs 0.20 at P = 12)
+// With B > 0, segments of at most FEW_KEYS keys also go dense whatever the other side's length: the abs walk's row
+// emission adds the segment totals as -Btot - (q - k_max) Wtot, whose fp32 rounding is about eps * sum_n (k_max - k_n)
+// |w_n|; with a handful of keys that can exceed 1e-5 of the sum of |term| (2 keys, one heavy near q and one light far
+// away: 1.8e-5 measured), while the dense kernels sum the terms themselves. (The backward's second walk takes the
+// queries as its keys, so there the fewer of N and M counts.) The Laplace walk has no totals and keeps its rule.
+constexpr int FEW_KEYS = 16;
 std::atomic<int> g_direct_max{512};
 inline int64_t direct_base() { return g_direct_max.load(std::memory_order_relaxed); }
-inline bool dense_abs_fwd(int N, int M) { return std::max(N, M) <= 2 * direct_base(); }
+inline bool few_keys(int keys) { return direct_base() > 0 && keys <= FEW_KEYS; }
+inline bool dense_abs_fwd(int N, int M) { return std::max(N, M) <= 2 * direct_base() || few_keys(N); }
 inline bool dense_laplace_fwd(int N, int M) { return std::max(N, M) <= direct_base(); }
 inline bool dense_sign(int P, int N, int M) {
     const int64_t L = std::max(N, M), B = direct_base();
-    return L <= B || (4 * L <= 5 * B && (int64_t)P * ((L + 31) / 32) >= 512);
+    return L <= B || (4 * L <= 5 * B && (int64_t)P * ((L + 31) / 32) >= 512) || few_keys(std::min(N, M));
 }
 
 // Same limits and wording as check_qkv (Weighted_Abs_Sum/csrc/binding.cpp:79-83).

@@ -168,3 +168,12 @@ def test_keep_sorts_entries_validate(lib):
     assert rc != 0 and b"non-null" in lib.qlka_last_error()
     assert lib.qlka_abs_bwd_walks(12, 16384, 16384) == 1
     assert lib.qlka_abs_bwd_walks(512, 65, 65) == 0
+    # a handful of keys on either side: the dense route (the walk's segment totals would cost accuracy), unless the
+    # cutoff is 0
+    assert lib.qlka_abs_bwd_walks(12, 16384, 16) == 0 and lib.qlka_abs_bwd_walks(12, 16, 16384) == 0
+    assert lib.qlka_abs_bwd_walks(12, 16384, 17) == 1
+    prev = lib.qlka_set_direct_max(0)
+    try:
+        assert lib.qlka_abs_bwd_walks(12, 16384, 16) == 1
+    finally:
+        lib.qlka_set_direct_max(prev)

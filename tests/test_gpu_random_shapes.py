@@ -133,3 +133,29 @@ def test_random_shape(dev, oracle_cache, i, route):
     finally:
         if prev is not None:
             lib.qlka_set_direct_max(prev)
+
+
+# Shapes with a handful of keys on one side, where the abs walk's segment totals lose accuracy (one of them failed the
+# bar at 1.8e-5 on grad_v before such segments went to the dense kernels): the library's own routing must meet it.
+FEW_KEYS = [
+    (4, 1, 592, 2, 63, "s8", 66468720),      # grad_v: the backward's second walk has M = 2 keys
+    (3, 2, 2, 700, 33, "s8", 1234567),       # the forward over N = 2 keys
+    (2, 3, 16, 3000, 64, "s1", 7654321),
+]
+
+
+@pytest.mark.parametrize("case", FEW_KEYS, ids=[f"N{c[2]}M{c[3]}" for c in FEW_KEYS])
+def test_few_keys_dense_route(dev, case):
+    from weighted_abs_sum import _ext, weighted_abs_sum_full
+    P, D, N, M, C, kind, seed = case
+    q, k, v, g_w, g_u = _data(P, D, N, M, C, kind, seed)
+    tq, tk, tv, tgw, tgu = (_t(a, dev) for a in (q, k, v, g_w, g_u))
+    w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+    ow, ou, nw = brute.abs_sum(q, k, v)
+    _check(_np(w), ow, nw, "abs out_w")
+    _check(_np(u), ou, ou, "abs out_u")
+    gq, gk, gv = _ext.weighted_abs_sum_full_backward(tq, tk, tv, tgw, tgu)
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u, tie=-1.0)
+    _check(_np(gq), wq, nq, "grad_q")
+    _check(_np(gk), wk, nk, "grad_k")
+    _check(_np(gv), wv, nv, "grad_v")
