@@ -1287,6 +1287,10 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
     const float* rowB = tb + ((size_t)s * (G + 1) + g) * CS;
     const float* totA = ta + ((size_t)s * (G + 1) + G) * CS;
     const float* totB = tb + ((size_t)s * (G + 1) + G) * CS;
+    // The segment-total terms -Btot - (q - k_max) Wtot (rows) and -B1t - (q - k_max) N (v == 1) of the three query
+    // sets of add_bump cancel in its numerator and denominator, (T+ + T-) / 2 - T0 = 0 for q +- 1: that walk leaves
+    // them out, and with them their rounding, which grows with the span of the keys.
+    constexpr bool TOT = NS == 1;
     float PW[NV], Bv[NV], Bt[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
@@ -1295,17 +1299,17 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         const int cc = min(c, C - 1);
         PW[j] = (EMIT && ok) ? rowA[cc] : 0.f;
         Bv[j] = (ROW && ok) ? rowB[cc] : 0.f;
-        Bt[j] = (ROW && ok) ? totB[cc] : 0.f;
+        Bt[j] = (ROW && TOT && ok) ? totB[cc] : 0.f;
     }
     float PU = 0.f, Ut = 0.f, B1 = 0.f, B1t = 0.f;
     if constexpr (X2 || (ONES && KEEP)) { PU = rowA[C]; Ut = totA[C]; }   // u sums (X2) / kept-key counts (KEEP)
-    if constexpr (ONES) { B1 = rowB[C]; B1t = totB[C]; }
+    if constexpr (ONES) { B1 = rowB[C]; B1t = TOT ? totB[C] : 0.f; }
     const float Nf = (float)Ns;
 
     // Emission lanes: channels c4 .. c4+3 of one query row; Wtot of those channels
     const EmitLanes el_(slab_stride(C));
     f4_t wt4 = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (EMIT) {
+    if constexpr (EMIT && TOT) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) wt4[i] = (el_.c4 + i < C) ? totA[min(el_.c4 + i, C - 1)] : 0.f;
     }
@@ -1365,11 +1369,11 @@ void abs_range_walk(AbsWalkArgs a, const float* __restrict__ ta, const float* __
         if constexpr (ONES) {
             const float gp = __shfl(gci, max(t - 1, 0), WAVE);
             const float b1 = B1 + (t > 0 ? gp : 0.f);
-            float below = cnt, all = Nf;                  // (kept) keys below q, all (kept) keys
+            float below = cnt, all = TOT ? Nf : 0.f;      // (kept) keys below q, all (kept) keys
             if constexpr (KEEP) {
                 const float kp_ = __shfl(kci, max(t - 1, 0), WAVE);
                 below = PU + (t > 0 ? kp_ : 0.f);
-                all = Ut;
+                all = TOT ? Ut : 0.f;
             }
             if (act) useg[u_query_order(Mq) ? (int)mq : qb0 + l] = 2.f * (lq * below + b1) - B1t - qm * all;
         }
