@@ -612,3 +612,46 @@ def test_long_segments_wide_channels(dev, shape):
     _assert_rel(sub(_np(gq), bq, 1), wq, nq, "long grad_q")
     _assert_rel(sub(_np(gk), bk, 1), wk, nk, "long grad_k")
     _assert_rel(sub(_np(gv), bk, 0), wv, nv, "long grad_v")
+
+
+def test_largest_inputs(dev):
+    # P * D * max(N, M) at the limit the boundary accepts (INT32_MAX): 255 p of 64 features over 131072 keys and
+    # queries, 8.6 GB per input. The calls run 85 pipelined chunks of 3 p, the last of them 8.5 GB into each input and
+    # output. Both forwards on 4 queries of the first, middle and last p, the _full backward on 4 queries and 4 keys
+    # of the first and last p, against the fp64 oracle (every key, feature and channel).
+    from weighted_abs_sum import _ext
+    from weighted_laplace_sum import weighted_laplace_sum
+    P, D, N, M, C = 255, 64, 131072, 131072, 64
+    assert P * D * max(N, M) <= 2**31 - 1 < (P + 1) * D * max(N, M)
+    print(f"largest inputs P={P} D={D} N={N} M={M} C={C}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(31)
+    tq = torch.randn((P, D, M), generator=g, device=dev)
+    tk = torch.randn((P, D, N), generator=g, device=dev)
+    tv = torch.randn((P, N, C), generator=g, device=dev)
+    ps = [0, P // 2, P - 1]
+    ms = [0, 1, M // 2 + 3, M - 1]
+    q, k, v = _np(tq[ps]), _np(tk[ps]), _np(tv[ps])
+    qidx = np.array([ms] * len(ps))
+
+    w, u = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v, qidx=qidx)
+    _assert_rel(_np(w[ps][:, ms]), ow, nw, "largest laplace out_w")
+    _assert_rel(_np(u[ps][:, ms]), ou, ou, "largest laplace out_u")
+    del w, u
+    w, u = _ext.weighted_abs_sum_full_forward(tq, tk, tv)
+    ow, ou, nw = brute.abs_sum(q, k, v, qidx=qidx)
+    _assert_rel(_np(w[ps][:, ms]), ow, nw, "largest abs out_w")
+    _assert_rel(_np(u[ps][:, ms]), ou, ou, "largest abs out_u")
+    del w, u
+
+    g_w = torch.randn((P, M, C), generator=g, device=dev)
+    g_u = torch.randn((P, M), generator=g, device=dev)
+    gq, gk, gv = _ext.weighted_abs_sum_full_backward(tq, tk, tv, g_w, g_u)
+    pb = [0, P - 1]
+    bq = np.array([[2, 77, M // 3, M - 2]] * len(pb))
+    bk = np.array([[0, 5000, N // 2, N - 1]] * len(pb))
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward_sub(_np(tq[pb]), _np(tk[pb]), _np(tv[pb]), _np(g_w[pb]),
+                                                        _np(g_u[pb]), bq, bk)
+    _assert_rel(_np(gq[pb][:, :, bq[0]]), wq, nq, "largest grad_q")
+    _assert_rel(_np(gk[pb][:, :, bk[0]]), wk, nk, "largest grad_k")
+    _assert_rel(_np(gv[pb][:, bk[0]]), wv, nv, "largest grad_v")
