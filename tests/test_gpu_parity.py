@@ -655,3 +655,43 @@ def test_largest_inputs(dev):
     _assert_rel(_np(gq[pb][:, :, bq[0]]), wq, nq, "largest grad_q")
     _assert_rel(_np(gk[pb][:, :, bk[0]]), wk, nk, "largest grad_k")
     _assert_rel(_np(gv[pb][:, bk[0]]), wv, nv, "largest grad_v")
+
+
+def test_largest_inputs_dense(dev):
+    # The same limit on the dense route: 65535 p of 64 features over 512 keys and queries (8.6 GB per input) go to
+    # the dense kernels in one launch each (about a million workgroups), whose per-p offsets pass 8 GB. Both forwards
+    # and the _full backward on 4 queries / keys of the first, middle and last p against the fp64 oracle.
+    from weighted_abs_sum import _ext
+    from weighted_laplace_sum import weighted_laplace_sum
+    P, D, N, M, C = 65535, 64, 512, 512, 64
+    assert P * D * max(N, M) <= 2**31 - 1 < (P + 1) * D * max(N, M)
+    print(f"largest dense inputs P={P} D={D} N={N} M={M} C={C}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(37)
+    tq = torch.randn((P, D, M), generator=g, device=dev)
+    tk = torch.randn((P, D, N), generator=g, device=dev)
+    tv = torch.randn((P, N, C), generator=g, device=dev)
+    ps = [0, P // 2, P - 1]
+    ms = [0, 7, M // 2, M - 1]
+    q, k, v = _np(tq[ps]), _np(tk[ps]), _np(tv[ps])
+    qidx = np.array([ms] * len(ps))
+
+    w, u = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v, qidx=qidx)
+    _assert_rel(_np(w[ps][:, ms]), ow, nw, "largest dense laplace out_w")
+    _assert_rel(_np(u[ps][:, ms]), ou, ou, "largest dense laplace out_u")
+    del w, u
+    w, u = _ext.weighted_abs_sum_full_forward(tq, tk, tv)
+    ow, ou, nw = brute.abs_sum(q, k, v, qidx=qidx)
+    _assert_rel(_np(w[ps][:, ms]), ow, nw, "largest dense abs out_w")
+    _assert_rel(_np(u[ps][:, ms]), ou, ou, "largest dense abs out_u")
+    del w, u
+
+    g_w = torch.randn((P, M, C), generator=g, device=dev)
+    g_u = torch.randn((P, M), generator=g, device=dev)
+    gq, gk, gv = _ext.weighted_abs_sum_full_backward(tq, tk, tv, g_w, g_u)
+    bq = np.array([[1, 100, 300, M - 1]] * len(ps))
+    bk = np.array([[0, 64, 257, N - 2]] * len(ps))
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward_sub(q, k, v, _np(g_w[ps]), _np(g_u[ps]), bq, bk)
+    _assert_rel(_np(gq[ps][:, :, bq[0]]), wq, nq, "largest dense grad_q")
+    _assert_rel(_np(gk[ps][:, :, bk[0]]), wk, nk, "largest dense grad_k")
+    _assert_rel(_np(gv[ps][:, bk[0]]), wv, nv, "largest dense grad_v")
