@@ -159,3 +159,56 @@ def test_few_keys_dense_route(dev, case):
     _check(_np(gq), wq, nq, "grad_q")
     _check(_np(gk), wk, nk, "grad_k")
     _check(_np(gv), wv, nv, "grad_v")
+
+
+# Seeded random shapes large enough for the two-copy chunk pipeline (P * D * max(N, M) >= 2^22 mostly): P in [2, 16]
+# (so the last chunk is often partial), D in {16, 32, 64}, N and M log-uniform in [3000, 40000] (both sides of the
+# 16384-key LDS run, M != N in most), C from awkward widths. Both forwards and the C-ABI _full backward, checked on 6
+# queries and 6 keys per p against the fp64 oracle over every key, feature and channel.
+N_PIPE = 10
+PIPE_WIDTHS = (1, 3, 16, 31, 32, 33, 64, 65, 100, 128)
+
+
+def _pipe_cases():
+    rng = np.random.default_rng(np.random.PCG64(31))
+    out = []
+    for _ in range(N_PIPE):
+        P, D = int(rng.integers(2, 17)), int(rng.choice([16, 32, 64]))
+        N = int(np.exp(rng.uniform(np.log(3000), np.log(40000))))
+        M = N if rng.random() < 0.4 else int(np.exp(rng.uniform(np.log(3000), np.log(40000))))
+        C = int(rng.choice(PIPE_WIDTHS))
+        out.append((P, D, N, M, C, str(rng.choice(KINDS)), int(rng.integers(0, 1 << 30))))
+    return out
+
+
+PIPE_CASES = _pipe_cases()
+
+
+@pytest.mark.parametrize("case", PIPE_CASES, ids=[f"P{c[0]}D{c[1]}N{c[2]}M{c[3]}C{c[4]}-{c[5]}" for c in PIPE_CASES])
+def test_random_pipelined_shape(dev, case):
+    from oracle import inputs
+    from weighted_abs_sum import _ext, weighted_abs_sum_full
+    from weighted_laplace_sum import weighted_laplace_sum
+    P, D, N, M, C, kind, seed = case
+    print(f"pipelined case {case}", flush=True)
+    q, k, v, g_w, g_u = _data(P, D, N, M, C, kind, seed)
+    tq, tk, tv, tgw, tgu = (_t(a, dev) for a in (q, k, v, g_w, g_u))
+    qi = inputs.query_subsample(P, M, per_p=6, seed=seed % 1000)
+    ki = inputs.query_subsample(P, N, per_p=6, seed=seed % 997)
+
+    def sub(a, idx, axis):
+        return np.stack([np.take(a[p], idx[p], axis=axis) for p in range(P)])
+
+    w, u = weighted_laplace_sum(tq, tk, tv)
+    ow, ou, nw = brute.laplace_sum(q, k, v, qidx=qi)
+    _check(sub(_np(w), qi, 0), ow, nw, "laplace out_w")
+    _check(sub(_np(u), qi, 0), ou, ou, "laplace out_u")
+    w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+    ow, ou, nw = brute.abs_sum(q, k, v, qidx=qi)
+    _check(sub(_np(w), qi, 0), ow, nw, "abs out_w")
+    _check(sub(_np(u), qi, 0), ou, ou, "abs out_u")
+    gq, gk, gv = _ext.weighted_abs_sum_full_backward(tq, tk, tv, tgw, tgu)
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward_sub(q, k, v, g_w, g_u, qi, ki)
+    _check(sub(_np(gq), qi, 1), wq, nq, "grad_q")
+    _check(sub(_np(gk), ki, 1), wk, nk, "grad_k")
+    _check(sub(_np(gv), ki, 0), wv, nv, "grad_v")
