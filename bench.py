@@ -358,9 +358,10 @@ def main():
                     help="only time libqlka's segmented sort against torch.sort(stable=True) (rocPRIM's segmented "
                          "radix sort) on a configs[4]-sized chunk and on headline-length segments, check that the two "
                          "permutations agree, and print one JSON line")
-    ap.add_argument("--op", choices=("laplace", "abs"), default=None,
-                    help="only run --warmup + --steps calls of this one headline op and print the call count (for "
-                         "per-op rocprofv3 counter runs: traffic per call = the sum over its dispatches / calls)")
+    ap.add_argument("--op", choices=("laplace", "abs", "add_laplace", "add_riesz", "add_bump"), default=None,
+                    help="only run --warmup + --steps calls of this one headline op or fused attention layer (on the "
+                         "headline q, k, v) and print the call count (for per-call rocprofv3 runs: traffic per call = "
+                         "the sum over its dispatches / calls)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -405,8 +406,13 @@ def main():
         weighted_abs_sum_full(q, k, v, backend="cuda")
 
     if args.op is not None:
-        fn = (lambda: weighted_laplace_sum(q, k, v)) if args.op == "laplace" else \
-            (lambda: weighted_abs_sum_full(q, k, v, backend="cuda"))
+        if args.op == "laplace":
+            fn = lambda: weighted_laplace_sum(q, k, v)  # noqa: E731
+        elif args.op == "abs":
+            fn = lambda: weighted_abs_sum_full(q, k, v, backend="cuda")  # noqa: E731
+        else:
+            from qlka import layers
+            fn = lambda: layers.layer_forward(args.op, q, k, v)  # noqa: E731
         for _ in range(args.warmup + args.steps):
             fn()
         torch.cuda.synchronize()
