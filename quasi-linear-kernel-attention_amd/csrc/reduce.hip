@@ -19,36 +19,41 @@ namespace qlka {
 constexpr int RT = 256;        // threads per block
 
 // uq[s][qperm[s][i]] = uslab[s][i] for every segment s (M <= U_LDS_CAP): one workgroup per segment, through LDS.
-// Up to three sets of terms sorted alike (add_bump's q, q + 1, q - 1) go in one launch: block b does segment b % S
-// of set b / S.
+// Up to three sets of terms sorted alike (add_bump's q, q + 1, q - 1) go in one launch: the workgroup of a segment
+// reads the permutation once and all sets' terms at once, then moves the sets through LDS one after another.
 constexpr int UT_T = 1024;
 struct USets { const float* uslab[3]; float* uq[3]; };
 __global__ __launch_bounds__(UT_T)
-void u_to_query(const USets sets, const uint32_t* __restrict__ qperm, const int S, const int M)
+void u_to_query(const USets sets, const int nsets, const uint32_t* __restrict__ qperm, const int M)
 {
     constexpr int UT_I = U_LDS_CAP / UT_T;          // items per thread; all of a thread's loads are issued at once
     __shared__ float buf[U_LDS_CAP];
-    const int set = blockIdx.x / S, seg = blockIdx.x - set * S;
-    const float* __restrict__ uslab = sets.uslab[set];
-    float* __restrict__ uq = sets.uq[set];
-    const size_t base = (size_t)seg * M;
+    const size_t base = (size_t)blockIdx.x * M;
     const int tid = threadIdx.x;
-    float x[UT_I];
+    float x[3][UT_I];
     uint32_t dst[UT_I];
 #pragma unroll
     for (int j = 0; j < UT_I; ++j) {
         const int i = min(tid + j * UT_T, M - 1);     // clamped: unconditional loads
-        x[j] = uslab[base + i];
         dst[j] = qperm[base + i];
+#pragma unroll
+        for (int set = 0; set < 3; ++set)
+            x[set][j] = set < nsets ? sets.uslab[set][base + i] : 0.f;
     }
 #pragma unroll
-    for (int j = 0; j < UT_I; ++j)
-        if (tid + j * UT_T < M) buf[dst[j]] = x[j];
-    __syncthreads();
+    for (int set = 0; set < 3; ++set) {
+        if (set >= nsets) break;
+        if (set > 0) __syncthreads();                 // the previous set's reads of buf are done
 #pragma unroll
-    for (int j = 0; j < UT_I; ++j) {
-        const int i = tid + j * UT_T;
-        if (i < M) uq[base + i] = buf[i];
+        for (int j = 0; j < UT_I; ++j)
+            if (tid + j * UT_T < M) buf[dst[j]] = x[set][j];
+        __syncthreads();
+        float* __restrict__ uq = sets.uq[set];
+#pragma unroll
+        for (int j = 0; j < UT_I; ++j) {
+            const int i = tid + j * UT_T;
+            if (i < M) uq[base + i] = buf[i];
+        }
     }
 }
 
@@ -261,7 +266,7 @@ void order_u_terms_sets(const float* const* uslab, const uint32_t* qperm, float*
     USets sets{};
     for (int i = 0; i < nsets; ++i) { sets.uslab[i] = uslab[i]; sets.uq[i] = uq[i]; }
     StageTimer t("u_to_query", st);
-    hipLaunchKernelGGL(u_to_query, dim3((unsigned)(nsets * P * D)), dim3(UT_T), 0, st, sets, qperm, P * D, M);
+    hipLaunchKernelGGL(u_to_query, dim3((unsigned)(P * D)), dim3(UT_T), 0, st, sets, nsets, qperm, M);
 }
 
 bool reduce_folds_epilogue(int M, int C) {
