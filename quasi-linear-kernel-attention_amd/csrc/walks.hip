@@ -829,103 +829,48 @@ void abs_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 
 }
 
-// Query bounds of every key range, from the sorted queries in one pass: qb[s, g] = #{i : q_i + qshift <= klast_g},
-// klast_g the largest key of range g. A workgroup (segment, RB_T * RB_Q queries) stages the segment's G range
-// boundaries in LDS; query i finds its bucket b_i = #{g : klast_g < q_i + qshift} by binary search there. The b_i do
-// not decrease with i, so qb[g] = i + 1 for every g in [b_i, b_{i+1}) (b_M = G), and qb[g] = 0 below b_0: every bound
-// is written exactly once, by the query it follows. (One search per query instead of a dependent search chain per
-// range.) Up to three query shifts (add_bump's q, q + 1, q - 1) share the staged boundaries and the loaded queries:
-// each thread searches its queries once per shift, each search starting from the previous bucket. 16 queries per
-// thread read the boundaries (one cache line each) once per 16384 queries. Segments of up to QB_LDS queries take
-// query_bounds_lds below instead; at N = M = 131072 this kernel takes 0.112 ms a launch (0.153 with 4 queries per
-// thread, one workgroup per shift and a full search per query).
-constexpr int RB_T = 1024;         // threads per workgroup
-constexpr int RB_Q = 16;           // consecutive queries per thread
-constexpr int RB_MAXG = 4096;      // ranges per segment: N <= 131072 keys in ranges of >= 32
+// Query bounds of every key range from the sorted queries: qb[s, g] = #{i : fl(q_i + qshift) <= klast_g}, klast_g the
+// largest key of range g, for up to three query shifts in one launch (add_bump's q, q + 1, q - 1). fl(q_i + qshift)
+// does not decrease with i, so each bound is one binary search over the queries. A workgroup takes one piece of up to
+// QB_LDS consecutive queries of a segment into LDS (coalesced) and, for every (shift, range) pair, searches the bound
+// there if the piece holds it: every query before the piece is <= klast_g (the last one is) and not every query of
+// the piece is (or the piece is the segment's last). Exactly one piece passes both tests, so every bound is written
+// once, and coalesced. G searches per shift and segment instead of one per query: 10.5 us a launch for add_bump's
+// three shifts at the headline shape (46 us searching per query); 0.081 ms a configs[4] chunk (0.153).
+constexpr int QB_T = 1024;         // threads per workgroup
+constexpr int QB_LDS = 16384;      // queries per piece
+constexpr int QB_MAXG = 4096;      // ranges per segment: N <= 131072 keys in ranges of >= 32
 
 struct BoundSets { int* qb[3]; float shift[3]; };
 
 template <int RK>
-__global__ __launch_bounds__(RB_T)
-void query_bounds_kernel(const float* __restrict__ ks, const float* __restrict__ qs, const BoundSets sets,
-                         const int nsets, const int S, const int Ns, const int Mq, const int G, const int chunks)
-{
-    __shared__ float bnd[RB_MAXG];
-    const int s = blockIdx.x / chunks, ch = blockIdx.x - s * chunks;
-    const float* kseg = ks + (size_t)s * Ns;
-    for (int g = threadIdx.x; g < G; g += RB_T) bnd[g] = kseg[min(Ns, (g + 1) * RK) - 1];
-    __syncthreads();
-    // bucket of x, #{g : bnd[g] < x}, given a lower bound b of it (bnd is sorted): a few steps forward from b, then a
-    // binary search over the rest. A thread's queries are consecutive in sorted order, so after its first query the
-    // next bucket is almost always within the first steps.
-    auto bucket_from = [&](int b, const float x) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            if (b < G && bnd[b] < x) ++b;
-        if (b < G && bnd[b] < x) {
-            int lo = b + 1, hi = G;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (bnd[mid] < x) lo = mid + 1;
-                else hi = mid;
-            }
-            b = lo;
-        }
-        return b;
-    };
-    // thread t: queries i0 .. i0 + RB_Q - 1 and, for the bounds after the last of them, the query that follows
-    const int i0 = (ch * RB_T + (int)threadIdx.x) * RB_Q;
-    if (i0 >= Mq) return;
-    const float* qseg = qs + (size_t)s * Mq;
-    float x[RB_Q + 1];
-#pragma unroll
-    for (int j = 0; j <= RB_Q; ++j) x[j] = qseg[min(i0 + j, Mq - 1)];   // clamped: all loads in flight
-    for (int set = 0; set < nsets; ++set) {
-        int* qbs = sets.qb[set] + (size_t)s * G;
-        const float qshift = sets.shift[set];
-        int b = bucket_from(0, x[0] + qshift);
-        if (i0 == 0)
-            for (int g = 0; g < b; ++g) qbs[g] = 0;
-#pragma unroll
-        for (int j = 0; j < RB_Q; ++j) {
-            const int i = i0 + j;
-            if (i >= Mq) break;
-            const int bn = (i + 1 < Mq) ? bucket_from(b, x[j + 1] + qshift) : G;
-            for (int g = b; g < bn; ++g) qbs[g] = i + 1;
-            b = bn;
-        }
-    }
-}
-
-// The same bounds for segments of up to QB_LDS queries, one workgroup per segment: the sorted queries go to LDS
-// (coalesced), and each (shift, range) pair finds its bound qb[g] = #{i : q_i + qshift <= klast_g} by one binary search
-// there over the same comparison (fl(q_i + qshift) does not decrease with i), written coalesced. G searches per shift
-// instead of one per query: 10.5 us a launch for add_bump's three shifts at the headline shape (46 us searching per query).
-constexpr int QB_LDS = 16384;
-
-template <int RK>
-__global__ __launch_bounds__(RB_T)
+__global__ __launch_bounds__(QB_T)
 void query_bounds_lds(const float* __restrict__ ks, const float* __restrict__ qs, const BoundSets sets,
-                      const int nsets, const int Ns, const int Mq, const int G)
+                      const int nsets, const int Ns, const int Mq, const int G, const int pieces)
 {
     __shared__ float qv[QB_LDS];
-    const int s = blockIdx.x;
+    const int s = blockIdx.x / pieces, pc = blockIdx.x - s * pieces;
+    const int p0 = pc * QB_LDS, len = min(QB_LDS, Mq - p0);
     const float* qseg = qs + (size_t)s * Mq;
-    for (int i = threadIdx.x; i < Mq; i += RB_T) qv[i] = qseg[i];
+    for (int i = threadIdx.x; i < len; i += QB_T) qv[i] = qseg[p0 + i];
+    const float qprev = p0 > 0 ? qseg[p0 - 1] : 0.f;       // the last query before the piece
     __syncthreads();
     const float* kseg = ks + (size_t)s * Ns;
-    for (int t = threadIdx.x; t < nsets * G; t += RB_T) {
+    const bool last = pc == pieces - 1;
+    for (int t = threadIdx.x; t < nsets * G; t += QB_T) {
         const int set = t / G, g = t - set * G;
         const float qshift = set == 0 ? sets.shift[0] : set == 1 ? sets.shift[1] : sets.shift[2];
         int* qb = set == 0 ? sets.qb[0] : set == 1 ? sets.qb[1] : sets.qb[2];
         const float kl = kseg[min(Ns, (g + 1) * RK) - 1];
-        int lo = 0, hi = Mq;                              // first i with fl(q_i + qshift) > klast_g
+        if (p0 > 0 && !(qprev + qshift <= kl)) continue;   // a query before the piece is above klast_g
+        if (!last && qv[len - 1] + qshift <= kl) continue; // the whole piece is <= klast_g: a later piece holds it
+        int lo = 0, hi = len;                             // first i of the piece with fl(q_i + qshift) > klast_g
         while (lo < hi) {
             const int mid = (lo + hi) >> 1;
             if (qv[mid] + qshift <= kl) lo = mid + 1;
             else hi = mid;
         }
-        qb[(size_t)s * G + g] = lo;
+        qb[(size_t)s * G + g] = p0 + lo;
     }
 }
 
@@ -933,27 +878,16 @@ int query_bounds_sets(const float* ks, const float* qs, int* const qb[], const f
                       int Ns, int Mq, int C, hipStream_t st) {
     const int RK = range_keys(C);
     const int G = (Ns + RK - 1) / RK;
-    if (G > RB_MAXG || nsets < 1 || nsets > 3) return (int)hipErrorInvalidValue;
+    if (G > QB_MAXG || nsets < 1 || nsets > 3) return (int)hipErrorInvalidValue;
     BoundSets sets{};
     for (int i = 0; i < nsets; ++i) { sets.qb[i] = qb[i]; sets.shift[i] = shift[i]; }
+    const int pieces = (Mq + QB_LDS - 1) / QB_LDS;
+    const dim3 grid((unsigned)((long)S * pieces));
     StageTimer t("query_bounds", st);
-    if (Mq <= QB_LDS) {
-        if (RK == 64)
-            hipLaunchKernelGGL((query_bounds_lds<64>), dim3((unsigned)S), dim3(RB_T), 0, st, ks, qs, sets, nsets, Ns,
-                               Mq, G);
-        else
-            hipLaunchKernelGGL((query_bounds_lds<32>), dim3((unsigned)S), dim3(RB_T), 0, st, ks, qs, sets, nsets, Ns,
-                               Mq, G);
-        return (int)hipGetLastError();
-    }
-    const int chunks = (Mq + RB_T * RB_Q - 1) / (RB_T * RB_Q);
-    const dim3 grid((unsigned)((long)S * chunks));
     if (RK == 64)
-        hipLaunchKernelGGL((query_bounds_kernel<64>), grid, dim3(RB_T), 0, st, ks, qs, sets, nsets, S, Ns, Mq, G,
-                           chunks);
+        hipLaunchKernelGGL((query_bounds_lds<64>), grid, dim3(QB_T), 0, st, ks, qs, sets, nsets, Ns, Mq, G, pieces);
     else
-        hipLaunchKernelGGL((query_bounds_kernel<32>), grid, dim3(RB_T), 0, st, ks, qs, sets, nsets, S, Ns, Mq, G,
-                           chunks);
+        hipLaunchKernelGGL((query_bounds_lds<32>), grid, dim3(QB_T), 0, st, ks, qs, sets, nsets, Ns, Mq, G, pieces);
     return (int)hipGetLastError();
 }
 
