@@ -171,7 +171,7 @@ int sort_both(const float* q, const float* k, SortedWs& w, int S, int N, int M, 
 // The query side of a forward walk that keeps no sorts, after the k sort: q grouped by key chunk, with the range
 // bounds, in one pass (the walks take grouped queries as well as sorted ones) where a segment's queries and chunk
 // bounds fit one workgroup's LDS; longer segments sort q instead and search the bounds (at N = M = 131072 the
-// multi-workgroup grouping's scattered 4-byte stores wrote 6.8x their bytes: 1.19 ms a chunk of 3 p, against 0.86
+// multi-workgroup grouping's scattered 4-byte stores wrote 6.8x their bytes: 1.19 ms a chunk of 3 p, against 0.77
 // for the q sort and the bounds).
 static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int M, int C, hipStream_t st) {
     if (group_fits(N, M, C))
