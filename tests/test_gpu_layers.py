@@ -218,3 +218,66 @@ def test_masked_layer_validation(dev):
     q, k, v = _inputs(2, 2, 16, 16, 4, seed=1, dev=dev)
     with pytest.raises(RuntimeError, match="keep must be"):
         layers.layer_forward("add_riesz", q, k, v, keep=torch.ones(2, 15, dtype=torch.bool, device=dev))
+
+
+# Seeded random shapes, including ill-conditioned ones (wide spreads, a handful of keys or queries, add_riesz whose
+# denominator cancels, add_bump queries with no key within distance 1): there the output is rounding noise of the
+# epilogue's cancellation for any fp32 evaluation, the reference's own included, so no fixed tolerance between two fp32
+# evaluations holds. The bar is relative to the reference: against the float64 evaluation of the same composition,
+# the fused layer's largest error is at most twice that of the reference's fp32 composition (the ops + torch epilogue,
+# over zeroed keys with n_pad for a mask), plus 1e-5 of the output scale.
+def _random_layer_cases(n=16, seed=5):
+    rng = np.random.default_rng(np.random.PCG64(seed))
+    widths = (1, 2, 3, 5, 8, 16, 31, 32, 33, 63, 64, 65, 100, 127, 128)
+    out = []
+    while len(out) < n:
+        P, D = int(rng.integers(1, 6)), int(rng.integers(1, 17))
+        N = int(np.clip(np.exp(rng.uniform(0, np.log(3000))), 1, 3000))
+        M = N if rng.random() < 0.5 else int(np.clip(np.exp(rng.uniform(0, np.log(3000))), 1, 3000))
+        C = int(rng.choice(widths))
+        if P * D * N * M > 3e7:
+            continue
+        out.append((P, D, N, M, C, str(rng.choice(KERNELS)), float(rng.choice([0.3, 0.7, 2.0])),
+                    bool(rng.random() < 0.4), int(rng.integers(0, 1 << 20))))
+    return out
+
+
+# plus shapes a wider sweep of the same generator found where the two fp32 evaluations differ by up to 1e-3 relative
+# (denominators that cancel) or, for add_bump with one key, by O(1) on rows that are 0 / 0 in exact arithmetic
+RANDOM_LAYER_CASES = _random_layer_cases() + [
+    (2, 14, 494, 77, 8, "add_riesz", 0.3, False, 551394),
+    (1, 1, 2980, 6, 8, "add_riesz", 2.0, False, 276024),
+    (5, 2, 1, 4, 128, "add_bump", 2.0, False, 424025),
+    (2, 2, 16, 20, 2, "add_bump", 2.0, False, 936295),
+]
+
+
+@pytest.mark.parametrize("case", RANDOM_LAYER_CASES,
+                         ids=[f"{c[5]}-P{c[0]}D{c[1]}N{c[2]}M{c[3]}C{c[4]}-s{c[6]}{'-masked' if c[7] else ''}"
+                              for c in RANDOM_LAYER_CASES])
+def test_random_layer_shapes_vs_float64(dev, case):
+    from qlka import layers
+    P, D, N, M, C, kernel, scale, masked, seed = case
+    print(f"random layer {case}", flush=True)
+    q, k, v = _inputs(P, D, N, M, C, seed=seed, dev=dev, scale=scale)
+    if masked:
+        keep = _mask(P, N, seed=seed, dev=dev)
+        got = layers.layer_forward(kernel, q, k, v, keep=keep).cpu().double()
+        kp = keep.float()
+        n_pad = N - kp.sum(dim=1, keepdim=True)
+        op = _op_layer(kernel, q, k * kp[:, None, :], v * kp[:, :, None], n_pad).cpu().double()
+        ref = _reference_masked(kernel, q, k, v, keep)
+    else:
+        n_pad = torch.arange(P, device=dev, dtype=torch.float32).reshape(P, 1) * 0.25
+        got = layers.layer_forward(kernel, q, k, v, n_pad).cpu().double()
+        op = _op_layer(kernel, q, k, v, n_pad).cpu().double()
+        q64, k64, v64 = (t.cpu().double() for t in (q, k, v))
+        lap, absf = dense.dense_laplace_sum, dense.dense_abs_sum
+        ref = (dense.add_laplace_layer(q64, k64, v64, n_pad.cpu().double(), lap) if kernel == "add_laplace" else
+               dense.add_riesz_layer(q64, k64, v64, n_pad.cpu().double(), absf) if kernel == "add_riesz" else
+               dense.add_bump_layer(q64, k64, v64, n_pad.cpu().double(), absf))
+    assert got.shape == (P, M, C) and torch.all(torch.isfinite(got))
+    e_fused = float((got - ref).abs().max())
+    e_op = float((op - ref).abs().max())
+    bar = 2.0 * e_op + 1e-5 * float(ref.abs().max()) + 1e-12
+    assert e_fused <= bar, f"{case}: fused error {e_fused:.3e} > {bar:.3e} (reference composition's {e_op:.3e})"
