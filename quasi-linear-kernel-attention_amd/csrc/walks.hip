@@ -3,8 +3,8 @@
 // Per segment s = (p, d) the keys are sorted (sort.hip) and cut into key ranges of RK keys; one wave owns one range
 // and the queries whose merge rank r = #{keys < q} falls in it (the last range also owns r = N). Four kernels:
 //
-//   query_bounds   one thread per sorted query: the query bounds of every range (a binary search over the range
-//                  boundaries in LDS per query; the bounds fall between consecutive queries).
+//   query_bounds   the query bounds of every range from the sorted queries (pieces of them staged in LDS, one
+//                  binary search per range there), or group_queries: the queries grouped by key chunk instead.
 //   *_range_sums   one wave per range: the range's summary, computed directly (every term has its own weight,
 //                  no recurrence).
 //   *_range_scan   one wave per segment: turns the summaries into each range's entry state (exclusive prefix over
