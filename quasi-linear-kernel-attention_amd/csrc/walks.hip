@@ -7,8 +7,9 @@
 //                  binary search per range there), or group_queries: the queries grouped by key chunk instead.
 //   *_range_sums   one wave per range: the range's summary, computed directly (every term has its own weight,
 //                  no recurrence).
-//   *_range_scan   one wave per segment: turns the summaries into each range's entry state (exclusive prefix over
-//                  the ranges to the left) and, for the Laplace sum, exit state (exclusive suffix to the right).
+//   *_range_scan   one workgroup per segment (or per 256 ranges of a longer one, in two launches): turns the
+//                  summaries into each range's entry state (exclusive prefix over the ranges to the left) and, for
+//                  the Laplace sum, exit state (exclusive suffix to the right).
 //   *_range_walk   one wave per range: gathers the range's RK value rows into registers (lane = channel), runs the
 //                  recurrences key by key in 4 chunks, stages each chunk's state rows in wave-private LDS and emits
 //                  the owned queries ranked in the chunk from there, 64 / LQ query rows per 16-byte-per-lane store.
