@@ -236,17 +236,7 @@ void lap_range_sums(const float* __restrict__ ks, const uint32_t* __restrict__ k
 // row holds the range's link to its neighbour (a decay factor or a key gap, written by the sums kernel), so the scan
 // loop is loads and FMAs only.
 constexpr int SCAN_W = 16;
-constexpr int SCAN_BATCH = 8;      // rows loaded ahead in a piece
-
-template <int NV>
-__device__ __forceinline__ void load_scan_row(const float* __restrict__ row, const int C, float (&r)[NV + 1],
-                                              float& link) {
-#pragma unroll
-    for (int j = 0; j < NV; ++j) r[j] = row[min(lane_id() + WAVE * j, C - 1)];   // lanes >= C are never stored
-    r[NV] = row[C];
-    link = row[C + 1];
-}
-
+constexpr int SCAN_BLOCK = 256;     // ranges of a scan workgroup
 template <int NV>
 __device__ __forceinline__ void store_scan_row(float* __restrict__ row, const int C, const float (&r)[NV + 1]) {
 #pragma unroll
@@ -257,12 +247,42 @@ __device__ __forceinline__ void store_scan_row(float* __restrict__ row, const in
     if (lane_id() == 0) row[C] = r[NV];
 }
 
+// A wave's piece of at most SCAN_PIECE range summaries, loaded once with all its loads in flight together and kept in
+// registers for both passes of the scan (instead of reloading it per pass and direction in batches): the lane's
+// channels of row i in v[i], and the row's two scalars (slot C and the link to the neighbour) in lane i of u / link.
+// Rows past the piece repeat its last row and are never used.
+template <int NV>
+struct ScanPiece {
+    float v[SCAN_BLOCK / SCAN_W][NV];
+    float u, link;
+    __device__ __forceinline__ void load(const float* __restrict__ rows, const int CS, const int C, const int glo,
+                                         const int ghi) {
+        if (ghi <= glo) return;                           // empty piece (uniform)
+        const int l = lane_id();
+#pragma unroll
+        for (int i = 0; i < SCAN_BLOCK / SCAN_W; ++i) {
+            const float* row = rows + (size_t)min(glo + i, ghi - 1) * CS;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) v[i][j] = row[min(l + WAVE * j, C - 1)];   // lanes >= C are never stored
+        }
+        const float* row = rows + (size_t)min(glo + l, ghi - 1) * CS;
+        u = row[C];
+        link = row[C + 1];
+    }
+    // row i (a constant after unrolling): its NV lane values, slot C, and the link
+    __device__ __forceinline__ void get(const int i, float (&r)[NV + 1], float& lk) const {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) r[j] = v[i][j];
+        r[NV] = bcast(u, i);
+        lk = bcast(link, i);
+    }
+};
+
 // Long segments are scanned by several workgroups of SCAN_BLOCK ranges each, in two launches: phase 1 runs every wave's
 // piece from a zero state and writes the wave aggregates and, composed in order, the workgroup's aggregate; phase 2
 // composes the aggregates of the workgroups before (and, for a suffix, after) its own into its incoming state, then
 // the waves of its own before (after) theirs, and reruns each piece from the true state, writing the range states.
 // Segments of up to SCAN_BLOCK ranges (N <= 16384 at 64-key ranges) run both phases in one workgroup (phase 0).
-constexpr int SCAN_BLOCK = 256;
 __host__ __device__ inline int scan_blocks(int G) { return (G + SCAN_BLOCK - 1) / SCAN_BLOCK; }
 // floats of one workgroup's aggregate record: SCAN_W wave aggregates + the workgroup aggregate, each two (state,
 // link) pairs of NV + 1 lane vectors and one lane vector
@@ -303,43 +323,38 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
     const int glo = min(b1, b0 + w * per), ghi = min(b1, b0 + w * per + per);
     float* seg_aggs = PHASE == 0 ? nullptr : aggs + (size_t)s * nb * scan_rec_floats<NV>();
 
+    ScanPiece<NV> piece_a, piece_b;
+    piece_a.load(SA, CS, C, glo, ghi);
+    piece_b.load(SB, CS, C, glo, ghi);
     // forward piece walk from state cur; writes entry states when OUT; returns the product of the piece's decays
     auto fwd = [&](float (&cur)[NV + 1], const bool out) {
         float prod = 1.f;
-        for (int g0 = glo; g0 < ghi; g0 += SCAN_BATCH) {
-            float a[SCAN_BATCH][NV + 1], dec[SCAN_BATCH];
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b)
-                load_scan_row<NV>(SA + (size_t)min(g0 + b, ghi - 1) * CS, C, a[b], dec[b]);
+        for (int i = 0; i < SCAN_BLOCK / SCAN_W; ++i) {
+            const int g = glo + i;
+            if (g >= ghi) break;
+            float a[NV + 1], dec;
+            piece_a.get(i, a, dec);
+            if (out) store_scan_row<NV>(A + (size_t)g * CS, C, cur);
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b) {
-                const int g = g0 + b;
-                if (g >= ghi) break;
-                if (out) store_scan_row<NV>(A + (size_t)g * CS, C, cur);
-#pragma unroll
-                for (int j = 0; j <= NV; ++j) cur[j] = a[b][j] + dec[b] * cur[j];
-                prod *= dec[b];
-            }
+            for (int j = 0; j <= NV; ++j) cur[j] = a[j] + dec * cur[j];
+            prod *= dec;
         }
         return prod;
     };
     // backward piece walk from state cur; writes exit states when OUT; returns the product of the piece's decays
     auto bwd = [&](float (&cur)[NV + 1], const bool out) {
         float prod = 1.f;
-        for (int g0 = ghi - 1; g0 >= glo; g0 -= SCAN_BATCH) {
-            float b_[SCAN_BATCH][NV + 1], dec[SCAN_BATCH];
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b)
-                load_scan_row<NV>(SB + (size_t)max(g0 - b, glo) * CS, C, b_[b], dec[b]);
+        for (int i = SCAN_BLOCK / SCAN_W - 1; i >= 0; --i) {
+            const int g = glo + i;
+            if (g >= ghi) continue;
+            float b_[NV + 1], dec;
+            piece_b.get(i, b_, dec);
+            if (out) store_scan_row<NV>(B + (size_t)g * CS, C, cur);
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b) {
-                const int g = g0 - b;
-                if (g < glo) break;
-                if (out) store_scan_row<NV>(B + (size_t)g * CS, C, cur);
-#pragma unroll
-                for (int j = 0; j <= NV; ++j) cur[j] = b_[b][j] + dec[b] * cur[j];
-                prod *= dec[b];
-            }
+            for (int j = 0; j <= NV; ++j) cur[j] = b_[j] + dec * cur[j];
+            prod *= dec;
         }
         return prod;
     };
@@ -1081,28 +1096,25 @@ void abs_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
     // piece walk from (pw, bb); writes entry states when OUT; returns the sum of the piece's gaps. Slot NV (slot C
     // of the rows) runs the same recurrence: its B state (the v == 1 channel) is weighted by its PW state, the count of
     // kept keys so far (for the u-weighted walks that slot of B is not read).
+    ScanPiece<NV> piece_a, piece_b;
+    piece_a.load(SA, CS, C, glo, ghi);
+    piece_b.load(SB, CS, C, glo, ghi);
     auto walk = [&](float (&pw)[NV + 1], float (&bb)[NV + 1], const bool out) {
         float gsum = 0.f;
-        for (int g0 = glo; g0 < ghi; g0 += SCAN_BATCH) {
-            float a[SCAN_BATCH][NV + 1], b_[SCAN_BATCH][NV + 1], gap[SCAN_BATCH], unused;
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b) {
-                const int g = min(g0 + b, ghi - 1);
-                load_scan_row<NV>(SA + (size_t)g * CS, C, a[b], gap[b]);
-                load_scan_row<NV>(SB + (size_t)g * CS, C, b_[b], unused);
+        for (int i = 0; i < SCAN_BLOCK / SCAN_W; ++i) {
+            const int g = glo + i;
+            if (g >= ghi) break;
+            float a[NV + 1], b_[NV + 1], gap, unused;
+            piece_a.get(i, a, gap);
+            piece_b.get(i, b_, unused);
+            if (out) {
+                store_scan_row<NV>(A + (size_t)g * CS, C, pw);
+                store_scan_row<NV>(B + (size_t)g * CS, C, bb);
             }
 #pragma unroll
-            for (int b = 0; b < SCAN_BATCH; ++b) {
-                const int g = g0 + b;
-                if (g >= ghi) break;
-                if (out) {
-                    store_scan_row<NV>(A + (size_t)g * CS, C, pw);
-                    store_scan_row<NV>(B + (size_t)g * CS, C, bb);
-                }
-#pragma unroll
-                for (int j = 0; j <= NV; ++j) { bb[j] = b_[b][j] + bb[j] + gap[b] * pw[j]; pw[j] += a[b][j]; }
-                gsum += gap[b];
-            }
+            for (int j = 0; j <= NV; ++j) { bb[j] = b_[j] + bb[j] + gap * pw[j]; pw[j] += a[j]; }
+            gsum += gap;
         }
         return gsum;
     };
