@@ -106,17 +106,24 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
  * the same inputs. qlka_abs_bwd_walks tells whether qlka_abs_bwd would sort and walk at this shape (1) or run the
  * dense kernels (0), i.e. whether keeping the sorts pays; qlka_abs_fwd_keep computes what qlka_abs_fwd computes and
  * sets *kept = 1 when it filled the four buffers (0: left untouched, the backward would not use them); after
- * *kept = 1, qlka_abs_bwd_sorted with the same q, k, v computes what qlka_abs_bwd computes without sorting. Same
+ * *kept != 0, qlka_abs_bwd_sorted with the same q, k, v computes what qlka_abs_bwd computes without sorting. Same
  * workspace sizes as qlka_abs_fwd / qlka_abs_bwd.
+ * states (optional, may be NULL; qlka_abs_keep_state_bytes() bytes, 0 when the backward does not walk): the forward
+ * also leaves there the range states and query bounds of its walk over the sorted keys, which the backward's grad_q
+ * walk would compute again (the same range sums, scan and bounds); it sets *kept = 3 when it wrote them (its own walk
+ * ran; a forward on the dense kernels keeps only the sorts). Passing them to qlka_abs_bwd_sorted after *kept = 3
+ * skips one range-sum pass, one scan and one bound search per chunk of the backward, with bit-identical gradients.
  */
 int qlka_abs_bwd_walks(int P, int N, int M);
+size_t qlka_abs_keep_state_bytes(int P, int D, int N, int M, int C);
 int qlka_abs_fwd_keep(const float* q, const float* k, const float* v, float* out_w, float* out_u,
                       int P, int D, int N, int M, int C, int path, float* k_sorted, uint32_t* k_perm,
-                      float* q_sorted, uint32_t* q_perm, int* kept, void* ws, size_t ws_bytes, void* stream);
+                      float* q_sorted, uint32_t* q_perm, void* states, int* kept, void* ws, size_t ws_bytes,
+                      void* stream);
 int qlka_abs_bwd_sorted(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
                         float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C,
                         const float* k_sorted, const uint32_t* k_perm, const float* q_sorted, const uint32_t* q_perm,
-                        void* ws, size_t ws_bytes, void* stream);
+                        const void* states, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * weighted_sgn_sum: out[p,d,m] = sum_n sgn(k[p,d,n] - q[p,d,m]) <v[p,n,:], g[p,m,:]>, with a tie counted +1

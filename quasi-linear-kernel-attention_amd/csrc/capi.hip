@@ -438,11 +438,33 @@ size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {
 
 namespace {
 // Sorted k and q of one call, in caller-owned buffers (k_sorted / q_sorted as sorted keys, k_perm / q_perm as their
-// permutations), so that the backward of the same inputs can skip both sorts.
-struct Presorted { float* ks; uint32_t* kp; float* qs; uint32_t* qp; };
+// permutations), so that the backward of the same inputs can skip both sorts; optionally (states) also the range
+// states and query bounds of the walk over sorted k with v as rows and the sorted q as queries, which the forward
+// computes and the backward's grad_q walk would compute again (same range sums, scan and bounds).
+struct Presorted { float* ks; uint32_t* kp; float* qs; uint32_t* qp; void* states = nullptr; };
 
 Presorted offset(const Presorted& a, size_t p0, int D, int N, int M) {
-    return Presorted{a.ks + p0 * D * N, a.kp + p0 * D * N, a.qs + p0 * D * M, a.qp + p0 * D * M};
+    return Presorted{a.ks + p0 * D * N, a.kp + p0 * D * N, a.qs + p0 * D * M, a.qp + p0 * D * M, nullptr};
+}
+
+// The kept range states of a call over P p: ta and tb ([P*D][G+1][range_stride(C)] floats, the scan's entry states
+// with the segment totals in row G) and qb ([P*D][G] ints), G = range_count(N, C); pointers of chunk [p0, ...).
+size_t kept_state_bytes(int P, int D, int N, int C) {
+    const size_t G = (size_t)range_count(N, C), rows = (size_t)P * D * (G + 1);
+    return 2 * align256(rows * range_stride(C) * sizeof(float)) + align256((size_t)P * D * G * sizeof(int));
+}
+
+void kept_states(void* base, int P, int D, int N, int C, size_t p0, RangeArrays& ra) {
+    const size_t G = (size_t)range_count(N, C), rows = (size_t)P * D * (G + 1);
+    char* b = (char*)base;
+    float* ta = (float*)b;
+    b += align256(rows * range_stride(C) * sizeof(float));
+    float* tb = (float*)b;
+    b += align256(rows * range_stride(C) * sizeof(float));
+    const size_t r0 = p0 * D * (G + 1) * range_stride(C);
+    ra.ta = ta + r0;
+    ra.tb = tb + r0;
+    ra.qb = (int*)b + p0 * D * G;
 }
 
 int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P, int D, int N, int M,
@@ -484,6 +506,7 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         if (keep_sorts) {
             const Presorted ks = offset(*keep, (size_t)p0, D, N, M);
             w.ks = ks.ks; w.kp = ks.kp; w.qs = ks.qs; w.qp = ks.qp;
+            if (keep->states) kept_states(keep->states, P, D, N, C, (size_t)p0, w.ra);   // the scan writes them there
         }
         a = AbsWalkArgs{};
         a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v + (size_t)p0 * N * C; a.u = nullptr;
@@ -525,7 +548,7 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
                                        out_u ? out_u + p * M : nullptr, np, D, M, C, s), "abs reduce");
     };
     if (int e = run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back)) return e;
-    if (keep_sorts) *kept = 1;
+    if (keep_sorts) *kept = keep->states ? 3 : 1;
     return QLKA_OK;
 }
 }  // namespace
@@ -539,9 +562,15 @@ int qlka_abs_fwd(const float* q, const float* k, const float* v, float* out_w, f
 
 int qlka_abs_fwd_keep(const float* q, const float* k, const float* v, float* out_w, float* out_u,
                       int P, int D, int N, int M, int C, int path, float* k_sorted, uint32_t* k_perm,
-                      float* q_sorted, uint32_t* q_perm, int* kept, void* ws, size_t ws_bytes_given, void* stream) {
-    const Presorted keep{k_sorted, k_perm, q_sorted, q_perm};
+                      float* q_sorted, uint32_t* q_perm, void* states, int* kept, void* ws, size_t ws_bytes_given,
+                      void* stream) {
+    const Presorted keep{k_sorted, k_perm, q_sorted, q_perm, states};
     return abs_fwd_impl(q, k, v, out_w, out_u, P, D, N, M, C, path, &keep, kept, ws, ws_bytes_given, stream);
+}
+
+size_t qlka_abs_keep_state_bytes(int P, int D, int N, int M, int C) {
+    if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || C > 128 || N > 131072 || dense_sign(P, N, M)) return 0;
+    return kept_state_bytes(P, D, N, C);
 }
 
 int qlka_abs_bwd_walks(int P, int N, int M) { return (P > 0 && N > 0 && M > 0 && !dense_sign(P, N, M)) ? 1 : 0; }
@@ -599,7 +628,14 @@ int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_
         a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v + p * N * C; a.u = nullptr;
         a.qs = w.qs; a.qp = w.qp; a.Mq = M; a.g = g_w + p * M * C; a.uq = g_u ? g_u + p * M : nullptr;
         a.out_dot = grad_q + p * D * M; a.sign = 1.f; a.P = np; a.D = D; a.C = C;
-        if (int e = abs_walk(a, g_u ? (ABS_DOT | ABS_DOTX1) : ABS_DOT, w.ra, s)) return hip_status(e, "grad_q walk");
+        const int mode_q = g_u ? (ABS_DOT | ABS_DOTX1) : ABS_DOT;
+        if (pre && pre->states) {   // the forward's range states and bounds of this walk: only the walk runs
+            RangeArrays ra = w.ra;
+            kept_states(pre->states, P, D, N, C, p, ra);
+            if (int e = abs_emit(a, mode_q, ra, s)) return hip_status(e, "grad_q walk");
+        } else if (int e = abs_walk(a, mode_q, w.ra, s)) {
+            return hip_status(e, "grad_q walk");
+        }
         // grad_k and grad_v: stream = sorted q with rows g_w (+ scalars g_u), queries = k
         AbsWalkArgs b{};
         b.ks = w.qs; b.kp = w.qp; b.Ns = M; b.w = g_w + p * M * C; b.u = g_u ? g_u + p * M : nullptr;
@@ -630,13 +666,13 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
 int qlka_abs_bwd_sorted(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
                         float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C,
                         const float* k_sorted, const uint32_t* k_perm, const float* q_sorted, const uint32_t* q_perm,
-                        void* ws, size_t ws_bytes_given, void* stream) {
+                        const void* states, void* ws, size_t ws_bytes_given, void* stream) {
     if (!k_sorted || !k_perm || !q_sorted || !q_perm) {
         g_err.clear();
         return fail(QLKA_EINVAL, "the sorted k / q arrays and their permutations must be non-null");
     }
     const Presorted pre{const_cast<float*>(k_sorted), const_cast<uint32_t*>(k_perm), const_cast<float*>(q_sorted),
-                        const_cast<uint32_t*>(q_perm)};
+                        const_cast<uint32_t*>(q_perm), const_cast<void*>(states)};
     return abs_bwd_impl(q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, &pre, ws, ws_bytes_given, stream);
 }
 

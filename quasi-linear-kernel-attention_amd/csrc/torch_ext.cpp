@@ -121,12 +121,16 @@ std::tuple<Tensor, OptTensor, std::vector<Tensor>> abs_forward_keep(const Tensor
     const auto i32 = q.options().dtype(at::kInt);
     srt = {empty_f({d.P, d.D, d.N}, q), at::empty({d.P, d.D, d.N}, i32), empty_f({d.P, d.D, d.M}, q),
            at::empty({d.P, d.D, d.M}, i32)};
+    // the walk's range states and bounds too, so that the backward's grad_q walk skips its range passes
+    Tensor states = at::empty({(int64_t)qlka_abs_keep_state_bytes(d.P, d.D, d.N, d.M, d.C)},
+                              q.options().dtype(at::kByte));
     int kept = 0;
     check_rc(qlka_abs_fwd_keep(fptr(q), fptr(k), fptr(v), fptr(out), fptr(out_u), d.P, d.D, d.N, d.M, d.C, (int)path,
                                fptr(srt[0]), (uint32_t*)srt[1].data_ptr<int32_t>(), fptr(srt[2]),
-                               (uint32_t*)srt[3].data_ptr<int32_t>(), &kept, ws.data_ptr(), (size_t)ws.numel(),
-                               stream_of(q)));
+                               (uint32_t*)srt[3].data_ptr<int32_t>(), states.numel() ? states.data_ptr() : nullptr,
+                               &kept, ws.data_ptr(), (size_t)ws.numel(), stream_of(q)));
     if (!kept) srt.clear();
+    else if (kept & 2) srt.push_back(states);
     return {out, out_u, srt};
 }
 
@@ -159,17 +163,24 @@ std::tuple<Tensor, Tensor, Tensor> abs_backward_sorted(const Tensor& q, const Te
     const Dims d = check_qkv(q, k, v);
     check_grad("g_w", g_w, q, {d.P, d.M, d.C});
     if (g_u.has_value()) check_grad("g_u", *g_u, q, {d.P, d.M});
-    TORCH_CHECK(srt.size() == 4 && srt[0].sizes() == at::IntArrayRef({d.P, d.D, d.N}) &&
+    TORCH_CHECK((srt.size() == 4 || srt.size() == 5) && srt[0].sizes() == at::IntArrayRef({d.P, d.D, d.N}) &&
                     srt[1].sizes() == at::IntArrayRef({d.P, d.D, d.N}) &&
                     srt[2].sizes() == at::IntArrayRef({d.P, d.D, d.M}) &&
                     srt[3].sizes() == at::IntArrayRef({d.P, d.D, d.M}),
                 "sorted arrays do not match q and k");
+    const void* states = nullptr;
+    if (srt.size() == 5) {
+        TORCH_CHECK(srt[4].numel() == (int64_t)qlka_abs_keep_state_bytes(d.P, d.D, d.N, d.M, d.C) &&
+                        srt[4].scalar_type() == at::kByte && srt[4].is_contiguous(),
+                    "kept range states do not match q and k");
+        states = srt[4].data_ptr();
+    }
     c10::DeviceGuard guard(q.device());
     Tensor gq = empty_f({d.P, d.D, d.M}, q), gk = empty_f({d.P, d.D, d.N}, q), gv = empty_f({d.P, d.N, d.C}, q);
     Tensor ws = workspace(qlka_abs_bwd_ws_bytes(d.P, d.D, d.N, d.M, d.C), q);
     check_rc(qlka_abs_bwd_sorted(fptr(q), fptr(k), fptr(v), fptr(g_w), fptr(g_u), fptr(gq), fptr(gk), fptr(gv), d.P,
                                  d.D, d.N, d.M, d.C, fptr(srt[0]), (const uint32_t*)srt[1].data_ptr<int32_t>(),
-                                 fptr(srt[2]), (const uint32_t*)srt[3].data_ptr<int32_t>(), ws.data_ptr(),
+                                 fptr(srt[2]), (const uint32_t*)srt[3].data_ptr<int32_t>(), states, ws.data_ptr(),
                                  (size_t)ws.numel(), stream_of(q)));
     return {gq, gk, gv};
 }
@@ -294,7 +305,8 @@ struct AbsSumFn : public torch::autograd::Function<AbsSumFn> {
         if (path == DIRECT)
             std::tie(gq, gk, gv) = direct_backward(q, k, v, g_w, g_u, 0.0);
         else if (ctx->saved_data["sorted"].toBool())
-            std::tie(gq, gk, gv) = abs_backward_sorted(q, k, v, g_w, g_u, {saved[3], saved[4], saved[5], saved[6]});
+            std::tie(gq, gk, gv) = abs_backward_sorted(q, k, v, g_w, g_u,
+                                                       std::vector<Tensor>(saved.begin() + 3, saved.end()));
         else
             std::tie(gq, gk, gv) = abs_backward(q, k, v, g_w, g_u);
         return {gq, gk, gv, Tensor(), Tensor(), Tensor()};
@@ -324,8 +336,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("g"), "out[p,d,m] = sum_n sgn(k - q) dot(v[n], g[m]), a tie counted +1 (binding.cpp:383-439)");
     m.def("weighted_abs_sum_forward_keep", &abs_forward_keep, py::arg("q"), py::arg("k"), py::arg("v"),
           py::arg("path"), py::arg("full"),
-          "(out_w, out_u or None, [k_sorted, k_perm, q_sorted, q_perm] or []): the forward that keeps its sorts "
-          "when the backward at this shape walks (qlka_abs_fwd_keep)");
+          "(out_w, out_u or None, [k_sorted, k_perm, q_sorted, q_perm (, range states)] or []): the forward that "
+          "keeps its sorts (and, when it walked, its range states) when the backward at this shape walks "
+          "(qlka_abs_fwd_keep)");
     m.def("weighted_abs_sum_backward_sorted", &abs_backward_sorted, py::arg("q"), py::arg("k"), py::arg("v"),
           py::arg("g_w"), py::arg("g_u"), py::arg("srt"),
           "the backward over the sorts a weighted_abs_sum_forward_keep left (qlka_abs_bwd_sorted)");

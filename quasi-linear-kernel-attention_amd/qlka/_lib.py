@@ -32,8 +32,9 @@ _SIGNATURES = {
     "qlka_abs_bwd_ws_bytes": (_c_size, [_c_int] * 5),
     "qlka_abs_bwd": (_c_int, [_c_ptr] * 8 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_abs_bwd_walks": (_c_int, [_c_int] * 3),
-    "qlka_abs_fwd_keep": (_c_int, [_c_ptr] * 5 + [_c_int] * 6 + [_c_ptr] * 5 + [_c_ptr, _c_size, _c_ptr]),
-    "qlka_abs_bwd_sorted": (_c_int, [_c_ptr] * 8 + [_c_int] * 5 + [_c_ptr] * 4 + [_c_ptr, _c_size, _c_ptr]),
+    "qlka_abs_keep_state_bytes": (_c_size, [_c_int] * 5),
+    "qlka_abs_fwd_keep": (_c_int, [_c_ptr] * 5 + [_c_int] * 6 + [_c_ptr] * 6 + [_c_ptr, _c_size, _c_ptr]),
+    "qlka_abs_bwd_sorted": (_c_int, [_c_ptr] * 8 + [_c_int] * 5 + [_c_ptr] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_sgn_fwd_ws_bytes": (_c_size, [_c_int] * 5),
     "qlka_sgn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_direct_fwd": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr]),

@@ -160,14 +160,22 @@ def test_keep_sorts_entries_validate(lib):
     import ctypes
     kept = ctypes.c_int(7)
     # null sorted-array buffers are rejected before any launch, and *kept is cleared
-    rc = lib.qlka_abs_fwd_keep(1, 1, 1, 1, None, 1, 1, 8, 8, 4, -1, None, None, None, None, ctypes.byref(kept),
+    rc = lib.qlka_abs_fwd_keep(1, 1, 1, 1, None, 1, 1, 8, 8, 4, -1, None, None, None, None, None, ctypes.byref(kept),
                                None, 0, None)
     assert rc != 0 and kept.value == 0
     assert b"non-null" in lib.qlka_last_error()
-    rc = lib.qlka_abs_bwd_sorted(1, 1, 1, 1, None, 1, 1, 1, 1, 1, 8, 8, 4, None, None, None, None, None, 0, None)
+    rc = lib.qlka_abs_bwd_sorted(1, 1, 1, 1, None, 1, 1, 1, 1, 1, 8, 8, 4, None, None, None, None, None, None, 0,
+                                 None)
     assert rc != 0 and b"non-null" in lib.qlka_last_error()
     assert lib.qlka_abs_bwd_walks(12, 16384, 16384) == 1
     assert lib.qlka_abs_bwd_walks(512, 65, 65) == 0
+    # the optional range states: ta and tb ([P*D][G+1][C+2] floats) and qb ([P*D][G] ints), 256-byte aligned each;
+    # none where the backward takes the dense kernels
+    def al(x):
+        return (x + 255) // 256 * 256
+    P, D, N, C, G = 12, 64, 16384, 64, 16384 // 64
+    assert lib.qlka_abs_keep_state_bytes(P, D, N, N, C) == 2 * al(P * D * (G + 1) * (C + 2) * 4) + al(P * D * G * 4)
+    assert lib.qlka_abs_keep_state_bytes(512, 32, 65, 65, 32) == 0
     # a handful of keys on either side: the dense route (the walk's segment totals would cost accuracy), unless the
     # cutoff is 0
     assert lib.qlka_abs_bwd_walks(12, 16384, 16) == 0 and lib.qlka_abs_bwd_walks(12, 16, 16384) == 0

@@ -298,6 +298,39 @@ def test_autograd_keeps_sorts_for_backward(dev, shape, full):
     _assert_rel(grads[True][2], wv, nv, "kept-sorts grad_v")
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 1500, 1300, 16),      # one chunk
+                                   (6, 64, 16384, 16384, 32),   # pipelined chunks of 2 p
+                                   (2, 8, 40000, 30000, 65)])   # two-launch scans, two channel slots per lane
+def test_kept_range_states_match_recomputed(dev, shape):
+    # A walking forward that keeps its sorts also leaves its range states and query bounds (a fifth tensor): the
+    # backward over them (its grad_q walk skips its range passes) must equal the backward over the sorts alone, which
+    # recomputes them, bit for bit, with and without g_u; the gradients also against the oracle on a subsample.
+    from oracle import inputs
+    from weighted_abs_sum import _ext
+    P, D, N, M, C = shape
+    print(f"kept range states {shape}", flush=True)
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) % 997, kind="ties")
+    rng = np.random.default_rng(19)
+    g_w = _t(rng.standard_normal((P, M, C)).astype(np.float32), dev)
+    g_u = _t(rng.standard_normal((P, M)).astype(np.float32), dev)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    w, u, srt = _ext.weighted_abs_sum_forward_keep(tq, tk, tv, -1, True)
+    assert len(srt) == 5 and srt[4].dtype == torch.uint8
+    for gu in (g_u, None):
+        with_states = _ext.weighted_abs_sum_backward_sorted(tq, tk, tv, g_w, gu, srt)
+        without = _ext.weighted_abs_sum_backward_sorted(tq, tk, tv, g_w, gu, srt[:4])
+        for name, a, b in zip(("grad_q", "grad_k", "grad_v"), with_states, without):
+            assert torch.equal(a, b), f"{name} (g_u {'given' if gu is not None else 'none'}): kept states differ"
+    bq = inputs.query_subsample(P, M, per_p=4, seed=3)
+    bk = inputs.query_subsample(P, N, per_p=4, seed=4)
+    gq, gk, gv = _ext.weighted_abs_sum_backward_sorted(tq, tk, tv, g_w, g_u, srt)
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward_sub(q, k, v, _np(g_w), _np(g_u), bq, bk)
+    sub = lambda a, idx, axis: np.stack([np.take(a[p], idx[p], axis=axis) for p in range(P)])  # noqa: E731
+    _assert_rel(sub(_np(gq), bq, 1), wq, nq, "kept-states grad_q")
+    _assert_rel(sub(_np(gk), bk, 1), wk, nk, "kept-states grad_k")
+    _assert_rel(sub(_np(gv), bk, 0), wv, nv, "kept-states grad_v")
+
+
 def test_full_backward_only_u(dev):
     # out_w unused: g_w is None inside the autograd Function and becomes zeros (ops.py:99-101)
     from weighted_abs_sum import weighted_abs_sum_full
