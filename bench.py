@@ -266,7 +266,7 @@ def _cpu_model():
     return "unknown"
 
 
-STAGES = ("lds_radix_sort", "merge_runs", "group_queries", "query_bounds", "fill_zero", "lap_range_sums",
+STAGES = ("lds_radix_sort", "lds_count_sort", "merge_runs", "group_queries", "query_bounds", "fill_zero", "lap_range_sums",
           "lap_range_scan", "lap_range_walk", "abs_range_sums", "abs_range_scan", "abs_range_walk", "u_to_query",
           "u_sum", "slab_reduce")
 DENSE_STAGES = ("direct_fwd", "direct_sign")
@@ -283,7 +283,7 @@ def kernel_algorithmic_bytes(name):
     table = {
         "lap_range_walk": walk, "abs_range_walk": walk,
         "slab_reduce": 4.0 * P * M * (D * C + D + C + 1),
-        "lds_radix_sort": 12.0 * S * N,
+        "lds_radix_sort": 12.0 * S * N, "lds_count_sort": 12.0 * S * N,
         "lap_range_sums": 4.0 * S * (2 * N + N * C), "abs_range_sums": 4.0 * S * (2 * N + N * C),
         "group_queries": 12.0 * S * M,
     }

@@ -180,6 +180,16 @@ static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int 
     return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, qshift, S, N, M, C, st), "query bounds");
 }
 
+// The prep of a forward walk that keeps no sorts: the k sort, then the query side (group_q). (One kernel doing both,
+// the grouping in the sort's workgroup against the sorted keys still in LDS, measured slower: 1.760 vs 1.748 ms per
+// Laplace call. Beside the previous chunk's reduce it holds its CU slots for the grouping too, while the grouping as
+// its own launch mostly waits for the reduce to drain and then runs alone.)
+static int sort_k_group_q(const float* k, const float* q, SortedWs& w, float qshift, int S, int N, int M, int C,
+                          hipStream_t st) {
+    if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
+    return group_q(q, w, qshift, S, N, M, C, st);
+}
+
 // ---- overlap of the query side (q sort, range boundaries) with the key side (range summaries, scan)
 // The two sides read and write disjoint parts of the workspace and both need only the sorted keys. The key side runs
 // on the caller's stream, the query side on a side stream of the calling thread (one per device, created on first
@@ -401,10 +411,7 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
     auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
         const size_t p = (size_t)p0;
-        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s),
-                               "segmented sort of k"))
-            return e;
-        return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
+        return sort_k_group_q(k + p * D * N, q + p * D * M, w, 0.f, np * D, N, M, C, s);
     };
     auto main = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
@@ -526,10 +533,7 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
                 return e;
             return hip_status(range_bounds(a, w.ra.qb, s), "query bounds");
         }
-        if (int e = hip_status(seg_sort(k + p * D * N, w.ks, w.kp, np * D, N, w.sort_scratch, s),
-                               "segmented sort of k"))
-            return e;
-        return group_q(q + p * D * M, w, 0.f, np * D, N, M, C, s);
+        return sort_k_group_q(k + p * D * N, q + p * D * M, w, 0.f, np * D, N, M, C, s);
     };
     auto main = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w; AbsWalkArgs a;
@@ -920,10 +924,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         const bool lap_masked = kind == LAYER_ADD_LAPLACE && masked;
         if (lap_masked)
             if (int e = hip_status(mask_keys(kc, keepc, L.kmask, np, D, N, s), "masked keys")) return e;
-        if (int e = hip_status(seg_sort(lap_masked ? L.kmask : kc, L.op.ks, L.op.kp, np * D, N, L.op.sort_scratch, s),
-                               "segmented sort of k"))
-            return e;
-        return group_q(qc, L.op, 0.f, np * D, N, M, C, s);
+        return sort_k_group_q(lap_masked ? L.kmask : kc, qc, L.op, 0.f, np * D, N, M, C, s);
     };
     // the abs walk's arguments of a chunk (add_riesz, add_bump)
     auto abs_args = [&](const SortedWs& w, const float* vc, const uint8_t* keepc, int np) {

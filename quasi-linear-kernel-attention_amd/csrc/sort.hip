@@ -1,10 +1,12 @@
 // Stage 1 of the hot path: per-segment stable ascending sort of fp32 keys with a uint32 permutation payload.
 //
 // Replaces the reference's CUB segmented radix sort + iota (Weighted_Abs_Sum/csrc/sort_utils.cu:17-117,
-// Weighted_Laplace_Sum/csrc/sort_utils.cu:14-126) with two gfx950 kernels of our own:
-//  * lds_radix_sort: one workgroup sorts one run of up to 16384 keys entirely in LDS (keys + indices = 128 KB of the
-//    160 KB LDS), 4 LSD passes of 8-bit digits. Stable ranking inside a wave uses 8 ballots to find the lanes that
-//    share a digit (no match instruction on CDNA), per-wave digit counters in LDS, and a digit-major exclusive scan.
+// Weighted_Laplace_Sum/csrc/sort_utils.cu:14-126) with gfx950 kernels of our own:
+//  * lds_count_sort (runs of 4097 .. 16384 keys): one workgroup sorts one run entirely in LDS, 8 LSD passes of 4-bit
+//    digits ranked with per-thread digit counters (no ballots); see the kernel.
+//  * lds_radix_sort (runs of up to 4096 keys): one workgroup sorts one run entirely in LDS, 4 LSD passes of 8-bit
+//    digits. Stable ranking inside a wave uses 8 ballots to find the lanes that share a digit (no match instruction on
+//    CDNA), per-wave digit counters in LDS, and a digit-major exclusive scan.
 //  * merge_runs: for segments longer than one LDS run, stable merge-path merges of sorted runs (ties keep the left
 //    run first), ping-ponging between two scratch buffers; the last pass writes floats + perm.
 // Output contract: sorted[i] are the keys in stable ascending order (-0.0 written as +0.0), perm[i] the index within
@@ -144,6 +146,164 @@ void lds_radix_sort(const float* __restrict__ in1, const int seg_len, const int 
     }
 }
 
+// Counter-based stable LDS sort for runs of up to THREADS * 16 keys (the long runs: 8192 and 16384 keys). Thread t
+// owns the 16 consecutive positions 16t .. 16t + 15 of the current order ("blocked"). Each of 8 LSD passes over 4-bit
+// digits:
+//  1. every thread counts its items per digit in its own column of a [16 digits][THREADS] counter table (LDS
+//     atomics that return the old count, so an item also learns how many of the thread's earlier items share its
+//     digit; a column has one writer, so the counts do not depend on timing);
+//  2. one exclusive scan of the table in digit-major order (each thread rakes 16 consecutive counters, a workgroup
+//     scan joins the threads) turns every counter into the first output slot of its (digit, thread);
+//  3. item rank = its (digit, thread) slot + its count among the thread's earlier items: stable, since positions are
+//     ordered thread-major and, within a thread, item by item;
+//  4. keys and indices are scattered to their ranks and read back blocked for the next pass.
+// No ballots: about 8 VALU instructions per item and pass for the ranking, against about 98 for the 8-ballot digit
+// match of lds_radix_sort, which made that kernel VALU-bound. The table lives in the key array while the keys are in
+// registers (steps 1-3). LDS arrays are padded by one word per 16, so a blocked access (thread t at 16t + j) and a
+// counter rake hit 64 different banks.
+constexpr int CS_ITEMS = 16;
+constexpr int CS_BITS = 4;
+constexpr int CS_DIGITS = 1 << CS_BITS;
+__device__ __forceinline__ int cs_pad(int i) { return i + (i >> 4); }
+
+template <int THREADS>
+struct CountSortLds {
+    uint32_t key[THREADS * (CS_ITEMS + 1)];    // padded keys; the digit counters during ranking
+    uint32_t idx[THREADS * (CS_ITEMS + 1)];    // padded positions in the run
+    uint32_t wsum[THREADS / WAVE];
+};
+static_assert(CS_DIGITS <= CS_ITEMS, "the digit counters must fit the key array");
+
+// Exclusive workgroup scan of one value per thread (wave scan, then the waves' totals through LDS).
+template <int THREADS>
+__device__ __forceinline__ uint32_t cs_block_scan(const uint32_t x, uint32_t* wsum) {
+    const int lane = lane_id(), w = threadIdx.x / WAVE;
+    uint32_t incl = x;
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)incl, off, WAVE);
+        if (lane >= off) incl += y;
+    }
+    if (lane == WAVE - 1) wsum[w] = incl;
+    __syncthreads();
+    uint32_t base = 0;
+#pragma unroll
+    for (int i = 0; i < THREADS / WAVE; ++i) base += (i < w) ? wsum[i] : 0u;
+    return base + incl - x;
+}
+
+// The run's sort in LDS: on return sm.key / sm.idx hold the sorted run at padded positions (ordered keys and positions
+// in the run). All THREADS threads of the workgroup take part.
+template <int THREADS>
+__device__ __forceinline__ void count_sort_run(CountSortLds<THREADS>& sm, const float* __restrict__ src, const int len)
+{
+    const int t = threadIdx.x;
+    // striped loads (coalesced, all in flight) into the padded LDS order; pads sort after every key
+    {
+        float f[CS_ITEMS];
+#pragma unroll
+        for (int r = 0; r < CS_ITEMS; ++r) f[r] = src[min(t + r * THREADS, len - 1)];
+#pragma unroll
+        for (int r = 0; r < CS_ITEMS; ++r) {
+            const int i = t + r * THREADS;
+            sm.key[cs_pad(i)] = float_to_ordered(f[r]) | ((i < len) ? 0u : 0xffffffffu);
+            sm.idx[cs_pad(i)] = (uint32_t)i;
+        }
+    }
+
+    uint32_t* const cnt = sm.key;
+#pragma unroll 1
+    for (int shift = 0; shift < 32; shift += CS_BITS) {
+        __syncthreads();                                  // the previous scatter (or the load) is complete
+        uint32_t key[CS_ITEMS];
+#pragma unroll
+        for (int j = 0; j < CS_ITEMS; ++j) key[j] = sm.key[cs_pad(CS_ITEMS * t + j)];
+        __syncthreads();                                  // every thread holds its keys: the key array is free
+        // 1. this thread's column of the counter table, and each item's count among the thread's earlier items
+#pragma unroll
+        for (int d = 0; d < CS_DIGITS; ++d) cnt[cs_pad(d * THREADS + t)] = 0u;
+        uint32_t rank[CS_ITEMS];
+#pragma unroll
+        for (int j = 0; j < CS_ITEMS; ++j) {
+            const int d = (int)((key[j] >> shift) & (CS_DIGITS - 1));
+            rank[j] = atomicAdd(&cnt[cs_pad(d * THREADS + t)], 1u);
+        }
+        __syncthreads();
+        // 2. exclusive scan of the table in digit-major order: thread t rakes counters 16t .. 16t + 15
+        {
+            uint32_t s = 0;
+#pragma unroll
+            for (int i = 0; i < CS_ITEMS; ++i) s += cnt[cs_pad(CS_ITEMS * t + i)];
+            uint32_t base = cs_block_scan<THREADS>(s, sm.wsum);
+#pragma unroll
+            for (int i = 0; i < CS_ITEMS; ++i) {
+                const uint32_t c = cnt[cs_pad(CS_ITEMS * t + i)];
+                cnt[cs_pad(CS_ITEMS * t + i)] = base;
+                base += c;
+            }
+        }
+        __syncthreads();
+        // 3. ranks
+#pragma unroll
+        for (int j = 0; j < CS_ITEMS; ++j) {
+            const int d = (int)((key[j] >> shift) & (CS_DIGITS - 1));
+            rank[j] += cnt[cs_pad(d * THREADS + t)];
+        }
+        uint32_t idx[CS_ITEMS];
+#pragma unroll
+        for (int j = 0; j < CS_ITEMS; ++j) idx[j] = sm.idx[cs_pad(CS_ITEMS * t + j)];
+        __syncthreads();                                  // every rank and index read: both arrays take the scatter
+        // 4. scatter
+#pragma unroll
+        for (int j = 0; j < CS_ITEMS; ++j) {
+            sm.key[cs_pad((int)rank[j])] = key[j];
+            sm.idx[cs_pad((int)rank[j])] = idx[j];
+        }
+    }
+    __syncthreads();
+}
+
+// Only the keys and their counts stay in registers through a pass (the indices are read just before the scatter):
+// 103 VGPRs, so that the 16 waves of a workgroup leave room in each SIMD's registers for the waves of the previous
+// chunk's slab reduce, which runs beside the sort (at 127 VGPRs no reduce wave fitted beside it and each op took
+// 0.02-0.04 ms longer).
+template <int THREADS>
+__global__ __launch_bounds__(THREADS)
+void lds_count_sort(const float* __restrict__ in1, const int seg_len, const int run_len, const int runs_per_seg,
+                    float* __restrict__ out_keys1, uint32_t* __restrict__ out_perm1,
+                    uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_idx,
+                    const int blocks1, const float* __restrict__ in2, float* __restrict__ out_keys2,
+                    uint32_t* __restrict__ out_perm2)
+{
+    const bool second = (int)blockIdx.x >= blocks1;
+    const int bid = second ? (int)blockIdx.x - blocks1 : (int)blockIdx.x;
+    const float* in = second ? in2 : in1;
+    float* out_keys = second ? out_keys2 : out_keys1;
+    uint32_t* out_perm = second ? out_perm2 : out_perm1;
+    __shared__ CountSortLds<THREADS> sm;
+
+    const int seg   = bid / runs_per_seg;
+    const int run   = bid - seg * runs_per_seg;
+    const int start = run * run_len;
+    const int len   = min(run_len, seg_len - start);
+    const size_t seg_off = (size_t)seg * seg_len;
+    count_sort_run<THREADS>(sm, in + seg_off + start, len);
+
+    // the sorted run is in LDS: striped, coalesced stores
+    const int t = threadIdx.x;
+    if (runs_per_seg == 1) {
+        for (int i = t; i < len; i += THREADS) {
+            out_keys[seg_off + i] = ordered_to_float(sm.key[cs_pad(i)]);
+            out_perm[seg_off + i] = (uint32_t)start + sm.idx[cs_pad(i)];
+        }
+    } else {
+        for (int i = t; i < len; i += THREADS) {
+            run_keys[seg_off + start + i] = sm.key[cs_pad(i)];
+            run_idx[seg_off + start + i]  = (uint32_t)start + sm.idx[cs_pad(i)];
+        }
+    }
+}
+
 // One stable merge pass: runs of `width` become runs of 2*width (A = the left run wins ties). A workgroup owns
 // MERGE_TILE consecutive outputs of one pair of runs:
 //  1. merge_partition, a launch before, finds where every tile starts on the merge path (the number of A elements
@@ -279,6 +439,16 @@ static void launch_lds(const float* in, int S, int L, int run_len, int runs, flo
                        in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
 }
 
+template <int THREADS>
+static void launch_cs(const float* in, int S, int L, int run_len, int runs, float* ok, uint32_t* op,
+                      uint32_t* rk, uint32_t* ri, hipStream_t st, const float* in2 = nullptr, float* ok2 = nullptr,
+                      uint32_t* op2 = nullptr) {
+    StageTimer t("lds_count_sort", st);
+    const int blocks1 = S * runs;
+    hipLaunchKernelGGL((lds_count_sort<THREADS>), dim3(in2 ? 2 * blocks1 : blocks1), dim3(THREADS), 0, st,
+                       in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
+}
+
 static inline int merge_tiles(int L) { return (L + MERGE_TILE - 1) / MERGE_TILE; }
 
 size_t seg_sort_scratch_bytes(int S, int L) {
@@ -300,9 +470,11 @@ static int lds_sort(const float* in, float* out_keys, uint32_t* out_perm, const 
     else if (L <= 1024)  QLKA_LDS(4, 4);
     else if (L <= 2048)  QLKA_LDS(8, 4);
     else if (L <= 4096)  QLKA_LDS(16, 4);
-    else if (L <= 8192)  QLKA_LDS(16, 8);
-    else                 QLKA_LDS(16, 16);
 #undef QLKA_LDS
+    else if (L <= 8192)  launch_cs<512>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st, in2, out_keys2,
+                                        out_perm2);
+    else                 launch_cs<1024>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st, in2, out_keys2,
+                                         out_perm2);
     return (int)hipGetLastError();
 }
 
@@ -324,7 +496,7 @@ int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L,
     uint32_t* k1 = i0 + n;
     uint32_t* i1 = k1 + n;
     const int runs = (L + LDS_SORT_MAX - 1) / LDS_SORT_MAX;
-    launch_lds<16, 16>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
+    launch_cs<1024>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
     int err = (int)hipGetLastError();
     if (err) return err;
     const int bps = merge_tiles(L);

@@ -34,6 +34,7 @@
 // fixed order); scalar emissions (v == 1 sums, dots, ranks) have exactly one writer each and are plain stores.
 #include "qlka_common.h"
 #include "qlka_internal.h"
+#include "group_device.h"
 
 namespace qlka {
 
@@ -914,139 +915,19 @@ int query_bounds(const float* ks, const float* qs, int* qb, float qshift, int S,
     return query_bounds_sets(ks, qs, qbs, sh, 1, S, Ns, Mq, C, st);
 }
 
-// Queries grouped by key chunk, the forward walks' alternative to sorting them. The sorted keys of a segment fall into
-// chunks of CH = RK / 4 (four per key range, the walks' emission chunks); a query's bucket is the chunk holding the
-// first key >= q + qshift, b = #{c : klast_c < q + qshift} (Gc = ceil(Ns / CH) when it is above every key). Queries
-// come out in bucket order, so each range owns a contiguous run (range g: buckets 4g .. 4g + 3, the last range also
-// bucket Gc) and, inside it, its queries come chunk by chunk, which is all a walk needs of their order: it ranks each
-// query inside the range itself, and a block of 64 queries then covers consecutive chunks as with sorted queries.
-// qb[g] = #queries of ranges <= g, as query_bounds writes it. One workgroup per segment: the Gc chunk boundaries go to
-// LDS, every query finds its bucket by binary search there and counts it with an LDS atomic; an exclusive scan of the
-// Gc + 1 counts gives the bucket offsets; returning LDS atomics then hand out slots in each bucket, staged in LDS for
-// coalesced stores when the segment fits. The order inside a bucket is the order in which the atomics return, which
-// is not fixed; no output of any walk depends on it (each query's sums come from its own rank and go to its own index,
-// directly or through qp).
-constexpr int GQ_T = 1024;         // threads per workgroup
-constexpr int GQ_STAGE = 16384;    // longest segment staged in LDS (its values and indices: 128 KB)
-constexpr int GQ_STAGE_MAXB = 2048;        // most chunk buckets of a staged segment
-
-template <int MAXB, int STAGE>
-struct GroupLds {
-    float bnd[MAXB];
-    float rb[MAXB / 4];
-    int off[MAXB + 1];
-    int wsum[GQ_T / WAVE];
-    float sv[STAGE];
-    uint32_t si[STAGE];
-};
-
-// Bucket of x among the nb chunk boundaries in LDS: #{c : bnd[c] < x} (bnd ascending). A branch-free descent over
-// the range boundaries rb (the last key of each range, in an array of their own so that the descent's reads spread
-// over the LDS banks) finds the range, then the range's first three chunk boundaries are compared at once; the NI
-// searches of a thread run interleaved step by step, so that their LDS reads overlap.
-template <int NI>
-__device__ __forceinline__ void buckets(const float* bnd, const float* rb, const int nb, const float (&x)[NI],
-                                        int (&b)[NI]) {
-    const int ng = (nb + 3) >> 2;
-    int g[NI];
-#pragma unroll
-    for (int j = 0; j < NI; ++j) g[j] = 0;
-    int step = 1;
-    while (step * 2 <= ng) step *= 2;
-    for (; step >= 1; step >>= 1) {
-        float y[NI];
-#pragma unroll
-        for (int j = 0; j < NI; ++j) y[j] = rb[min(g[j] + step, ng) - 1];
-#pragma unroll
-        for (int j = 0; j < NI; ++j) g[j] += (g[j] + step <= ng && y[j] < x[j]) ? step : 0;
-    }
-#pragma unroll
-    for (int j = 0; j < NI; ++j) {
-        const int c0 = min(4 * g[j], nb - 1);
-        const float y0 = bnd[c0], y1 = bnd[min(c0 + 1, nb - 1)], y2 = bnd[min(c0 + 2, nb - 1)];
-        b[j] = 4 * g[j];
-        if (g[j] < ng) b[j] += (y0 < x[j]) + (c0 + 1 < nb && y1 < x[j]) + (c0 + 2 < nb && y2 < x[j]);
-        else b[j] = nb;
-    }
-}
-
-// Exclusive scan of off[0..n) in place by the whole workgroup (thread t owns a contiguous piece), then the range
-// bounds: qb[g] = offset of bucket 4 (g + 1), or of bucket n - 1 = Gc for the last range.
-__device__ __forceinline__ void group_scan(int* off, int* wsum, const int n, int* qbs) {
-    const int tid = threadIdx.x;
-    const int E = (n + GQ_T - 1) / GQ_T;
-    const int e0 = min(tid * E, n), e1 = min(e0 + E, n);
-    int own = 0;
-    for (int c = e0; c < e1; ++c) own += off[c];
-    int incl = own;
-#pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        const int y = __shfl_up(incl, d, WAVE);
-        if (lane_id() >= d) incl += y;
-    }
-    if (lane_id() == WAVE - 1) wsum[tid / WAVE] = incl;
-    __syncthreads();
-    int base = incl - own;
-    for (int w = 0; w < tid / WAVE; ++w) base += wsum[w];
-    for (int c = e0; c < e1; ++c) {
-        const int cnt = off[c];
-        off[c] = base;
-        if (c > 0 && ((c & 3) == 0 || c == n - 1)) qbs[(c - 1) >> 2] = base;
-        base += cnt;
-    }
-    __syncthreads();
-}
-
-// Segments of up to GQ_STAGE queries: a thread's GQ_I queries stay in registers from the load to the placement (one
-// load and one search each), and the grouped segment is staged in LDS and stored coalesced.
-constexpr int GQ_I = GQ_STAGE / GQ_T;
-
 template <int CH>
 __global__ __launch_bounds__(GQ_T)
 void group_queries_staged(const float* __restrict__ ks, const float* __restrict__ q, float* __restrict__ qs,
                           uint32_t* __restrict__ qp, int* __restrict__ qb, const float qshift, const int Ns,
                           const int Mq, const int G, const int Gc)
 {
-    __shared__ GroupLds<GQ_STAGE_MAXB, GQ_STAGE> sm;
-    const int s = blockIdx.x, tid = threadIdx.x;
+    __shared__ GroupTables tb;
+    __shared__ float sv[GQ_STAGE];
+    __shared__ uint32_t si[GQ_STAGE];
+    const int s = blockIdx.x;
     const float* kseg = ks + (size_t)s * Ns;
-    const float* qseg = q + (size_t)s * Mq;
-    float x[GQ_I], xs[GQ_I];
-#pragma unroll
-    for (int j = 0; j < GQ_I; ++j) x[j] = qseg[min(tid + j * GQ_T, Mq - 1)];   // clamped: all loads in flight
-    for (int c = tid; c < Gc; c += GQ_T) {
-        const float y = kseg[min(Ns, (c + 1) * CH) - 1];
-        sm.bnd[c] = y;
-        if ((c & 3) == 3 || c == Gc - 1) sm.rb[c >> 2] = y;
-    }
-    for (int c = tid; c <= Gc; c += GQ_T) sm.off[c] = 0;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < GQ_I; ++j) xs[j] = x[j] + qshift;
-    int b[GQ_I];
-    buckets<GQ_I>(sm.bnd, sm.rb, Gc, xs, b);
-#pragma unroll
-    for (int j = 0; j < GQ_I; ++j)
-        if (tid + j * GQ_T < Mq) atomicAdd(&sm.off[b[j]], 1);
-    __syncthreads();
-    group_scan(sm.off, sm.wsum, Gc + 1, qb + (size_t)s * G);
-#pragma unroll
-    for (int j = 0; j < GQ_I; ++j) {
-        const int i = tid + j * GQ_T;
-        if (i < Mq) {
-            const int pos = atomicAdd(&sm.off[b[j]], 1);
-            sm.sv[pos] = x[j];
-            sm.si[pos] = (uint32_t)i;
-        }
-    }
-    __syncthreads();
-    float* qso = qs + (size_t)s * Mq;
-    uint32_t* qpo = qp + (size_t)s * Mq;
-#pragma unroll
-    for (int j = 0; j < GQ_I; ++j) {
-        const int i = tid + j * GQ_T;
-        if (i < Mq) { qso[i] = sm.sv[i]; qpo[i] = sm.si[i]; }
-    }
+    group_segment<CH>([&](int i) { return kseg[i]; }, q + (size_t)s * Mq, qs + (size_t)s * Mq, qp + (size_t)s * Mq,
+                      qb + (size_t)s * G, qshift, Ns, Mq, Gc, tb, sv, si);
 }
 
 bool group_fits(int Ns, int Mq, int C) {
