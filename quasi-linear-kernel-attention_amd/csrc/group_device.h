@@ -1,5 +1,5 @@
-// Device code of the query grouping (the forward walks' alternative to sorting the queries), shared by its own kernel
-// (walks.hip) and by the kernel that sorts a segment's keys and groups its queries in one workgroup (sort.hip).
+// Device code of the query grouping, the forward walks' alternative to sorting the queries (group_queries_staged in
+// walks.hip), as a workgroup-level function that takes its LDS from the caller.
 #pragma once
 
 #include "qlka_common.h"
@@ -23,7 +23,7 @@ constexpr int GQ_STAGE = 16384;    // longest segment staged in LDS (its values 
 constexpr int GQ_STAGE_MAXB = 2048;        // most chunk buckets of a staged segment
 
 // The grouping's LDS tables (chunk and range boundaries, bucket offsets); the staging of the grouped segment (values and
-// indices, GQ_STAGE each) is passed separately, so that a kernel can place it over LDS it no longer needs.
+// indices, GQ_STAGE each) is passed separately.
 struct GroupTables {
     float bnd[GQ_STAGE_MAXB];
     float rb[GQ_STAGE_MAXB / 4];
