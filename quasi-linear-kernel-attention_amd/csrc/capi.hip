@@ -40,15 +40,17 @@ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 //   Laplace forward  L <= B    (its exp per term: about even at L = 700 for P = 12)
 //   backward, sgn    L <= B, or L <= 5B/4 when P * ceil(L / 32) >= 512 workgroups fill the GPU (at L = 600: dense
 //                    0.30 vs 0.44 ms at P = 32, but 0.22 vs 0.20 at P = 12)
-// With B > 0, segments of at most FEW_KEYS keys also go dense whatever the other side's length: the abs walk's row
-// emission adds the segment totals as -Btot - (q - k_max) Wtot, whose fp32 rounding is about eps * sum_n (k_max - k_n)
-// |w_n|; with a handful of keys that can exceed 1e-5 of the sum of |term| (2 keys, one heavy near q and one light far
-// away: 1.8e-5 measured), while the dense kernels sum the terms themselves. (The backward's second walk takes the
-// queries as its keys, so there the fewer of N and M counts.) The Laplace walk has no totals and keeps its rule.
+// Segments of at most FEW_KEYS keys go dense whatever the other side's length, the cutoff (B = 0 included) and the
+// pinned path: the abs walk's row emission adds the segment totals as -Btot - (q - k_max) Wtot, whose fp32 rounding
+// is about eps * sum_n (k_max - k_n) |w_n|; with a handful of keys that can exceed 1e-5 of the sum of |term| (2 keys,
+// one heavy near q and one light far away: 1.8e-5 measured), while the dense kernels sum the terms themselves. (The
+// backward's second walk takes the queries as its keys, so there the fewer of N and M counts.) The Laplace walk has
+// no totals and keeps its rule. The routing does not depend on the path: path 1 only adds the reference's error for
+// max(N, M) > 4096.
 constexpr int FEW_KEYS = 16;
 std::atomic<int> g_direct_max{512};
 inline int64_t direct_base() { return g_direct_max.load(std::memory_order_relaxed); }
-inline bool few_keys(int keys) { return direct_base() > 0 && keys <= FEW_KEYS; }
+inline bool few_keys(int keys) { return keys <= FEW_KEYS; }
 inline bool dense_abs_fwd(int N, int M) { return std::max(N, M) <= 2 * direct_base() || few_keys(N); }
 inline bool dense_laplace_fwd(int N, int M) { return std::max(N, M) <= direct_base(); }
 inline bool dense_sign(int P, int N, int M) {
@@ -435,8 +437,15 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
 // ---------------------------------------------------------------------------------------------------- abs forward
 static WsSpec abs_fwd_spec(int P, int D, int N, int M, int C, bool full) { return WsSpec{P, D, N, M, C, N, M, full}; }
 
+// The dense route's only workspace: the sort scratch of sorts kept for a backward that walks (none when the backward
+// is dense too, and none for segments of one LDS run).
+static size_t abs_dense_ws(int P, int pc, int D, int N, int M, int C) {
+    return dense_sign(P, N, M) ? 0 : ws_part(abs_fwd_spec(pc, D, N, M, C, true), 4);
+}
+
 size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
+    if (dense_abs_fwd(N, M)) return budget_bytes(P, [&](int pc) { return abs_dense_ws(P, pc, D, N, M, C); });
     auto b1 = [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); };
     return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, M), b1), b1);
 }
@@ -487,18 +496,17 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
     if (path == 1 && std::max(N, M) > 4096)
         return fail(QLKA_EINVAL, "fused path pinned but unavailable: needs max(N,M) <= 4096 and the "
                                  "bucket's shared memory to fit this device");
-    // the workspace is sized for the _full op (an upper bound of the plain one), so one size serves both
-    auto b1 = [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); };
-    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, M), b1);
-    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     hipStream_t st = (hipStream_t)stream;
     const bool keep_sorts = keep && !dense_sign(P, N, M);   // the backward will walk: hand it the sorts
-    if (path == -1 && dense_abs_fwd(N, M)) {
+    if (dense_abs_fwd(N, M)) {
         if (keep_sorts) {
-            const int e = for_chunks(P, pl.pc, [&](int p0, int np) {
+            auto db = [&](int pc) { return abs_dense_ws(P, pc, D, N, M, C); };
+            const int pc = fit_chunk(P, ws_bytes_given, db);
+            if (int e = check_ws(ws, ws_bytes_given, db(pc))) return e;
+            const int e = for_chunks(P, pc, [&](int p0, int np) {
                 const Presorted ks = offset(*keep, (size_t)p0, D, N, M);
-                SortedWs w = carve(ws, abs_fwd_spec(np, D, N, M, C, true));
-                w.ks = ks.ks; w.kp = ks.kp; w.qs = ks.qs; w.qp = ks.qp;
+                SortedWs w{};
+                w.ks = ks.ks; w.kp = ks.kp; w.qs = ks.qs; w.qp = ks.qp; w.sort_scratch = ws;
                 const size_t p = (size_t)p0;
                 return sort_both(q + p * D * M, k + p * D * N, w, np * D, N, M, st); });
             if (e) return e;
@@ -506,6 +514,10 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         }
         return hip_status(direct_fwd(0, q, k, v, out_w, out_u, P, D, N, M, C, st), "abs direct sum");
     }
+    // the workspace is sized for the _full op (an upper bound of the plain one), so one size serves both
+    auto b1 = [&](int pc) { return ws_bytes(abs_fwd_spec(pc, D, N, M, C, true)); };
+    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, M), b1);
+    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
     const int mode = out_u ? (ABS_ROW | ABS_ONES) : ABS_ROW;
     // the chunk's workspace view, with the sorted arrays in the caller's buffers when the sorts are kept
     auto view = [&](int p0, int np, void* buf, SortedWs& w, AbsWalkArgs& a) {
@@ -899,6 +911,16 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         npc = n_pad ? n_pad + p : nullptr; keepc = keep ? keep + p * N : nullptr; outc = out + p * M * C;
     };
     const bool bump = kind == LAYER_ADD_BUMP;
+    if (kind == LAYER_ADD_RIESZ && keep == nullptr && few_keys(N))   // the abs sums dense (few_keys), then the epilogue
+        return for_chunks(P, pl.pc, [&](int p0, int np) {
+            const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
+            chunk_in(p0, qc, kc, vc, npc, keepc, outc);
+            LayerWs L = carve_layer(kind, ws, WsSpec{np, D, N, M, C, N, M, true});
+            if (int e = riesz_prefix(kc, vc, nullptr, L.pre, np, D, N, C, st)) return hip_status(e, "riesz prefixes");
+            if (int e = direct_fwd(0, qc, kc, vc, L.w[0], L.u[0], np, D, N, M, C, st))
+                return hip_status(e, "abs direct sum");
+            return hip_status(layer_epilogue(kind, false, qc, npc, L.w[0], L.u[0], nullptr, nullptr, nullptr, nullptr,
+                                             L.pre, L.qt, outc, np, D, N, M, C, st), "layer epilogue"); });
     if (bump && !reduce_folds_epilogue(M, C))   // three walks and reduces over one slab per chunk: chunks in order
         return for_chunks(P, pl.pc, [&](int p0, int np) {
             const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
@@ -924,6 +946,14 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         const bool lap_masked = kind == LAYER_ADD_LAPLACE && masked;
         if (lap_masked)
             if (int e = hip_status(mask_keys(kc, keepc, L.kmask, np, D, N, s), "masked keys")) return e;
+        if (kind == LAYER_ADD_RIESZ && masked) {
+            // the abs walk's distances and totals between kept keys only (fill_masked_keys); the grouping then runs on
+            // the filled keys, as the walk ranks queries among them
+            if (int e = hip_status(seg_sort(kc, L.op.ks, L.op.kp, np * D, N, L.op.sort_scratch, s), "segmented sort of k"))
+                return e;
+            if (int e = hip_status(fill_masked_keys(L.op.ks, L.op.kp, keepc, np, D, N, s), "masked keys")) return e;
+            return group_q(qc, L.op, 0.f, np * D, N, M, C, s);
+        }
         return sort_k_group_q(lap_masked ? L.kmask : kc, qc, L.op, 0.f, np * D, N, M, C, s);
     };
     // the abs walk's arguments of a chunk (add_riesz, add_bump)

@@ -17,8 +17,10 @@
 // and u then already run over the kept keys only, which is what the n_pad terms above remove from the reference's
 // sums over zeroed keys (a zeroed key adds e^{-|q_d|}, |q_d| or max(0, 1 - |q_d|) per feature to u). So add_laplace
 // and add_bump drop their n_pad term, and add_riesz, whose u lost n_pad |q|_1, keeps the reference's algebra as
-//   den = (|q|_1 + EPS) * S + sum_kept |k_n|_1 - u - n_pad (|q|_1 + EPS),  n_pad = N - #kept,
-// with sum_n v and sum_n |k_n|_1 v_n over the kept keys.
+//   den = (|q|_1 + EPS) * (S - n_pad) + sum_kept |k_n|_1 - u,  n_pad = N - #kept,
+// with sum_n v and sum_n |k_n|_1 v_n over the kept keys. S - n_pad is an exact integer in fp32; written as
+// (|q|_1 + EPS) S - n_pad (|q|_1 + EPS) it would be the difference of two products that cancel when most keys are
+// masked (a short document in a long padded batch: 9240 - 9236 at S = 4200 with 2 kept keys, 1e-4 of den lost).
 #include <algorithm>
 #include <cfloat>
 
@@ -178,6 +180,83 @@ int mask_keys(const float* k, const uint8_t* keep, float* out, int P, int D, int
     return (int)hipGetLastError();
 }
 
+// The sorted keys of a masked abs walk, in place: a masked key takes the value of the last kept key before it in the
+// sorted order; masked keys before the first kept key (and every key of a segment with none kept) keep their own. The
+// order stays ascending and every distance the walk measures between consecutive keys, from the last key below a query
+// and from the largest key (the segment totals -Btot - (q - k_max) Wtot) runs between kept keys: masked keys, weighing 0
+// in every sum, become transparent. Without this, the totals of a segment whose largest key is masked and far above
+// the kept ones cancel quantities of size (k_max - k_n) |w_n| far larger than the kept keys' own terms.
+// One workgroup of FM_T threads per segment; each thread takes FM_I consecutive keys of a piece, and the last kept
+// value carries across threads (a wave scan, then the waves' totals through LDS) and across pieces.
+constexpr int FM_T = 1024, FM_I = 16;
+__global__ __launch_bounds__(FM_T)
+void fill_masked_keys_kernel(float* __restrict__ ks, const uint32_t* __restrict__ kp, const uint8_t* __restrict__ keep,
+                             const int D, const int N)
+{
+    __shared__ float wval[FM_T / WAVE];
+    __shared__ int whave[FM_T / WAVE];
+    const int s = blockIdx.x, p = s / D, t = threadIdx.x, lane = t & (WAVE - 1), w = t / WAVE;
+    float* seg = ks + (size_t)s * N;
+    const uint32_t* pseg = kp + (size_t)s * N;
+    const uint8_t* kk = keep + (size_t)p * N;
+    float carry = 0.f;
+    int have_carry = 0;
+    for (int base = 0; base < N; base += FM_T * FM_I) {
+        const int i0 = base + t * FM_I;
+        float x[FM_I];
+        bool kept[FM_I];
+#pragma unroll
+        for (int j = 0; j < FM_I; ++j) {
+            const int i = min(i0 + j, N - 1);             // clamped: unconditional loads
+            x[j] = seg[i];
+            kept[j] = i0 + j < N && kk[pseg[i]] != 0;
+        }
+        // this thread's last kept value, then the last kept value before this thread (exclusive scan)
+        float tv = 0.f;
+        int th = 0;
+#pragma unroll
+        for (int j = 0; j < FM_I; ++j)
+            if (kept[j]) { tv = x[j]; th = 1; }
+        float iv = tv;
+        int ih = th;
+#pragma unroll
+        for (int off = 1; off < WAVE; off <<= 1) {
+            const float uv = __shfl_up(iv, off, WAVE);
+            const int uh = __shfl_up(ih, off, WAVE);
+            if (lane >= off && !ih) { iv = uv; ih = uh; }
+        }
+        if (lane == WAVE - 1) { wval[w] = iv; whave[w] = ih; }
+        // both shuffles unconditional: a cross-lane read inside a lane-dependent branch reads 0 from inactive lanes
+        float ev = __shfl_up(iv, 1, WAVE);
+        const int eh_up = __shfl_up(ih, 1, WAVE);
+        int eh = lane > 0 ? eh_up : 0;
+        __syncthreads();
+        float pv = carry;                                 // before this wave: earlier pieces, then earlier waves
+        int ph = have_carry;
+        for (int ww = 0; ww < w; ++ww)
+            if (whave[ww]) { pv = wval[ww]; ph = 1; }
+        if (!eh) { ev = pv; eh = ph; }
+        // the piece's last kept value carries to the next piece
+        for (int ww = 0; ww < FM_T / WAVE; ++ww)
+            if (whave[ww]) { carry = wval[ww]; have_carry = 1; }
+#pragma unroll
+        for (int j = 0; j < FM_I; ++j) {
+            if (kept[j]) { ev = x[j]; eh = 1; }
+            else if (eh) x[j] = ev;
+        }
+#pragma unroll
+        for (int j = 0; j < FM_I; ++j)
+            if (i0 + j < N) seg[i0 + j] = x[j];
+        __syncthreads();                                  // the wave totals are read before the next piece's
+    }
+}
+
+int fill_masked_keys(float* ks, const uint32_t* kp, const uint8_t* keep, int P, int D, int N, hipStream_t st) {
+    StageTimer t("fill_masked_keys", st);
+    hipLaunchKernelGGL(fill_masked_keys_kernel, dim3((unsigned)(P * D)), dim3(FM_T), 0, st, ks, kp, keep, D, N);
+    return (int)hipGetLastError();
+}
+
 // Per (p, m): the reduction over d of the layer's query-only term (e^{-|q|}, |q| or max(0, 1 - |q|)); one thread per
 // query, d in order, coalesced across m.
 template <int KIND>
@@ -223,7 +302,7 @@ void layer_epilogue_kernel(const float* __restrict__ qt, const float* __restrict
     } else if constexpr (KIND == LAYER_ADD_RIESZ) {
         const float aqe = qt[pm] + LAYER_EPS;
         num = aqe * vsum[(size_t)p * C + c] + akv[(size_t)p * C + c] - w0[i];
-        den = MASKED ? aqe * (float)M + sak[p] - u0[pm] - np * aqe
+        den = MASKED ? aqe * ((float)M - np) + sak[p] - u0[pm]
                      : aqe * (float)M + sak[p] - u0[pm] - LAYER_EPS * np;
     } else {
         num = (wp[i] + wm[i]) / 2.f - w0[i];

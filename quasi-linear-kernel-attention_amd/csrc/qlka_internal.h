@@ -204,6 +204,10 @@ int riesz_prefix(const float* k, const float* v, const uint8_t* keep, void* pre,
                  hipStream_t st);
 // out[p][d][n] = keep[p][n] ? k[p][d][n] : FLT_MAX: keys whose every Laplace term is exactly 0 and which sort last
 int mask_keys(const float* k, const uint8_t* keep, float* out, int P, int D, int N, hipStream_t st);
+// Sorted keys ks (P*D segments of N, permutation kp) of a masked abs walk, in place: every masked key (keep (P, N),
+// indexed by the original position) takes the value of the last kept key before it; masked keys before the first kept
+// key keep theirs. The abs walk's distances, its segment totals included, then run between kept keys only.
+int fill_masked_keys(float* ks, const uint32_t* kp, const uint8_t* keep, int P, int D, int N, hipStream_t st);
 // out[p][m][:] from the op outputs: w0/u0 (and, for add_bump, w+/u+ and w-/u- of q + 1 and q - 1). masked: the op
 // outputs are sums over the kept keys and n_pad is ignored (add_riesz takes its n_pad from pre); else n_pad (P) is
 // the reference's padded-key count (null: none). qt: (P, M) scratch for the per-query d-reductions

@@ -119,7 +119,7 @@ void slab_reduce(const float* __restrict__ slab, float* __restrict__ out, const 
                     for (int e = 0; e < 4; ++e) o[e] = a[e] / den;
                 } else {
                     const float aqe = qv + LAYER_EPS;
-                    const float den = fmaxf(MASKED ? aqe * (float)M + ep.sak[p] - u - np * aqe
+                    const float den = fmaxf(MASKED ? aqe * ((float)M - np) + ep.sak[p] - u
                                                    : aqe * (float)M + ep.sak[p] - u - LAYER_EPS * np, LAYER_CLAMP);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {

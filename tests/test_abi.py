@@ -48,10 +48,18 @@ def test_version_and_workspace_sizes(lib):
     assert lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4) == 0
     assert lib.qlka_abs_bwd_ws_bytes(32, 64, 600, 600, 64) == 0
     assert lib.qlka_sgn_fwd_ws_bytes(2, 3, 500, 500, 8) == 0
+    assert lib.qlka_abs_fwd_ws_bytes(32, 64, 1024, 1024, 64) == 0        # dense below 2 x the cutoff
+    assert lib.qlka_abs_fwd_ws_bytes(65535, 64, 512, 512, 64) == 0
+    assert lib.qlka_abs_fwd_ws_bytes(2, 3, 9, 100000, 8) == 0            # 16 keys or fewer: dense at any length
     assert lib.qlka_abs_bwd_ws_bytes(12, 64, 600, 600, 64) > 0          # too few workgroups at L = 600: walks
     prev = lib.qlka_set_direct_max(0)
     try:
         assert lib.qlka_laplace_fwd_ws_bytes(1, 1, 8, 8, 4) > 0          # cutoff 0: always sort and walk
+        assert lib.qlka_abs_fwd_ws_bytes(1, 1, 17, 8, 4) > 0
+        # ... except segments of at most 16 keys, which the abs sums always take dense
+        assert lib.qlka_abs_fwd_ws_bytes(1, 1, 16, 8, 4) == 0
+        assert lib.qlka_abs_bwd_ws_bytes(1, 1, 16, 800, 4) == 0
+        assert lib.qlka_abs_bwd_walks(1, 800, 16) == 0
     finally:
         lib.qlka_set_direct_max(prev)
     # the row-emitting ops carry one contribution row per (p, d, query) of a chunk: the D-fold slab
@@ -176,12 +184,13 @@ def test_keep_sorts_entries_validate(lib):
     P, D, N, C, G = 12, 64, 16384, 64, 16384 // 64
     assert lib.qlka_abs_keep_state_bytes(P, D, N, N, C) == 2 * al(P * D * (G + 1) * (C + 2) * 4) + al(P * D * G * 4)
     assert lib.qlka_abs_keep_state_bytes(512, 32, 65, 65, 32) == 0
-    # a handful of keys on either side: the dense route (the walk's segment totals would cost accuracy), unless the
-    # cutoff is 0
+    # a handful of keys on either side: the dense route (the walk's segment totals would cost accuracy), also with the
+    # cutoff at 0
     assert lib.qlka_abs_bwd_walks(12, 16384, 16) == 0 and lib.qlka_abs_bwd_walks(12, 16, 16384) == 0
     assert lib.qlka_abs_bwd_walks(12, 16384, 17) == 1
     prev = lib.qlka_set_direct_max(0)
     try:
-        assert lib.qlka_abs_bwd_walks(12, 16384, 16) == 1
+        assert lib.qlka_abs_bwd_walks(12, 16384, 16) == 0
+        assert lib.qlka_abs_bwd_walks(12, 16384, 17) == 1
     finally:
         lib.qlka_set_direct_max(prev)

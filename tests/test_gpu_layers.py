@@ -185,6 +185,33 @@ def test_masked_layer_matches_reference_composition(dev, kernel, shape):
         assert torch.all(got[2] == 0), "a p with every key masked gives zero rows"
 
 
+@pytest.mark.parametrize("kernel", ("add_riesz", "add_bump"))
+@pytest.mark.parametrize("kept,far", [(2, True), (3, True), (40, True), (40, False)])
+def test_masked_layer_few_kept_keys_among_far_masked_keys(dev, kernel, kept, far):
+    """A short document padded to a long length: p = 0 keeps 2, 3 or 40 of 4200 keys. With `far` the masked keys lie
+    far above and below the kept ones (+-60 .. 80 against keys of scale 0.7), so that the largest and smallest keys of
+    the segment are masked; otherwise they keep their values, interleaved with the kept ones. The masked abs walk must
+    measure its distances and segment totals between kept keys (fill_masked_keys), and add_riesz's masked denominator
+    must not cancel (S - n_pad formed exactly), to meet the masked-layer bar; p = 1 is an ordinary mask.
+    Self-attention shape (M = N): add_riesz's denominator counts the sequence as S = M keys (attention.py:78) and
+    clamps when M falls below the padded count."""
+    from qlka import layers
+    P, D, N, M, C = 2, 4, 4200, 4200, 16
+    q, k, v = _inputs(P, D, N, M, C, seed=40 + kept, dev=dev, scale=0.7)
+    keep = _mask(P, N, seed=41, dev=dev)
+    keep[0] = False
+    sel = [17, 2101, 4003][:kept] if kept <= 3 else list(range(5, N, N // kept))[:kept]
+    keep[0, torch.tensor(sel, device=dev)] = True
+    if far:
+        dist = torch.linspace(60.0, 80.0, N, device=dev)
+        side = torch.where(torch.arange(N, device=dev) % 2 == 0, 1.0, -1.0)
+        k[0] = torch.where(keep[0][None, :], k[0], (side * dist)[None, :])
+    got = layers.layer_forward(kernel, q, k, v, keep=keep).cpu().double()
+    want = _reference_masked(kernel, q, k, v, keep)
+    np.testing.assert_allclose(got.numpy(), want.numpy(), rtol=1e-4, atol=1e-5,
+                               err_msg=f"{kernel} kept={kept} far={far}")
+
+
 @pytest.mark.parametrize("kernel", KERNELS)
 def test_masked_layer_without_masked_keys_is_the_unmasked_layer(dev, kernel):
     from qlka import layers

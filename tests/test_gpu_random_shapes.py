@@ -212,3 +212,62 @@ def test_random_pipelined_shape(dev, case):
     _check(sub(_np(gq), qi, 1), wq, nq, "grad_q")
     _check(sub(_np(gk), ki, 1), wk, nk, "grad_k")
     _check(sub(_np(gv), ki, 0), wv, nv, "grad_v")
+
+
+def _abi_abs_fwd(q, k, v, path):
+    from qlka import _lib
+    lib = _lib.load()
+    P, D, M = q.shape
+    N, C = v.shape[1], v.shape[2]
+    w = torch.full((P, M, C), float("nan"), device=q.device)
+    u = torch.full((P, M), float("nan"), device=q.device)
+    ws = _lib.workspace(lib.qlka_abs_fwd_ws_bytes(P, D, N, M, C), q.device)
+    _lib.check(lib.qlka_abs_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(w), _lib.ptr(u), P, D, N, M, C, path,
+                                _lib.ptr(ws), ws.numel(), _lib.stream_of(q.device)))
+    return w, u
+
+
+def _abi_abs_bwd(q, k, v, g_w, g_u):
+    from qlka import _lib
+    lib = _lib.load()
+    P, D, M = q.shape
+    N, C = v.shape[1], v.shape[2]
+    gq, gk, gv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = _lib.workspace(lib.qlka_abs_bwd_ws_bytes(P, D, N, M, C), q.device)
+    _lib.check(lib.qlka_abs_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g_w), _lib.ptr(g_u), _lib.ptr(gq),
+                                _lib.ptr(gk), _lib.ptr(gv), P, D, N, M, C, _lib.ptr(ws), ws.numel(),
+                                _lib.stream_of(q.device)))
+    return gq, gk, gv
+
+
+@pytest.mark.parametrize("direct_max", [512, 0])
+def test_few_keys_adversarial_every_route(dev, direct_max):
+    """Two keys, one at distance 0.05 from the queries with weight 0.73, one at 11.2 with weight 0.003: the case where
+    the abs walk's segment totals (-Btot - (q - k_max) Wtot) rounded to 1.8e-5 of sum |term|. Through the C ABI with
+    the size routing on (512) and off (0), on every pinned path, forward and backward (whose grad_v walk takes the two
+    queries as its keys) must meet 1e-5: segments of at most 16 keys take the dense kernels on every route."""
+    from qlka import _lib
+    lib = _lib.load()
+    q = np.array([[[0.0, 0.01, -0.02, 0.04, 0.03]]], dtype=np.float32)          # (1, 1, 5) queries near key 0
+    k = np.array([[[0.05, 11.25]]], dtype=np.float32)                           # (1, 1, 2)
+    v = np.array([[[0.73, -0.73, 0.5], [0.003, -0.003, 0.002]]], dtype=np.float32)   # (1, 2, 3)
+    # backward: the grad_v walk streams the sorted queries (weights g_w) and emits at the keys
+    qb = np.array([[[0.05, 11.25]]], dtype=np.float32)                          # (1, 1, 2): two "keys" of that walk
+    kb = np.array([[[0.0, 0.01, -0.02, 0.04, 0.03]]], dtype=np.float32)         # (1, 1, 5)
+    vb = np.ones((1, 5, 3), dtype=np.float32)
+    g_w = np.array([[[0.73, -0.73, 0.5], [0.003, -0.003, 0.002]]], dtype=np.float32)
+    g_u = np.array([[0.5, -0.25]], dtype=np.float32)
+    prev = lib.qlka_set_direct_max(direct_max)
+    try:
+        for path in (-1, 0, 1):
+            w, u = _abi_abs_fwd(_t(q, dev), _t(k, dev), _t(v, dev), path)
+            ow, ou, nw = brute.abs_sum(q, k, v)
+            _check(_np(w), ow, nw, f"out_w path {path}")
+            _check(_np(u), ou, ou, f"out_u path {path}")
+        gq, gk, gv = _abi_abs_bwd(_t(qb, dev), _t(kb, dev), _t(vb, dev), _t(g_w, dev), _t(g_u, dev))
+        (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(qb, kb, vb, g_w, g_u, tie=-1.0)
+        _check(_np(gq), wq, nq, "grad_q")
+        _check(_np(gk), wk, nk, "grad_k")
+        _check(_np(gv), wv, nv, "grad_v")
+    finally:
+        lib.qlka_set_direct_max(prev)
