@@ -158,8 +158,19 @@ def config_timings(dev, reps=None, only=None):
             torch.cuda.synchronize()
             ts.append(e0.elapsed_time(e1))
         ms = statistics.fmean(ts)
+        # device memory of one call above its inputs (torch's allocator: outputs, workspace, kept sorts and range
+        # states, gradients), as the reference's speed bench records torch.cuda.max_memory_allocated
+        # (Experiments/speed_and_memory/bench.py:101-104)
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        fn()
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated() - base
         entry = {"ms": round(ms, 4), "ms_median": round(statistics.median(ts), 4), "calls": n_rep,
-                 "work": c["work"], "shape": f"P={c['P']} D={c['D']} N=M={c['N']} C={c['C']}"}
+                 "work": c["work"], "shape": f"P={c['P']} D={c['D']} N=M={c['N']} C={c['C']}",
+                 "peak_mem_bytes": int(peak)}
         flops = dense_flops(i, c)
         if flops is not None:
             lib.qlka_timing_reset()

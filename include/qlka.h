@@ -34,20 +34,22 @@ int qlka_version(void);
  * Base cutoff B of the dense evaluation (the qlka_direct_* kernels: same results to fp32 rounding, same tie
  * conventions) in qlka_laplace_fwd, qlka_abs_fwd (path -1), qlka_abs_bwd and qlka_sgn_fwd, with L = max(N, M): the
  * abs forward goes dense for L <= 2B, the Laplace forward for L <= B, the backward and the sgn sum for L <= B or for
- * L <= 5B/4 when P * ceil(L / 32) >= 512. With B > 0 the abs forward also goes dense for N <= 16 keys, and the
- * backward and the sgn sum for min(N, M) <= 16 (the walk's segment totals lose accuracy with a handful of keys).
- * Default 512; 0 always sorts and walks. Process-wide; returns the previous
+ * L <= 5B/4 when P * ceil(L / 32) >= 512. Whatever B (0 included) and the pinned path, the abs forward also goes
+ * dense for N <= 16 keys, and the backward and the sgn sum for min(N, M) <= 16 (the walk's segment totals lose
+ * accuracy with a handful of keys). Default 512; 0 sorts and walks everything else. Process-wide; returns the previous
  * value (or -QLKA_EINVAL for n < 0). The C-level counterpart of the reference's set_keops_cutoff
  * (Weighted_Abs_Sum/weighted_abs_sum/ops.py:21-25), which picks the KeOps backend in Python.
  */
 int qlka_set_direct_max(int n);
 /*
- * Workspace budget in bytes (default 16 GiB). Every operator below runs its whole pipeline on chunks of consecutive
+ * Workspace budget in bytes (default 5 GiB). Every operator below runs its whole pipeline on chunks of consecutive
  * p = (batch, head) indices (every stage works on each p alone), taking the largest chunk the workspace it is given
  * holds (at least one p), so the caller bounds device memory by the workspace it passes. The *_ws_bytes() queries
  * report the workspace of the largest chunk within this budget (one p when even one p exceeds it); results do not
  * depend on the chunking. They report 0 for a call that takes the dense route at the current cutoff (qlka_laplace_fwd,
- * qlka_abs_bwd, qlka_abs_bwd_sorted, qlka_sgn_fwd): such a call takes no workspace, and ws may be null. Process-wide; returns the previous value. The reference has no counterpart: its
+ * qlka_abs_fwd, qlka_abs_bwd, qlka_abs_bwd_sorted, qlka_sgn_fwd): such a call takes no workspace, and ws may be null
+ * (a dense abs forward that keeps its sorts for a walking backward needs sort scratch only for segments longer than
+ * 16384). Process-wide; returns the previous value. The reference has no counterpart: its
  * workspace is O(P*D*(N+M)) (Weighted_Abs_Sum/csrc/binding.cpp:101-111), where this build's per-feature slab of
  * contribution rows is O(P*D*M*C).
  */
@@ -71,7 +73,11 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
  * the same results. Shapes whose single-p workspace (qlka_laplace_fwd_ws_bytes(1, D, N, M, C)) exceeds 512 MiB are
  * refused with QLKA_EINVAL (N = M = 16384, D = C = 64 needs 297 MiB). `stream` must belong to the current device.
  * All calls on one device share the array: calls that overlap in time on one device (e.g. on two streams) race and
- * must be serialised by the caller.
+ * must be serialised by the caller. The array takes device memory from the first call on a device on (hipMemGetInfo
+ * on MI355X: free memory unchanged by loading the library and by calls of the other entry points, 512 MiB less after
+ * this entry's first call); a process that never calls it does not hold it. A thread's first uncaptured call on a
+ * device may create that thread's side stream and its events (hipStreamCreateWithFlags, hipEventCreateWithFlags:
+ * no device memory); under stream capture, or once they exist, the call creates nothing.
  */
 int qlka_laplace_fwd_noalloc(const float* q, const float* k, const float* v, float* out_w, float* out_u,
                              int P, int D, int N, int M, int C, void* stream);

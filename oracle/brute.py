@@ -19,6 +19,8 @@ sgn_sum                        ops.py:129-139, binding.cpp:383-439 (tie +1), keo
 abs_backward                   binding.cpp:242-380, sgn_kernels.cu:8-15 (tie -1; keops: 0)      torch.autograd.gradcheck of a dense fp64
                                                                                                forward (tie-free), grad_v == abs_sum(k, q, g_w)
 stable_sort / merge_rank       sort_utils.cu:85-87, walk_common.cuh:10-20                       pure-Python stable sort / brute-force counts
+grad_q_fp32_prefix             sgn_kernels.cu:8-15, binding.cpp:242-262 (the reference's fp32   equals abs_backward's grad_q to fp32 rounding;
+                               prefix-sum composition of grad_q, tie -1)                        its error against it is reported, not a bar
 """
 
 import os
@@ -145,6 +147,41 @@ def abs_backward(q, k, v, g_w, g_u=None, tie=-1.0):
             nk[p, d] = Ba.sum(axis=0)
     gv, _, nv = abs_sum(k, q, g_w)                         # grad_v = sum_{d,m} |k_n - q_m| g_w[m, :]
     return (gq, gk, gv), (nq, nk, nv)
+
+
+def grad_q_fp32_prefix(q, k, v, g_w, g_u=None):
+    """grad_q as the reference's CUDA walk composes it, in float32 (sgn_kernels.cu:8-15, binding.cpp:242-262): per
+    feature, v summed in the keys' sorted order into prefix rows PW_r (float32, one key after the other), and for a
+    query of rank r = #{k < q} (a tie counts as a key above: s(0) = -1) grad_q = <g_m, 2 PW_r - W_tot>
+    (+ g_u (2 r - N)), the vector expression and the dot product in float32. Its error against the fp64
+    abs_backward is the rounding an fp32 implementation of this composition carries; the library's own error is held
+    to a small multiple of it."""
+    q, k, v, g_w = (np.asarray(a, dtype=np.float32) for a in (q, k, v, g_w))
+    g_u = None if g_u is None else np.asarray(g_u, dtype=np.float32)
+    P, D, M = q.shape
+    N = k.shape[2]
+    out = np.zeros((P, D, M), dtype=np.float32)
+    for p in range(P):
+        for d in range(D):
+            order = np.argsort(k[p, d], kind="stable")
+            pw = np.zeros((N + 1, v.shape[2]), dtype=np.float32)
+            pw[1:] = np.cumsum(v[p][order], axis=0, dtype=np.float32)
+            r = np.searchsorted(k[p, d][order], q[p, d], side="left")
+            t = np.float32(2.0) * pw[r] - pw[N]
+            out[p, d] = np.einsum("mc,mc->m", g_w[p], t, dtype=np.float32)
+            if g_u is not None:
+                out[p, d] += g_u[p] * (np.float32(2.0) * r.astype(np.float32) - np.float32(N))
+    return out
+
+
+def dot_normaliser(v, g_w, g_u=None):
+    """(P, M): sum_n |<g_m, v_n> (+ g_um)|, the per-key magnitude of grad_q's terms (the normaliser of the backward
+    before the elementary-product one of abs_backward; tighter when a C-channel dot product cancels)."""
+    v, g_w = _f64(v), _f64(g_w)
+    B = np.einsum("pmc,pnc->pmn", g_w, v)
+    if g_u is not None:
+        B = B + _f64(g_u)[:, :, None]
+    return np.abs(B).sum(axis=2)
 
 
 def abs_backward_sub(q, k, v, g_w, g_u, qidx, kidx):

@@ -8,7 +8,9 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
+#include <vector>
 
 using namespace qlka;
 
@@ -130,7 +132,9 @@ int check_ws(void* ws, size_t have, size_t need) {
 // whole pipeline (sorts, range passes, walks, reduce, epilogue) on a chunk of pc consecutive p at a time, with a
 // workspace sized for pc. An operator takes the largest chunk that the workspace it is given holds; the *_ws_bytes()
 // queries size the workspace for the largest chunk within the process-wide budget (qlka_set_workspace_budget).
-std::atomic<size_t> g_ws_budget{size_t(16) << 30};
+// Default 5 GiB: at configs[4] (P = 12, N = M = 131072) a call took 86.4 ms at 5 GiB and 86.6 ms at 16 GiB (one call's
+// peak 9.2 vs 19.5 GB); the headline's pipelined chunks (2.43 GB) fit either.
+std::atomic<size_t> g_ws_budget{size_t(5) << 30};
 
 // largest pc in [1, P] with bytes(pc) <= cap, or 1 when even one p does not fit (bytes() grows with pc)
 template <class Bytes>
@@ -205,6 +209,30 @@ struct SideStream {
     hipEvent_t walked = nullptr, reduced[2] = {nullptr, nullptr};   // the chunk pipeline's events (run_pipeline)
 };
 
+// Side streams outlive the threads that created them: a thread that exits hands its side streams (and their events)
+// back to a process-wide pool, and a thread's first call on a device takes one from there before creating a new one.
+// So a server whose worker threads come and go holds at most one side stream per device per thread alive at a time.
+// The pool is never destroyed, and returning to it makes no HIP call (a thread may exit after the runtime has shut
+// down, at process exit).
+constexpr int MAX_DEVICES = 64;
+struct SidePool {
+    std::mutex mu;
+    std::vector<SideStream> free[MAX_DEVICES];
+};
+SidePool& side_pool() {
+    static SidePool* p = new SidePool;                    // never destroyed: threads may exit after static teardown
+    return *p;
+}
+struct ThreadSides {
+    SideStream sides[MAX_DEVICES];
+    ~ThreadSides() {
+        SidePool& p = side_pool();
+        std::lock_guard<std::mutex> lock(p.mu);
+        for (int d = 0; d < MAX_DEVICES; ++d)
+            if (sides[d].s != nullptr) p.free[d].push_back(sides[d]);
+    }
+};
+
 hipError_t side_stream(hipStream_t st, SideStream** out) {
     *out = nullptr;
     int cur = 0;
@@ -215,10 +243,17 @@ hipError_t side_stream(hipStream_t st, SideStream** out) {
         if ((e = hipStreamGetDevice(st, &dev)) != hipSuccess) return e;
         if (dev != cur) return hipSuccess;              // stream of another device: run in order on it
     }
-    constexpr int MAX_DEVICES = 64;
-    thread_local SideStream sides[MAX_DEVICES];
+    thread_local ThreadSides mine;
     if (cur >= MAX_DEVICES) return hipSuccess;
-    SideStream& sd = sides[cur];
+    SideStream& sd = mine.sides[cur];
+    if (sd.s == nullptr) {
+        SidePool& p = side_pool();
+        std::lock_guard<std::mutex> lock(p.mu);
+        if (!p.free[cur].empty()) {
+            sd = p.free[cur].back();
+            p.free[cur].pop_back();
+        }
+    }
     if (sd.s == nullptr) {
         // Creating a stream inside a stream capture would invalidate it: a thread whose first call is captured runs
         // that call in order on the caller's stream and creates its side stream with a later, uncaptured call.

@@ -39,6 +39,8 @@ def _cases():
         "add_laplace_masked_layer": ((2, 3, 1500, 1500, 16),
                                      lambda q, k, v, gw, gu: layers.layer_forward("add_laplace", q, k, v,
                                                                                   keep=v[:, :, 0] > -0.5)),
+        # the allocation-free entry point (a static workspace, two chunks of p pipelined over the side stream)
+        "laplace_noalloc": ((3, 4, 3000, 2500, 33), _laplace_noalloc),
         # short segments: the dense kernels
         "abs_full_dense": ((64, 8, 65, 65, 32),
                            lambda q, k, v, gw, gu: weighted_abs_sum_full(q, k, v, backend="cuda")),
@@ -47,12 +49,26 @@ def _cases():
     }
 
 
+def _laplace_noalloc(q, k, v, gw, gu):
+    """qlka_laplace_fwd_noalloc through the C ABI on the current (capturing) stream: the library's static workspace,
+    no allocation by the library inside the capture."""
+    from qlka import _lib
+    P, D, M = q.shape
+    N, C = v.shape[1], v.shape[2]
+    w = torch.empty(P, M, C, device=q.device)
+    u = torch.empty(P, M, device=q.device)
+    _lib.check(_lib.load().qlka_laplace_fwd_noalloc(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(w), _lib.ptr(u),
+                                                    P, D, N, M, C, _lib.stream_of(q.device)))
+    return w, u
+
+
 def _flat(out):
     return [t for t in (out if isinstance(out, (tuple, list)) else (out,)) if t is not None]
 
 
 @pytest.mark.parametrize("case", ["laplace_walk", "abs_full_walk", "abs_full_backward_walk", "add_bump_layer",
-                                  "add_laplace_masked_layer", "abs_full_dense", "abs_backward_dense"])
+                                  "add_laplace_masked_layer", "laplace_noalloc", "abs_full_dense",
+                                  "abs_backward_dense"])
 def test_graph_replays_equal_eager(dev, case):
     shape, fn = _cases()[case]
     args = _inputs(dev, *shape, seed=sum(shape))

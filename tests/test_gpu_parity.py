@@ -241,6 +241,35 @@ def test_abs_backward(dev, shape, full, kind, route):
     _assert_rel(_np(gv), wv, nv, "grad_v")
 
 
+@pytest.mark.parametrize("shape", [(2, 3, 2000, 1500, 64), (1, 2, 600, 900, 128), (2, 2, 3000, 3000, 32)])
+@pytest.mark.parametrize("with_u", [False, True])
+def test_backward_error_against_reference_fp32_composition(dev, shape, with_u):
+    """grad_q under the per-key normaliser sum_n |<g_m, v_n> (+ g_u)| (tighter than the elementary-product one of the
+    other tests when a C-channel dot product cancels): the library's error must stay within twice the error of the
+    reference's own fp32 composition (prefix sums in sorted order, <g, 2 PW - W_tot>, oracle grad_q_fp32_prefix)
+    and below 1e-4. Both walk and dense routes at these sizes are the library's own choice."""
+    from weighted_abs_sum import _ext
+    P, D, N, M, C = shape
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape))
+    rng = np.random.default_rng(sum(shape) + 1)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32) if with_u else None
+    tq, tk, tv, tg = (_t(a, dev) for a in (q, k, v, g_w))
+    if with_u:
+        gq, _, _ = _ext.weighted_abs_sum_full_backward(tq, tk, tv, tg, _t(g_u, dev))
+    else:
+        gq, _, _ = _ext.weighted_abs_sum_backward(tq, tk, tv, tg)
+    (want, _, _), _ = brute.abs_backward(q, k, v, g_w, g_u, tie=-1.0)
+    ref32 = brute.grad_q_fp32_prefix(q, k, v, g_w, g_u)
+    dn = brute.dot_normaliser(v, g_w, g_u)[:, None, :]
+    err_lib = float((np.abs(_np(gq) - want) / dn).max())
+    err_ref = float((np.abs(ref32 - want) / dn).max())
+    print(f"grad_q error / per-key normaliser {shape} g_u={with_u}: library {err_lib:.3e}, reference fp32 "
+          f"composition {err_ref:.3e}")
+    assert err_lib <= 1e-4
+    assert err_lib <= max(2 * err_ref, 1e-6)
+
+
 @pytest.mark.parametrize("full", [False, True])
 def test_autograd_through_ops(dev, full):
     from weighted_abs_sum import weighted_abs_sum, weighted_abs_sum_full

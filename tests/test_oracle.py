@@ -320,3 +320,23 @@ def test_key_mask_matches_reference_composition(op):
     w2, u2, _ = fn(q, k, v)
     np.testing.assert_array_equal(w[2], w2[2])
     np.testing.assert_array_equal(u[2], u2[2])
+
+
+@pytest.mark.parametrize("g_u", [False, True])
+def test_grad_q_fp32_prefix_matches_fp64_backward(g_u):
+    """The fp32 restatement of the reference's grad_q composition (prefix sums in sorted order, <g, 2 PW - W_tot>)
+    equals the fp64 brute force to fp32 rounding, with ties (a tie counts as a key above the query, s(0) = -1: a rank
+    taken with side="right" misses here by whole terms)."""
+    rng = np.random.default_rng(3)
+    P, D, N, M, C = 2, 3, 300, 200, 16
+    q = (rng.integers(-20, 21, size=(P, D, M)) / 8).astype(np.float32)     # exact ties between q and k
+    k = (rng.integers(-20, 21, size=(P, D, N)) / 8).astype(np.float32)
+    v = rng.standard_normal((P, N, C)).astype(np.float32)
+    gw = rng.standard_normal((P, M, C)).astype(np.float32)
+    gu = rng.standard_normal((P, M)).astype(np.float32) if g_u else None
+    got = brute.grad_q_fp32_prefix(q, k, v, gw, gu)
+    (want, _, _), _ = brute.abs_backward(q, k, v, gw, gu, tie=-1.0)
+    dn = brute.dot_normaliser(v, gw, gu)[:, None, :]
+    err = np.abs(got - want) / dn
+    assert err.max() < 1e-5
+    assert err.max() > 0                                  # an fp32 evaluation, not the fp64 one again
