@@ -100,32 +100,41 @@ def add_laplace(q, k, v, n_pad=0):
 
 
 def unfused(kernel, q, k, v, n_pad=0):
-    """The reference's own composition (attention.py:67-92): separate op calls and a torch epilogue. Differentiable
-    for add_riesz / add_bump through weighted_abs_sum_full's autograd, on the backend the reference's _abs_sum picks
-    (attention.py:60-63: "keops" below KEOPS_BELOW queries, so a gradient tie counts 0 there, else "cuda")."""
-    from weighted_abs_sum import weighted_abs_sum_full as _full
+    """The layer as separate op calls plus a torch epilogue: the arithmetic of attention.py:67-92, differentiable for
+    add_riesz / add_bump through weighted_abs_sum_full's autograd. The abs sums run on the backend the reference's
+    _abs_sum picks (attention.py:60-63): "keops" below KEOPS_BELOW queries (a gradient tie then counts 0), else
+    "cuda". q (P, D, M), k (P, D, N), v (P, N, C); n_pad a number or (P, 1)."""
+    from weighted_abs_sum import weighted_abs_sum_full
     from weighted_laplace_sum import weighted_laplace_sum
 
-    def weighted_abs_sum_full(a, b, c):
-        return _full(a, b, c, backend="keops" if a.shape[2] < KEOPS_BELOW else "cuda")
+    backend = "keops" if q.shape[2] < KEOPS_BELOW else "cuda"
+    keys, vals = k.contiguous(), v.contiguous()
+
+    def sums(queries):                                   # (w (P, M, C), u (P, M)) of the abs kernel at these queries
+        return weighted_abs_sum_full(queries.contiguous(), keys, vals, backend=backend)
+
+    def normalise(num, den):                             # rows divided by their clamped weight
+        return num / den.clamp_min(CLAMP).unsqueeze(2)
 
     if kernel == "add_laplace":
-        out_w, out_u = weighted_laplace_sum(q.contiguous(), k.contiguous(), v.contiguous())
-        den = out_u - n_pad * (-q.abs()).exp().sum(dim=1)
-        return out_w / den.clamp_min(CLAMP)[:, :, None]
+        w, u = weighted_laplace_sum(q.contiguous(), keys, vals)
+        per_pad = torch.exp(-q.abs()).sum(dim=1)         # a key at 0: sum_d e^{-|q_d|} in u, nothing in w
+        return normalise(w, u - n_pad * per_pad)
     if kernel == "add_riesz":
-        out_w, out_u = weighted_abs_sum_full(q.contiguous(), k.contiguous(), v.contiguous())
-        aq, ak, S = q.abs().sum(dim=1), k.abs().sum(dim=1), q.shape[2]
-        num = (aq + EPS)[:, :, None] * v.sum(dim=1)[:, None, :] + (ak[:, :, None] * v).sum(dim=1)[:, None, :] - out_w
-        den = (aq + EPS) * S + ak.sum(dim=1, keepdim=True) - out_u - EPS * n_pad
-        return num / den.clamp_min(CLAMP)[:, :, None]
+        # A[m, n] = |q_m|_1 + |k_n|_1 - |q_m - k_n|_1 + EPS summed against [v, 1]
+        w, u = sums(q)
+        qn = q.abs().sum(dim=1) + EPS                    # (P, M)
+        kn = k.abs().sum(dim=1)                          # (P, N)
+        v_tot = v.sum(dim=1).unsqueeze(1)                # (P, 1, C)
+        kv_tot = torch.bmm(kn.unsqueeze(1), vals)        # (P, 1, C): sum_n |k_n|_1 v_n
+        num = qn.unsqueeze(2) * v_tot + kv_tot - w
+        den = qn * q.shape[2] + kn.sum(dim=1, keepdim=True) - u - EPS * n_pad
+        return normalise(num, den)
     if kernel == "add_bump":
-        w0, u0 = weighted_abs_sum_full(q.contiguous(), k.contiguous(), v.contiguous())
-        wp, up = weighted_abs_sum_full((q + 1).contiguous(), k.contiguous(), v.contiguous())
-        wm, um = weighted_abs_sum_full((q - 1).contiguous(), k.contiguous(), v.contiguous())
-        num = (wp + wm) / 2 - w0
-        den = (up + um) / 2 - u0 - n_pad * (1 - q.abs()).clamp_min(0).sum(dim=1)
-        return num / den.clamp_min(CLAMP)[:, :, None]
+        # max(0, 1 - |x|) = (|x + 1| + |x - 1|) / 2 - |x|, x = q_d - k_d
+        (w0, u0), (w1, u1), (w2, u2) = sums(q), sums(q + 1), sums(q - 1)
+        per_pad = (1 - q.abs()).clamp_min(0).sum(dim=1)  # a key at 0: sum_d max(0, 1 - |q_d|) in u
+        return normalise((w1 + w2) / 2 - w0, (u1 + u2) / 2 - u0 - n_pad * per_pad)
     raise ValueError(f"unknown additive kernel {kernel!r}")
 
 
@@ -156,16 +165,18 @@ def attention(q, k, v, kernel, tau, keep=None):
         raise ValueError(f"attention: kernel {kernel!r} is not one of {sorted(LAYERS)}")
     assert q.dtype == k.dtype == v.dtype == torch.float32, "kernel attention runs in fp32 only"
     B, H, S, D = q.shape
-    P = B * H
-    q = q.transpose(2, 3).reshape(P, D, S)
-    k = k.transpose(2, 3).reshape(P, D, S)
-    v = v.reshape(P, S, D)
-    keep = None if keep is None else keep.repeat_interleave(H, dim=0)       # (P, S)
-    q, k, n_pad = q / tau, k / tau, 0
-    if keep is not None and not _needs_grad(q, k, v):
-        return layer_forward(kernel, q, k, v, keep=keep).view(B, H, S, D)
-    if keep is not None:
-        k, v = k * keep[:, None, :], v * keep[:, :, None]
-        n_pad = S - keep.sum(dim=1, keepdim=True)
-    out = LAYERS[kernel](q, k, v, n_pad)
-    return out.view(B, H, S, D)
+
+    def features_first(x):                               # (B, H, S, D) -> (B*H, D, S), scaled by 1 / tau
+        return x.permute(0, 1, 3, 2).reshape(B * H, D, S) / tau
+
+    qf, kf, vf = features_first(q), features_first(k), v.reshape(B * H, S, D)
+    head_keep = None if keep is None else keep.unsqueeze(1).expand(B, H, S).reshape(B * H, S)
+    if head_keep is not None and not _needs_grad(qf, kf, vf):
+        return layer_forward(kernel, qf, kf, vf, keep=head_keep).view(B, H, S, D)
+    n_pad = 0
+    if head_keep is not None:
+        w8 = head_keep.to(kf.dtype)
+        kf, vf = kf * w8.unsqueeze(1), vf * w8.unsqueeze(2)
+        n_pad = S - w8.sum(dim=1, keepdim=True)
+    return LAYERS[kernel](qf, kf, vf, n_pad).view(B, H, S, D)
+
