@@ -74,8 +74,9 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
  * refused with QLKA_EINVAL (N = M = 16384, D = C = 64 needs 297 MiB). `stream` must belong to the current device.
  * All calls on one device share the array: calls that overlap in time on one device (e.g. on two streams) race and
  * must be serialised by the caller. The array takes device memory from the first call on a device on (hipMemGetInfo
- * on MI355X: free memory unchanged by loading the library and by calls of the other entry points, 512 MiB less after
- * this entry's first call); a process that never calls it does not hold it. A thread's first uncaptured call on a
+ * on MI355X: free memory unchanged by loading the library, 6 MiB less after a first qlka_laplace_fwd call, whose
+ * kernels' code loads on first use, and 512 MiB less after this entry's first call; unchanged by its later calls); a
+ * process that never calls it does not hold it. A thread's first uncaptured call on a
  * device may create that thread's side stream and its events (hipStreamCreateWithFlags, hipEventCreateWithFlags:
  * no device memory); under stream capture, or once they exist, the call creates nothing.
  */
