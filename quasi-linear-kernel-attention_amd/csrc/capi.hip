@@ -261,12 +261,15 @@ hipError_t side_stream(hipStream_t st, SideStream** out) {
         if ((e = hipStreamIsCapturing(st, &cs)) != hipSuccess) return e;
         if (cs != hipStreamCaptureStatusNone) return hipSuccess;
         SideStream n;
-        if ((e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&n.fork, hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&n.join, hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&n.walked, hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&n.reduced[0], hipEventDisableTiming)) != hipSuccess) return e;
-        if ((e = hipEventCreateWithFlags(&n.reduced[1], hipEventDisableTiming)) != hipSuccess) return e;
+        hipEvent_t* evs[5] = {&n.fork, &n.join, &n.walked, &n.reduced[0], &n.reduced[1]};
+        e = hipStreamCreateWithFlags(&n.s, hipStreamNonBlocking);
+        for (int i = 0; i < 5 && e == hipSuccess; ++i) e = hipEventCreateWithFlags(evs[i], hipEventDisableTiming);
+        if (e != hipSuccess) {                            // release what was created; the call reports the error
+            for (hipEvent_t* ev : evs)
+                if (*ev != nullptr) (void)hipEventDestroy(*ev);
+            if (n.s != nullptr) (void)hipStreamDestroy(n.s);
+            return e;
+        }
         sd = n;
     }
     *out = &sd;

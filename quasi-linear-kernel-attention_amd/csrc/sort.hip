@@ -2,8 +2,12 @@
 //
 // Replaces the reference's CUB segmented radix sort + iota (Weighted_Abs_Sum/csrc/sort_utils.cu:17-117,
 // Weighted_Laplace_Sum/csrc/sort_utils.cu:14-126) with gfx950 kernels of our own:
-//  * lds_count_sort (runs of 4097 .. 16384 keys): one workgroup sorts one run entirely in LDS, 8 LSD passes of 4-bit
-//    digits ranked with per-thread digit counters (no ballots); see the kernel.
+//  * lds_count_sort6 (runs of 8193 .. 16384 keys, and the runs of longer segments): one 512-thread workgroup sorts
+//    one run entirely in LDS, 6 LSD passes of 6-bit digits ranked with per-thread digit counters (no ballots), two
+//    16-bit counters to a word; see the kernel.
+//  * lds_count_sort (runs of 4097 .. 8192 keys): the same ranking with 4-bit digits and 32-bit counters, 8 passes,
+//    512 threads of 16 keys (the six-pass kernel's 256-thread form measured slower there: 0.070 vs 0.068 ms for
+//    768 runs of 8192).
 //  * lds_radix_sort (runs of up to 4096 keys): one workgroup sorts one run entirely in LDS, 4 LSD passes of 8-bit
 //    digits. Stable ranking inside a wave uses 8 ballots to find the lanes that share a digit (no match instruction on
 //    CDNA), per-wave digit counters in LDS, and a digit-major exclusive scan.
@@ -263,10 +267,10 @@ __device__ __forceinline__ void count_sort_run(CountSortLds<THREADS>& sm, const 
     __syncthreads();
 }
 
-// Only the keys and their counts stay in registers through a pass (the indices are read just before the scatter):
-// 103 VGPRs, so that the 16 waves of a workgroup leave room in each SIMD's registers for the waves of the previous
-// chunk's slab reduce, which runs beside the sort (at 127 VGPRs no reduce wave fitted beside it and each op took
-// 0.02-0.04 ms longer).
+// Only the keys and their counts stay in registers through a pass (the indices are read just before the scatter).
+// In its 1024-thread form (16384-key runs, before the six-pass kernel) that held it to 103 VGPRs, so that the 16 waves
+// of a workgroup left room in each SIMD's registers for the waves of the previous chunk's slab reduce, which runs
+// beside the sort (at 127 VGPRs no reduce wave fitted beside it and each op took 0.02-0.04 ms longer).
 template <int THREADS>
 __global__ __launch_bounds__(THREADS)
 void lds_count_sort(const float* __restrict__ in1, const int seg_len, const int run_len, const int runs_per_seg,
@@ -300,6 +304,211 @@ void lds_count_sort(const float* __restrict__ in1, const int seg_len, const int 
         for (int i = t; i < len; i += THREADS) {
             run_keys[seg_off + start + i] = sm.key[cs_pad(i)];
             run_idx[seg_off + start + i]  = (uint32_t)start + sm.idx[cs_pad(i)];
+        }
+    }
+}
+
+// ---- six-pass counting sort
+// The same ranking as count_sort_run with 6-bit digits: 6 LSD passes (bits 0-5, ..., 24-29, 30-31) instead of 8.
+// Each thread holds C6_ITEMS = 32 consecutive positions (32t .. 32t + 31), so THREADS = 512 cover 16384 keys and the
+// workgroup has 8 waves. The counter table has 64 digits per thread; its counts stay below 2^16 (a thread's own at
+// most 32, a first slot at most 16384), so the two digits 2dp and 2dp + 1 of a thread share one 32-bit word, low and
+// high half: [32 digit pairs][THREADS] words, as many as the 4-bit table's [16][1024], so a pass moves the same LDS
+// words as a 4-bit pass over 16 items and 1024 threads. LDS arrays are padded by one word per 32 (blocked accesses at
+// 33t + j and the rake hit 64 different banks; a thread's own counter words spread over about 3 accesses a bank).
+// Measured on MI355X against the 8-pass kernel (1024 threads of 16 keys): 256 runs of 16384 keys 0.0535 -> 0.0473 ms,
+// 64 segments of 131072 (with the merges) 0.224 -> 0.210 ms, both forward ops 0.6-0.8% faster. The workgroup's 8 waves
+// take 189 VGPRs each (LDS holds one workgroup per CU, so 2 waves per SIMD whatever the count); they leave a SIMD
+// 128 registers, 5 waves of the reduce that runs beside the sort (the 8-pass kernel's 4 waves at 103 left 4).
+constexpr int C6_ITEMS = 32;
+constexpr int C6_BITS = 6;
+constexpr int C6_PAIRS = 1 << (C6_BITS - 1);        // digit pairs (counter words per thread)
+__device__ __forceinline__ int c6_pad(int i) { return i + (i >> 5); }
+
+template <int THREADS>
+struct CountSort6Lds {
+    uint32_t key[THREADS * (C6_ITEMS + 1)];         // padded keys; the digit counters during ranking
+    uint32_t idx[THREADS * (C6_ITEMS + 1)];         // padded positions in the run
+    uint32_t wsum[THREADS / WAVE];
+};
+static_assert(C6_PAIRS <= C6_ITEMS, "the digit counters must fit the key array");
+
+// Exclusive scan, in digit-major order, of the counter table's rake sums: rake thread t = dp * BLKS + blk holds the
+// sums a (digit 2dp) and b (digit 2dp + 1) of threads 32 blk .. 32 blk + 31 of digit pair dp. In digit-major order
+// the sums of one digit pair are a of blocks 0 .. BLKS - 1, then b of blocks 0 .. BLKS - 1; a digit pair's BLKS rake
+// threads are consecutive lanes of one wave, and the waves hold consecutive digit pairs.
+template <int THREADS>
+__device__ __forceinline__ void c6_scan(const uint32_t a, const uint32_t b, uint32_t* wsum, uint32_t& a_ex,
+                                        uint32_t& b_ex) {
+    constexpr int BLKS = THREADS / 32;
+    static_assert(BLKS <= WAVE && WAVE % BLKS == 0, "a digit pair's rake threads lie in one wave");
+    const int lane = lane_id(), w = threadIdx.x / WAVE, gb = lane % BLKS, g0 = lane - gb;
+    uint32_t ai = a, bi = b;                         // inclusive scans within the digit pair
+#pragma unroll
+    for (int off = 1; off < BLKS; off <<= 1) {
+        const uint32_t ya = (uint32_t)__shfl_up((int)ai, off, WAVE), yb = (uint32_t)__shfl_up((int)bi, off, WAVE);
+        if (gb >= off) { ai += ya; bi += yb; }
+    }
+    const uint32_t A = (uint32_t)__shfl((int)ai, g0 + BLKS - 1, WAVE);   // the pair's digit 2dp total
+    const uint32_t B = (uint32_t)__shfl((int)bi, g0 + BLKS - 1, WAVE);
+    uint32_t gi = (gb == BLKS - 1) ? A + B : 0u;    // inclusive scan of the pairs' totals over the wave
+#pragma unroll
+    for (int off = 1; off < WAVE; off <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)gi, off, WAVE);
+        if (lane >= off) gi += y;
+    }
+    const uint32_t before = (uint32_t)__shfl((int)gi, g0 > 0 ? g0 - 1 : 0, WAVE);
+    const uint32_t gex = g0 > 0 ? before : 0u;       // the wave's pairs before this one
+    if (lane == WAVE - 1) wsum[w] = gi;
+    __syncthreads();
+    uint32_t base = 0;
+#pragma unroll
+    for (int i = 0; i < THREADS / WAVE; ++i) base += (i < w) ? wsum[i] : 0u;
+    a_ex = base + gex + ai - a;
+    b_ex = base + gex + A + bi - b;
+}
+
+// The run's sort in LDS. The two arrays trade roles every pass: after the ranks are known (the counter table, in the
+// key array, is then dead), each thread streams its indices from the index array into the key array at their ranks,
+// and then its keys, held in registers, into the index array: only the keys and the packed ranks stay live across a
+// pass, and no extra barrier is needed between the two scatters' reads and writes. Returns the array that holds the
+// sorted keys (the other holds the positions), at padded positions.
+template <int THREADS>
+__device__ __forceinline__ bool count_sort6_run(CountSort6Lds<THREADS>& sm, const float* __restrict__ src,
+                                                const int len)
+{
+    constexpr int BLKS = THREADS / 32;
+    constexpr int ROW = THREADS + THREADS / 32;       // padded words of one digit pair's counter row
+    const int t = threadIdx.x;
+    {
+        float f[C6_ITEMS];
+#pragma unroll
+        for (int r = 0; r < C6_ITEMS; ++r) f[r] = src[min(t + r * THREADS, len - 1)];
+#pragma unroll
+        for (int r = 0; r < C6_ITEMS; ++r) {
+            const int i = t + r * THREADS;
+            sm.key[c6_pad(i)] = float_to_ordered(f[r]) | ((i < len) ? 0u : 0xffffffffu);
+            sm.idx[c6_pad(i)] = (uint32_t)i;
+        }
+    }
+    // Padded addresses written out (the compiler does not see that c6_pad(32 t + j) = 33 t + j, and would keep 32 of
+    // each kind live): this thread's blocked positions, its counter column, its rake words.
+    const int blk0 = (C6_ITEMS + 1) * t;
+    const int col = t + (t >> 5);
+    const int rbase = (t / BLKS) * ROW + 33 * (t % BLKS);
+    bool swapped = false;                             // keys in sm.idx, positions in sm.key
+#pragma unroll 1
+    for (int shift = 0; shift < 32; shift += C6_BITS) {
+        uint32_t* const keys = swapped ? sm.idx : sm.key;
+        uint32_t* const pos = swapped ? sm.key : sm.idx;
+        uint32_t* const cnt = keys;                   // the counter table takes the key array while keys are in VGPRs
+        __syncthreads();                              // the previous scatter (or the load) is complete
+        uint32_t key[C6_ITEMS];
+#pragma unroll
+        for (int j = 0; j < C6_ITEMS; ++j) key[j] = keys[blk0 + j];
+        __syncthreads();                              // every thread holds its keys: the key array is free
+        // 1. this thread's counter words, and each item's count among the thread's earlier items (8 bits each, four
+        //    to a register)
+#pragma unroll
+        for (int dp = 0; dp < C6_PAIRS; ++dp) cnt[dp * ROW + col] = 0u;
+        uint32_t lc[C6_ITEMS / 4];
+#pragma unroll
+        for (int j = 0; j < C6_ITEMS; ++j) {
+            const uint32_t d = (key[j] >> shift) & ((1u << C6_BITS) - 1);
+            const uint32_t h = 16u * (d & 1u);       // the digit's half of the word
+            const uint32_t old = atomicAdd(&cnt[(int)(d >> 1) * ROW + col], 1u << h);
+            const uint32_t c = (old >> h) & 0xffffu;
+            if (j % 4 == 0) lc[j / 4] = c;
+            else lc[j / 4] |= c << (8 * (j % 4));
+        }
+        __syncthreads();
+        // 2. exclusive scan of the table in digit-major order: this thread rakes 32 words of one digit pair
+        {
+            uint32_t rw[32];
+            uint32_t sa = 0, sb = 0;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                rw[i] = cnt[rbase + i];
+                sa += rw[i] & 0xffffu;
+                sb += rw[i] >> 16;
+            }
+            uint32_t ea, eb;
+            c6_scan<THREADS>(sa, sb, sm.wsum, ea, eb);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                cnt[rbase + i] = ea | (eb << 16);
+                ea += rw[i] & 0xffffu;
+                eb += rw[i] >> 16;
+            }
+        }
+        __syncthreads();
+        // 3. ranks (two to a register). Digits and counter addresses are computed again from opaque copies of the
+        //    shift and the column: kept from step 1 instead, 64 more values would stay live across the scan.
+        int sh = shift, cl = col;
+        asm volatile("" : "+s"(sh), "+v"(cl));
+        const uint16_t* const cnt16 = reinterpret_cast<const uint16_t*>(cnt);
+        uint32_t rk[C6_ITEMS / 2];
+#pragma unroll
+        for (int j = 0; j < C6_ITEMS; ++j) {
+            const uint32_t d = (key[j] >> sh) & ((1u << C6_BITS) - 1);
+            const uint32_t first = cnt16[2 * ((int)(d >> 1) * ROW + cl) + (int)(d & 1u)];
+            const uint32_t r = first + ((lc[j / 4] >> (8 * (j % 4))) & 0xffu);
+            if (j % 2 == 0) rk[j / 2] = r;
+            else rk[j / 2] |= r << 16;
+        }
+        __syncthreads();                              // every rank read: the key array takes the positions
+        // 4. positions into the key array, then (all positions read) keys into the position array
+#pragma unroll
+        for (int j = 0; j < C6_ITEMS; ++j) {
+            const int r = (int)((rk[j / 2] >> (16 * (j % 2))) & 0xffffu);
+            keys[c6_pad(r)] = pos[blk0 + j];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < C6_ITEMS; ++j) {
+            const int r = (int)((rk[j / 2] >> (16 * (j % 2))) & 0xffffu);
+            pos[c6_pad(r)] = key[j];
+        }
+        swapped = !swapped;
+    }
+    __syncthreads();
+    return swapped;
+}
+
+template <int THREADS>
+__global__ __launch_bounds__(THREADS)
+void lds_count_sort6(const float* __restrict__ in1, const int seg_len, const int run_len, const int runs_per_seg,
+                     float* __restrict__ out_keys1, uint32_t* __restrict__ out_perm1,
+                     uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_idx,
+                     const int blocks1, const float* __restrict__ in2, float* __restrict__ out_keys2,
+                     uint32_t* __restrict__ out_perm2)
+{
+    const bool second = (int)blockIdx.x >= blocks1;
+    const int bid = second ? (int)blockIdx.x - blocks1 : (int)blockIdx.x;
+    const float* in = second ? in2 : in1;
+    float* out_keys = second ? out_keys2 : out_keys1;
+    uint32_t* out_perm = second ? out_perm2 : out_perm1;
+    __shared__ CountSort6Lds<THREADS> sm;
+
+    const int seg   = bid / runs_per_seg;
+    const int run   = bid - seg * runs_per_seg;
+    const int start = run * run_len;
+    const int len   = min(run_len, seg_len - start);
+    const size_t seg_off = (size_t)seg * seg_len;
+    const bool swapped = count_sort6_run<THREADS>(sm, in + seg_off + start, len);
+    const uint32_t* const keys = swapped ? sm.idx : sm.key;
+    const uint32_t* const pos = swapped ? sm.key : sm.idx;
+
+    const int t = threadIdx.x;
+    if (runs_per_seg == 1) {
+        for (int i = t; i < len; i += THREADS) {
+            out_keys[seg_off + i] = ordered_to_float(keys[c6_pad(i)]);
+            out_perm[seg_off + i] = (uint32_t)start + pos[c6_pad(i)];
+        }
+    } else {
+        for (int i = t; i < len; i += THREADS) {
+            run_keys[seg_off + start + i] = keys[c6_pad(i)];
+            run_idx[seg_off + start + i]  = (uint32_t)start + pos[c6_pad(i)];
         }
     }
 }
@@ -449,6 +658,16 @@ static void launch_cs(const float* in, int S, int L, int run_len, int runs, floa
                        in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
 }
 
+template <int THREADS>
+static void launch_cs6(const float* in, int S, int L, int run_len, int runs, float* ok, uint32_t* op,
+                       uint32_t* rk, uint32_t* ri, hipStream_t st, const float* in2 = nullptr, float* ok2 = nullptr,
+                       uint32_t* op2 = nullptr) {
+    StageTimer t("lds_count_sort", st);
+    const int blocks1 = S * runs;
+    hipLaunchKernelGGL((lds_count_sort6<THREADS>), dim3(in2 ? 2 * blocks1 : blocks1), dim3(THREADS), 0, st,
+                       in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
+}
+
 static inline int merge_tiles(int L) { return (L + MERGE_TILE - 1) / MERGE_TILE; }
 
 size_t seg_sort_scratch_bytes(int S, int L) {
@@ -473,7 +692,7 @@ static int lds_sort(const float* in, float* out_keys, uint32_t* out_perm, const 
 #undef QLKA_LDS
     else if (L <= 8192)  launch_cs<512>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st, in2, out_keys2,
                                         out_perm2);
-    else                 launch_cs<1024>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st, in2, out_keys2,
+    else                 launch_cs6<512>(in, S, L, L, 1, out_keys, out_perm, nullptr, nullptr, st, in2, out_keys2,
                                          out_perm2);
     return (int)hipGetLastError();
 }
@@ -496,7 +715,7 @@ int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L,
     uint32_t* k1 = i0 + n;
     uint32_t* i1 = k1 + n;
     const int runs = (L + LDS_SORT_MAX - 1) / LDS_SORT_MAX;
-    launch_cs<1024>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
+    launch_cs6<512>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
     int err = (int)hipGetLastError();
     if (err) return err;
     const int bps = merge_tiles(L);
