@@ -87,12 +87,27 @@ struct WsSpec {
     bool want_u;            // v == 1 contributions (out_u)
 };
 
+// Sort scratch of a call: one array at a time, or k and q as one sort when N == M (seg_sort2).
+size_t sort_scratch_need(const WsSpec& w) {
+    const int S = w.P * w.D;
+    const size_t one = std::max(seg_sort_scratch_bytes(S, w.N), seg_sort_scratch_bytes(S, w.M));
+    return w.N == w.M ? std::max(one, seg_sort_scratch_bytes(2 * S, w.N)) : one;
+}
+
+// The sorts run in a chunk's prep and are done before its walks write the slab, and the pipeline's prep of a chunk
+// waits for the reduce that last read its workspace copy's slab, so the sort scratch lives inside the slab when the
+// slab holds it (at N = M = 131072 that saves 268 MB a copy).
+bool scratch_in_slab(const WsSpec& w) {
+    const size_t slab = w.slab_rows ? (size_t)w.P * w.D * slab_rows(w.slab_rows) * slab_stride(w.C) * 4 : 0;
+    return sort_scratch_need(w) <= slab;
+}
+
 size_t ws_part(const WsSpec& w, int i) {
     const size_t S = (size_t)w.P * w.D;
     switch (i) {
         case 0: case 1: return align256(S * w.N * 4);
         case 2: case 3: return align256(S * w.M * 4);
-        case 4: return align256(std::max(seg_sort_scratch_bytes((int)S, w.N), seg_sort_scratch_bytes((int)S, w.M)));
+        case 4: return scratch_in_slab(w) ? 0 : align256(sort_scratch_need(w));
         case 5: return align256(range_arrays_bytes((int)S, w.range_stream_max, w.C));
         case 6: return w.slab_rows ? align256(S * slab_rows(w.slab_rows) * (size_t)slab_stride(w.C) * 4) : 0;
         case 7: return (w.slab_rows && w.want_u) ? align256(S * w.slab_rows * 4) : 0;
@@ -115,7 +130,7 @@ SortedWs carve(void* ws, const WsSpec& w) {
     for (int i = 0; i < WS_PARTS; ++i) { part[i] = b; b += ws_part(w, i); }
     SortedWs r;
     r.ks = (float*)part[0]; r.kp = (uint32_t*)part[1]; r.qs = (float*)part[2]; r.qp = (uint32_t*)part[3];
-    r.sort_scratch = part[4];
+    r.sort_scratch = scratch_in_slab(w) ? part[6] : part[4];
     r.ra = carve_range_arrays(part[5], w.P * w.D, w.range_stream_max, w.C);
     r.slab = (float*)part[6]; r.uslab = (float*)part[7];
     r.uq = ws_part(w, 8) ? (float*)part[8] : nullptr;
@@ -192,6 +207,12 @@ static int group_q(const float* q, SortedWs& w, float qshift, int S, int N, int 
 // its own launch mostly waits for the reduce to drain and then runs alone.)
 static int sort_k_group_q(const float* k, const float* q, SortedWs& w, float qshift, int S, int N, int M, int C,
                           hipStream_t st) {
+    if (N == M && !group_fits(N, M, C)) {   // both sorted: as one sort
+        if (int e = hip_status(seg_sort2(k, w.ks, w.kp, q, w.qs, w.qp, S, N, w.sort_scratch, st),
+                               "segmented sort of k and q"))
+            return e;
+        return hip_status(query_bounds(w.ks, w.qs, w.ra.qb, qshift, S, N, M, C, st), "query bounds");
+    }
     if (int e = hip_status(seg_sort(k, w.ks, w.kp, S, N, w.sort_scratch, st), "segmented sort of k")) return e;
     return group_q(q, w, qshift, S, N, M, C, st);
 }
@@ -482,7 +503,7 @@ static WsSpec abs_fwd_spec(int P, int D, int N, int M, int C, bool full) { retur
 // The dense route's only workspace: the sort scratch of sorts kept for a backward that walks (none when the backward
 // is dense too, and none for segments of one LDS run).
 static size_t abs_dense_ws(int P, int pc, int D, int N, int M, int C) {
-    return dense_sign(P, N, M) ? 0 : ws_part(abs_fwd_spec(pc, D, N, M, C, true), 4);
+    return dense_sign(P, N, M) ? 0 : align256(sort_scratch_need(abs_fwd_spec(pc, D, N, M, C, true)));
 }
 
 size_t qlka_abs_fwd_ws_bytes(int P, int D, int N, int M, int C) {

@@ -32,8 +32,9 @@ size_t seg_sort_scratch_bytes(int S, int L);
 // Stable ascending sort of S contiguous segments of length L. Returns a hipError_t value (0 on success).
 int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch,
              hipStream_t st);
-// seg_sort of two arrays of S segments of length L, in one launch when the segments fit one LDS sort (so that the
-// two sorts start together when they run beside other work); scratch as seg_sort's, reused in turn otherwise
+// seg_sort of two arrays of S segments of length L as one sort of 2S segments: one LDS-sort launch (so that the two
+// sorts start together when they run beside other work) and, for segments longer than one LDS run, each merge pass
+// over both arrays in one launch; scratch of seg_sort_scratch_bytes(2 S, L) bytes
 int seg_sort2(const float* a, float* a_keys, uint32_t* a_perm, const float* b, float* b_keys, uint32_t* b_perm,
               int S, int L, void* scratch, hipStream_t st);
 

@@ -18,6 +18,7 @@
 #include "qlka_common.h"
 #include "qlka_internal.h"
 
+#include <atomic>
 #include <utility>
 
 namespace qlka {
@@ -373,13 +374,16 @@ __device__ __forceinline__ void c6_scan(const uint32_t a, const uint32_t b, uint
 // and then its keys, held in registers, into the index array: only the keys and the packed ranks stay live across a
 // pass, and no extra barrier is needed between the two scatters' reads and writes. Returns the array that holds the
 // sorted keys (the other holds the positions), at padded positions.
-template <int THREADS>
+template <int THREADS, bool OPAQUE_T = false>
 __device__ __forceinline__ bool count_sort6_run(CountSort6Lds<THREADS>& sm, const float* __restrict__ src,
                                                 const int len)
 {
     constexpr int BLKS = THREADS / 32;
     constexpr int ROW = THREADS + THREADS / 32;       // padded words of one digit pair's counter row
-    const int t = threadIdx.x;
+    int t = threadIdx.x;
+    // OPAQUE_T, for a kernel that sorts several runs in a loop: an opaque copy of t, or the addresses derived from it
+    // are hoisted out of that loop and kept live through every pass (256 VGPRs and spills)
+    if constexpr (OPAQUE_T) asm volatile("" : "+v"(t));
     {
         float f[C6_ITEMS];
 #pragma unroll
@@ -475,6 +479,7 @@ __device__ __forceinline__ bool count_sort6_run(CountSort6Lds<THREADS>& sm, cons
     return swapped;
 }
 
+// One run per workgroup: runs of segments that fit one LDS run (runs_per_seg == 1).
 template <int THREADS>
 __global__ __launch_bounds__(THREADS)
 void lds_count_sort6(const float* __restrict__ in1, const int seg_len, const int run_len, const int runs_per_seg,
@@ -510,6 +515,41 @@ void lds_count_sort6(const float* __restrict__ in1, const int seg_len, const int
             run_keys[seg_off + start + i] = keys[c6_pad(i)];
             run_idx[seg_off + start + i]  = (uint32_t)start + pos[c6_pad(i)];
         }
+    }
+}
+
+// Runs of segments longer than one LDS run (runs_per_seg > 1), into the run buffers for the merges (the second
+// array's runs after the first array's segments). A grid of at most one workgroup per CU (LDS holds one) loops over
+// the runs, so all of it is resident from its start and runs past the first round do not wait for CU slots behind a
+// reduce that started beside them (configs[4], 512 runs of 16384 keys a p: 85.6 -> 84.7 ms a call).
+template <int THREADS>
+__global__ __launch_bounds__(THREADS)
+void lds_count_sort6_runs(const float* __restrict__ in1, const int seg_len, const int run_len,
+                          const int runs_per_seg, uint32_t* __restrict__ run_keys, uint32_t* __restrict__ run_idx,
+                          const int blocks1, const float* __restrict__ in2)
+{
+    __shared__ CountSort6Lds<THREADS> sm;
+    const int total = in2 ? 2 * blocks1 : blocks1;
+    for (int b = blockIdx.x; b < total; b += gridDim.x) {
+        const bool second = b >= blocks1;
+        const int bid = second ? b - blocks1 : b;
+        const float* in = second ? in2 : in1;
+        const int seg   = bid / runs_per_seg;
+        const int run   = bid - seg * runs_per_seg;
+        const int start = run * run_len;
+        const int len   = min(run_len, seg_len - start);
+        const size_t seg_off = (size_t)seg * seg_len;
+        const bool swapped = count_sort6_run<THREADS, true>(sm, in + seg_off + start, len);
+        const uint32_t* const keys = swapped ? sm.idx : sm.key;
+        const uint32_t* const pos = swapped ? sm.key : sm.idx;
+        int t = threadIdx.x;
+        asm volatile("" : "+v"(t));                       // (see count_sort6_run's OPAQUE_T)
+        const size_t ro = seg_off + start + (second ? (size_t)(blocks1 / runs_per_seg) * seg_len : 0);
+        for (int i = t; i < len; i += THREADS) {
+            run_keys[ro + i] = keys[c6_pad(i)];
+            run_idx[ro + i]  = (uint32_t)start + pos[c6_pad(i)];
+        }
+        __syncthreads();                                  // every read of this run's LDS is done before the next load
     }
 }
 
@@ -567,7 +607,8 @@ __global__ __launch_bounds__(MERGE_THREADS)
 void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__ src_i,
                 uint32_t* __restrict__ dst_k, uint32_t* __restrict__ dst_i,
                 float* __restrict__ out_keys, uint32_t* __restrict__ out_perm, const int* __restrict__ splits,
-                const int seg_len, const int width, const int final_pass, const int blocks_per_seg)
+                const int seg_len, const int width, const int final_pass, const int blocks_per_seg,
+                const int S1, float* __restrict__ out_keys2, uint32_t* __restrict__ out_perm2)
 {
     __shared__ uint32_t sk[MERGE_TILE];
     __shared__ uint32_t si[MERGE_TILE];
@@ -626,9 +667,14 @@ void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__
         if (d + t < n) { sk[d + t] = rk[t]; si[d + t] = ri[t]; }
     __syncthreads();
     if (final_pass) {
+        // segments from S1 on belong to the second array (two arrays merged in one pass)
+        const bool second = seg >= S1;
+        float* const ok = second ? out_keys2 : out_keys;
+        uint32_t* const op = second ? out_perm2 : out_perm;
+        const size_t fo = (size_t)(second ? seg - S1 : seg) * seg_len + o0;
         for (int e = tid; e < n; e += MERGE_THREADS) {
-            out_keys[so + o0 + e] = ordered_to_float(sk[e]);
-            out_perm[so + o0 + e] = si[e];
+            ok[fo + e] = ordered_to_float(sk[e]);
+            op[fo + e] = si[e];
         }
     } else {
         for (int e = tid; e < n; e += MERGE_THREADS) {
@@ -636,6 +682,19 @@ void merge_runs(const uint32_t* __restrict__ src_k, const uint32_t* __restrict__
             dst_i[so + o0 + e] = si[e];
         }
     }
+}
+
+// Compute units of the current device (cached per device).
+static int device_cus() {
+    static std::atomic<int> cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    int n = cus[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cus[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
 }
 
 template <int WAVES, int ITEMS>
@@ -663,12 +722,37 @@ static void launch_cs6(const float* in, int S, int L, int run_len, int runs, flo
                        uint32_t* rk, uint32_t* ri, hipStream_t st, const float* in2 = nullptr, float* ok2 = nullptr,
                        uint32_t* op2 = nullptr) {
     StageTimer t("lds_count_sort", st);
-    const int blocks1 = S * runs;
-    hipLaunchKernelGGL((lds_count_sort6<THREADS>), dim3(in2 ? 2 * blocks1 : blocks1), dim3(THREADS), 0, st,
-                       in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
+    const int blocks1 = S * runs, total = in2 ? 2 * blocks1 : blocks1;
+    if (runs > 1)
+        hipLaunchKernelGGL((lds_count_sort6_runs<THREADS>), dim3(std::min(total, device_cus())), dim3(THREADS), 0, st,
+                           in, L, run_len, runs, rk, ri, blocks1, in2);
+    else
+        hipLaunchKernelGGL((lds_count_sort6<THREADS>), dim3(total), dim3(THREADS), 0, st,
+                           in, L, run_len, runs, ok, op, rk, ri, blocks1, in2, ok2, op2);
 }
 
 static inline int merge_tiles(int L) { return (L + MERGE_TILE - 1) / MERGE_TILE; }
+
+// Merge passes over the S segments of length L whose LDS-sorted runs are in (k0, i0): runs of LDS_SORT_MAX become one
+// sorted run per segment, ping-ponging with (k1, i1); the last pass writes floats and permutations, segments from S1
+// on to the second output. (The splits of the tiles follow the four run buffers in the scratch.)
+static int merge_passes(uint32_t* k0, uint32_t* i0, uint32_t* k1, uint32_t* i1, int* splits, int S, int L, int S1,
+                        float* out_keys, uint32_t* out_perm, float* out_keys2, uint32_t* out_perm2, hipStream_t st) {
+    const int bps = merge_tiles(L);
+    const int tiles = bps * S;
+    const dim3 grid((unsigned)tiles), pgrid((unsigned)((tiles + MERGE_THREADS / WAVE - 1) / (MERGE_THREADS / WAVE)));
+    for (int width = LDS_SORT_MAX; width < L; width *= 2) {
+        const int fin = (2 * width >= L);
+        StageTimer t("merge_runs", st);
+        hipLaunchKernelGGL(merge_partition, pgrid, dim3(MERGE_THREADS), 0, st, k0, splits, L, width, bps, tiles);
+        hipLaunchKernelGGL(merge_runs, grid, dim3(MERGE_THREADS), 0, st, k0, i0, k1, i1, out_keys, out_perm, splits,
+                           L, width, fin, bps, S1, out_keys2, out_perm2);
+        if (int err = (int)hipGetLastError()) return err;
+        std::swap(k0, k1);
+        std::swap(i0, i1);
+    }
+    return 0;
+}
 
 size_t seg_sort_scratch_bytes(int S, int L) {
     if (L <= LDS_SORT_MAX) return 0;
@@ -701,8 +785,16 @@ int seg_sort2(const float* a, float* a_keys, uint32_t* a_perm, const float* b, f
               int S, int L, void* scratch, hipStream_t st) {
     if (S <= 0 || L <= 0) return 0;
     if (L <= LDS_SORT_MAX) return lds_sort(a, a_keys, a_perm, b, b_keys, b_perm, S, L, st);
-    if (int e = seg_sort(a, a_keys, a_perm, S, L, scratch, st)) return e;
-    return seg_sort(b, b_keys, b_perm, S, L, scratch, st);
+    // both arrays' runs in one LDS-sort launch, then each merge pass over the 2S segments at once
+    const size_t n = 2 * (size_t)S * (size_t)L;
+    uint32_t* k0 = (uint32_t*)scratch;
+    uint32_t* i0 = k0 + n;
+    uint32_t* k1 = i0 + n;
+    uint32_t* i1 = k1 + n;
+    const int runs = (L + LDS_SORT_MAX - 1) / LDS_SORT_MAX;
+    launch_cs6<512>(a, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st, b, nullptr, nullptr);
+    if (int err = (int)hipGetLastError()) return err;
+    return merge_passes(k0, i0, k1, i1, (int*)(i1 + n), 2 * S, L, S, a_keys, a_perm, b_keys, b_perm, st);
 }
 
 int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L, void* scratch,
@@ -716,24 +808,8 @@ int seg_sort(const float* in, float* out_keys, uint32_t* out_perm, int S, int L,
     uint32_t* i1 = k1 + n;
     const int runs = (L + LDS_SORT_MAX - 1) / LDS_SORT_MAX;
     launch_cs6<512>(in, S, L, LDS_SORT_MAX, runs, nullptr, nullptr, k0, i0, st);
-    int err = (int)hipGetLastError();
-    if (err) return err;
-    const int bps = merge_tiles(L);
-    int* splits = (int*)(i1 + n);
-    const int tiles = bps * S;
-    const dim3 grid((unsigned)tiles), pgrid((unsigned)((tiles + MERGE_THREADS / WAVE - 1) / (MERGE_THREADS / WAVE)));
-    for (int width = LDS_SORT_MAX; width < L; width *= 2) {
-        const int fin = (2 * width >= L);
-        StageTimer t("merge_runs", st);
-        hipLaunchKernelGGL(merge_partition, pgrid, dim3(MERGE_THREADS), 0, st, k0, splits, L, width, bps, tiles);
-        hipLaunchKernelGGL(merge_runs, grid, dim3(MERGE_THREADS), 0, st, k0, i0, k1, i1, out_keys, out_perm, splits,
-                           L, width, fin, bps);
-        err = (int)hipGetLastError();
-        if (err) return err;
-        std::swap(k0, k1);
-        std::swap(i0, i1);
-    }
-    return 0;
+    if (int err = (int)hipGetLastError()) return err;
+    return merge_passes(k0, i0, k1, i1, (int*)(i1 + n), S, L, S, out_keys, out_perm, nullptr, nullptr, st);
 }
 
 }  // namespace qlka
