@@ -195,13 +195,14 @@ def config_timings(dev, reps=None, only=None):
 def sort_compare(dev, reps=10):
     """ms per call of libqlka's segmented stable sort (qlka_seg_sort: LDS radix runs + merge passes) and of
     torch.sort(dim=1, stable=True) (rocPRIM's segmented radix sort) on (a) 192 segments of 131072 keys, a configs[4]
-    chunk of 3 p, half of the keys on 256 exact levels, and (b) 1536 segments of 16384 N(0,1) keys; both sorts must
-    give the same permutation."""
+    chunk of 3 p, half of the keys on 256 exact levels, (b) 1536 segments of 16384 N(0,1) keys and (c) 256 segments of
+    16384, the key sort of one headline chunk of 4 p; both sorts must give the same permutation."""
     from qlka import _lib
     lib = _lib.load()
     out = {}
     g = torch.Generator(device=dev).manual_seed(0)
-    for name, S, L, ties in (("192x131072", 192, 131072, True), ("1536x16384", 1536, 16384, False)):
+    for name, S, L, ties in (("192x131072", 192, 131072, True), ("1536x16384", 1536, 16384, False),
+                             ("256x16384", 256, 16384, False)):
         x = torch.randn(S, L, device=dev, generator=g)
         if ties:
             x[:, ::2] = torch.round(x[:, ::2] * 16) / 16
