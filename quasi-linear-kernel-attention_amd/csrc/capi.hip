@@ -415,19 +415,31 @@ int run_pipeline(int P, const Plan& pl, void* ws, size_t copy, hipStream_t st, P
     // the reduce of chunk j - 2. (A stream wait costs 12-16 us of host time here, a record about 1 us.)
     auto hipc = [](hipError_t e, const char* what) { return e == hipSuccess ? QLKA_OK : hip_status((int)e, what); };
     int err = QLKA_OK;
+    bool joined = false;                                  // st already waited for everything on the side stream
     int j = 0;
     for (int p0 = 0; p0 < P && !err; p0 += pl.pc, ++j) {
         const int np = std::min(pl.pc, P - p0);
         void* buf = (char*)ws + (size_t)(j % 2) * copy;
         err = prep(p0, np, buf, st);
         if (!err) err = early(p0, np, buf, st);
-        if (!err && j >= 1) err = hipc(hipStreamWaitEvent(st, sd->reduced[(j - 1) % 2], 0), "pipeline");
+        const bool last = p0 + np >= P, next_last = !last && p0 + np + pl.pc >= P;
+        if (!err && j >= 1)
+            err = hipc(hipStreamWaitEvent(st, last ? sd->join : sd->reduced[(j - 1) % 2], 0), "pipeline");
         if (!err) err = main(p0, np, buf, st);
+        if (last) {
+            // The last chunk's back has nothing to run beside: on the caller's stream it skips a cross-stream wait
+            // (about 9 us of GPU time at the headline shape). The wait before this main was for the side stream's
+            // last work through the join event (system-scope fence), so no join is needed after it.
+            if (!err) err = back(p0, np, buf, st);
+            joined = !err;
+            break;
+        }
         if (!err) err = hipc(hipEventRecord(sd->walked, st), "pipeline");
         if (!err) err = hipc(hipStreamWaitEvent(sd->s, sd->walked, 0), "pipeline");
         if (!err) err = back(p0, np, buf, sd->s);
-        if (!err) err = hipc(hipEventRecord(sd->reduced[j % 2], sd->s), "pipeline");
+        if (!err) err = hipc(hipEventRecord(next_last ? sd->join : sd->reduced[j % 2], sd->s), "pipeline");
     }
+    if (joined) return QLKA_OK;
     // join whatever happened, so that nothing later on st can overtake work issued on the side stream
     const hipError_t r = hipEventRecord(sd->join, sd->s);
     const hipError_t w = r == hipSuccess ? hipStreamWaitEvent(st, sd->join, 0) : r;
