@@ -490,10 +490,15 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
         const size_t p = (size_t)p0;
         return sort_k_group_q(k + p * D * N, q + p * D * M, w, 0.f, np * D, N, M, C, s);
     };
+    // the range passes before the wait for the previous chunk's reduce, beside its tail (1.721 -> 1.707 ms)
+    auto early = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
+        const float* vp = v + (size_t)p0 * N * C;
+        return hip_status(laplace_prepare(w.ks, w.kp, vp, np, D, N, C, w.ra, s), "laplace ranges");
+    };
     auto main = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w = carve(buf, laplace_spec(np, D, N, M, C));
         const float* vp = v + (size_t)p0 * N * C;
-        if (int e = hip_status(laplace_prepare(w.ks, w.kp, vp, np, D, N, C, w.ra, s), "laplace ranges")) return e;
         if (int e = laplace_emit(w.ks, w.kp, w.qs, w.qp, vp, w.slab, w.uslab, np, D, N, M, C, w.ra, s))
             return hip_status(e, "laplace walk");
         order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
@@ -506,7 +511,7 @@ int qlka_laplace_fwd(const float* q, const float* k, const float* v, float* out_
         return hip_status(reduce_slabs(w.slab, uq, nullptr, nullptr, out_w + p * M * C, out_u + p * M, np, D, M, C, s),
                           "laplace reduce");
     };
-    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back);
+    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back, early);
 }
 
 // ---------------------------------------------------------------------------------------------------- abs forward
@@ -622,10 +627,15 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         }
         return sort_k_group_q(k + p * D * N, q + p * D * M, w, 0.f, np * D, N, M, C, s);
     };
+    // the range passes before the wait for the previous chunk's reduce, beside its tail
+    auto early = [&](int p0, int np, void* buf, hipStream_t s) {
+        SortedWs w; AbsWalkArgs a;
+        view(p0, np, buf, w, a);
+        return hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges");
+    };
     auto main = [&](int p0, int np, void* buf, hipStream_t s) {
         SortedWs w; AbsWalkArgs a;
         view(p0, np, buf, w, a);
-        if (int e = hip_status(abs_prepare(a, mode, w.ra, s), "abs ranges")) return e;
         if (int e = hip_status(abs_emit(a, mode, w.ra, s), "abs walk")) return e;
         if (out_u) order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
         return hip_status((int)hipGetLastError(), "v == 1 terms to query order");
@@ -638,7 +648,7 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         return hip_status(reduce_slabs(w.slab, uq, nullptr, nullptr, out_w + p * M * C,
                                        out_u ? out_u + p * M : nullptr, np, D, M, C, s), "abs reduce");
     };
-    if (int e = run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back)) return e;
+    if (int e = run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back, early)) return e;
     if (keep_sorts) *kept = keep->states ? 3 : 1;
     return QLKA_OK;
 }
