@@ -1059,13 +1059,18 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         return a;
     };
     const int abs_mode = ABS_ROW | ABS_ONES | (masked ? ABS_KEEP : 0);
-    // add_bump: the range passes beside the previous chunk's reduce
+    // the range passes (and add_riesz's per-p prefixes) before the wait for the previous chunk's reduce, beside it
     auto early = [&](int p0, int np, void* buf, hipStream_t s) {
-        if (!bump) return (int)QLKA_OK;
         const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
         chunk_in(p0, qc, kc, vc, npc, keepc, outc);
         LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
-        return hip_status(abs_prepare(abs_args(L.op, vc, keepc, np), abs_mode, L.op.ra, s), "abs ranges");
+        SortedWs& w = L.op;
+        if (kind == LAYER_ADD_LAPLACE)
+            return hip_status(laplace_prepare(w.ks, w.kp, vc, np, D, N, C, w.ra, s), "laplace ranges");
+        if (int e = hip_status(abs_prepare(abs_args(w, vc, keepc, np), abs_mode, w.ra, s), "abs ranges")) return e;
+        if (!bump)
+            if (int e = riesz_prefix(kc, vc, keepc, L.pre, np, D, N, C, s)) return hip_status(e, "riesz prefixes");
+        return (int)QLKA_OK;
     };
     auto main = [&](int p0, int np, void* buf, hipStream_t s) {
         const float *qc, *kc, *vc, *npc; const uint8_t* keepc; float* outc;
@@ -1073,7 +1078,6 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         LayerWs L = carve_layer(kind, buf, WsSpec{np, D, N, M, C, N, M, true});
         SortedWs& w = L.op;
         if (kind == LAYER_ADD_LAPLACE) {
-            if (int e = hip_status(laplace_prepare(w.ks, w.kp, vc, np, D, N, C, w.ra, s), "laplace ranges")) return e;
             if (int e = laplace_emit(w.ks, w.kp, w.qs, w.qp, vc, w.slab, w.uslab, np, D, N, M, C, w.ra, s))
                 return hip_status(e, "laplace walk");
             order_u_terms(w.uslab, w.qp, w.uq, np, D, M, s);
@@ -1081,10 +1085,7 @@ static int layer_fwd(int kind, const float* q, const float* k, const float* v, c
         }
         AbsWalkArgs a = abs_args(w, vc, keepc, np);
         const int mode = abs_mode;
-        if (!bump) {
-            if (int e = abs_prepare(a, mode, w.ra, s)) return hip_status(e, "abs ranges");
-            if (int e = riesz_prefix(kc, vc, keepc, L.pre, np, D, N, C, s)) return hip_status(e, "riesz prefixes");
-        } else {
+        if (bump) {
             a.nsets = 3;
             for (int ev = 1; ev < 3; ++ev) {
                 a.set_shift[ev] = shift[ev];
