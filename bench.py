@@ -94,14 +94,14 @@ def dense_flops(i, c):
     """Algorithmic flops of configuration i's workload on the dense route (configs[0], [1]): forming
     A[m, n] = sum_d f(q_d - k_d) costs a subtract and an add per (m, n, d) (|x| is a free operand modifier) plus the
     exponential for the Laplace kernel, the contraction A^T [v, 1] 2 (C + 1) per (m, n); each sign sum of the backward
-    forms G = X Y^T (2 C per (i, j)) and adds a selected +-G per (d, i, j) (2); grad_v is the forward with q and k
-    swapped (no row sums)."""
+    forms G = X Y^T (2 C per (i, j)) and adds a selected +-G per (d, i, j) (2); grad_v contracts the A the forward kept
+    with g_w (2 C per (m, n): a differentiable dense call keeps A, qlka_abs_fwd_dense_keep)."""
     P, D, N, C = c["P"], c["D"], c["N"], c["C"]
     M = N
     fwd_abs = 2.0 * P * M * N * D + 2.0 * P * M * N * (C + 1)
     if i == 0:
         sign = 2.0 * P * M * N * C + 2.0 * P * D * M * N
-        grad_v = 2.0 * P * M * N * D + 2.0 * P * M * N * C
+        grad_v = 2.0 * P * M * N * C
         return fwd_abs + 2 * sign + grad_v
     if i == 1:
         fwd_lap = 3.0 * P * M * N * D + 2.0 * P * M * N * (C + 1)

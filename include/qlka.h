@@ -133,6 +133,22 @@ int qlka_abs_bwd_sorted(const float* q, const float* k, const float* v, const fl
                         const void* states, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Dense forward and backward that share the kernel matrix A[p,m,n] = sum_d |k[p,d,n] - q[p,d,m]|. No counterpart in
+ * the reference, whose dense (KeOps) route forms A again in the backward (Weighted_Abs_Sum/weighted_abs_sum/
+ * keops_backend.py:19-48). qlka_abs_dense_keep_bytes is the size of A (P*M rows of (N + 3) & ~3 floats) where the
+ * forward and the backward both run the dense kernels and A stays within 256 MB, else 0; then qlka_abs_fwd_dense_keep
+ * computes what qlka_abs_fwd computes and also writes A, and qlka_abs_bwd_dense_kept, given that A and the same q, k, v,
+ * computes what qlka_abs_bwd computes, with grad_v as the contraction of A with g_w instead of forming A again
+ * (bit-identical gradients). Both take no workspace; both return QLKA_EINVAL where the size is 0.
+ */
+size_t qlka_abs_dense_keep_bytes(int P, int D, int N, int M, int C);
+int qlka_abs_fwd_dense_keep(const float* q, const float* k, const float* v, float* out_w, float* out_u, float* A,
+                            int P, int D, int N, int M, int C, void* stream);
+int qlka_abs_bwd_dense_kept(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                            float* grad_q, float* grad_k, float* grad_v, const float* A, int P, int D, int N, int M,
+                            int C, void* stream);
+
+/*
  * weighted_sgn_sum: out[p,d,m] = sum_n sgn(k[p,d,n] - q[p,d,m]) <v[p,n,:], g[p,m,:]>, with a tie counted +1
  * (it is the negated grad_q walk). Replaces _ext.weighted_sgn_sum_forward (Weighted_Abs_Sum/csrc/binding.cpp:384-439).
  */

@@ -326,14 +326,20 @@ int fork_join(hipStream_t st, KeySide key_side, QuerySide query_side) {
 // so grad_k runs on the side stream beside grad_q and then grad_v on the caller's stream: 0.355 -> 0.313 ms for a
 // forward + backward at that size. grad_q is launched before the side stream's wait (12-16 us of host time), so the
 // GPU does not wait for it.
+// A (nullable): the forward's kernel matrix (direct_fwd_keep_a); grad_v is then its contraction with g_w instead of
+// the dense sum with the roles of q and k swapped, which forms A again (1.47 G of the 7.4 G VALU lane-operations of a
+// forward + backward at P = 32, N = M = 600), with the same bits.
 int dense_bwd(float tie, const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
-              float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, hipStream_t st) {
+              float* grad_q, float* grad_k, float* grad_v, int P, int D, int N, int M, int C, hipStream_t st,
+              const float* A = nullptr) {
     // grad_q[d, m] = sum_n s(q - k) (<g_w[m], v[n]> + g_u[m])
     auto gq = [&](hipStream_t s) { return direct_sign(true, q, k, g_w, v, g_u, grad_q, tie, 1.f, P, D, M, N, C, s); };
     // grad_k[d, n] = sum_m s(k - q) (<v[n], g_w[m]> + g_u[m])
     auto gk = [&](hipStream_t s) { return direct_sign(false, k, q, v, g_w, g_u, grad_k, tie, 1.f, P, D, N, M, C, s); };
     // grad_v[n, :] = sum_m A[m, n] g_w[m, :]: the dense abs sum with the roles of q and k swapped
-    auto gv = [&](hipStream_t s) { return direct_fwd(0, k, q, g_w, grad_v, nullptr, P, D, M, N, C, s); };
+    auto gv = [&](hipStream_t s) {
+        return A ? dense_at_g(A, g_w, grad_v, P, N, M, C, s) : direct_fwd(0, k, q, g_w, grad_v, nullptr, P, D, M, N, C, s);
+    };
     SideStream* sd = nullptr;
     if (hipError_t e = side_stream(st, &sd)) return hip_status((int)e, "side stream");
     int e = QLKA_OK;
@@ -675,6 +681,43 @@ size_t qlka_abs_keep_state_bytes(int P, int D, int N, int M, int C) {
 }
 
 int qlka_abs_bwd_walks(int P, int N, int M) { return (P > 0 && N > 0 && M > 0 && !dense_sign(P, N, M)) ? 1 : 0; }
+
+// ---- dense forward + backward sharing the kernel matrix A[p,m,n] = sum_d |k[p,d,n] - q[p,d,m]|
+// Kept where both directions run dense, the forward runs the tiled kernel, and A (P*M rows of pad4(N) floats) stays
+// within DENSE_KEEP_MAX: 46 MB at P = 32, N = M = 600.
+constexpr size_t DENSE_KEEP_MAX = size_t(256) << 20;
+
+size_t qlka_abs_dense_keep_bytes(int P, int D, int N, int M, int C) {
+    if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || C > 128 || N > 131072 || M > 131072) return 0;
+    if ((int64_t)P * D * std::max(N, M) > (int64_t)INT32_MAX) return 0;
+    if (!dense_abs_fwd(N, M) || !dense_sign(P, N, M) || !direct_fwd_tiled(D, N, M, C)) return 0;
+    const size_t bytes = (size_t)P * M * (size_t)((N + 3) & ~3) * sizeof(float);
+    return bytes <= DENSE_KEEP_MAX ? bytes : 0;
+}
+
+int qlka_abs_fwd_dense_keep(const float* q, const float* k, const float* v, float* out_w, float* out_u, float* A,
+                            int P, int D, int N, int M, int C, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !out_w || !A) return fail(QLKA_EINVAL, "q, k, v, out_w and A must be non-null");
+    if (qlka_abs_dense_keep_bytes(P, D, N, M, C) == 0)
+        return fail(QLKA_EINVAL, "the dense kernel matrix is not kept at this shape (qlka_abs_dense_keep_bytes is 0)");
+    return hip_status(direct_fwd_keep_a(q, k, v, out_w, out_u, A, P, D, N, M, C, (hipStream_t)stream),
+                      "abs direct sum keeping A");
+}
+
+int qlka_abs_bwd_dense_kept(const float* q, const float* k, const float* v, const float* g_w, const float* g_u,
+                            float* grad_q, float* grad_k, float* grad_v, const float* A, int P, int D, int N, int M,
+                            int C, void* stream) {
+    g_err.clear();
+    if (int e = check_dims(P, D, N, M, C)) return e;
+    if (!q || !k || !v || !g_w || !grad_q || !grad_k || !grad_v || !A)
+        return fail(QLKA_EINVAL, "q, k, v, g_w, the three gradients and A must be non-null");
+    if (qlka_abs_dense_keep_bytes(P, D, N, M, C) == 0)
+        return fail(QLKA_EINVAL, "the dense kernel matrix is not kept at this shape (qlka_abs_dense_keep_bytes is 0)");
+    // the walks' convention, as qlka_abs_bwd: a tie counts -1 in both gradients
+    return dense_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, (hipStream_t)stream, A);
+}
 
 // --------------------------------------------------------------------------------------------------- abs backward
 static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {

@@ -181,10 +181,10 @@ void direct_fwd_small_kernel(const float* __restrict__ q, const float* __restric
 // tiled sign sums: raw buffer descriptors that end at the segment's end (rows past it read 0), fixed LDS row strides;
 // columns past the tile (keys past N, queries past M, channels past C) may read the next row and never reach an
 // output or A (an MFMA output column depends only on its own column of v).
-template <int KIND, int IT, int CM>
+template <int KIND, int IT, int CM, bool SAVE = false>
 __global__ __launch_bounds__(ST_T)
 void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-                             float* __restrict__ out_w, float* __restrict__ out_u,
+                             float* __restrict__ out_w, float* __restrict__ out_u, float* __restrict__ a_out,
                              const int D, const int N, const int M, const int C, const int mtiles)
 {
     constexpr int DCK = 64;                               // features per chunk
@@ -275,6 +275,22 @@ void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restric
         if (h + 1 < chunks) continue;
         // the A tile is complete: keys past N weigh 0 (v reads 0 there, out_u would not)
         const int Nl = min(ST_JT, N - n0);
+        if constexpr (SAVE) {                             // kept for the backward: A[p][m][n], rows of pad4(N)
+            const int NP = (N + 3) & ~3, n = n0 + an;
+#pragma unroll
+            for (int u = 0; u < QM; ++u) {
+                const int m = mb + am + u;
+                if (m >= M || n >= N) continue;
+                float* row = a_out + ((size_t)p * M + m) * NP + n;
+                if (n + 3 < N) {
+                    *reinterpret_cast<f4_t*>(row) = f4_t{a[0][u], a[1][u], a[2][u], a[3][u]};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < N) row[r] = a[r][u];
+                }
+            }
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -312,19 +328,131 @@ void direct_fwd_tiled_kernel(const float* __restrict__ q, const float* __restric
 }
 
 template <int KIND, int IT, int CM>
-static void launch_fwd_tiled(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P,
-                             int D, int N, int M, int C, hipStream_t st) {
+static void launch_fwd_tiled(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                             float* a_out, int P, int D, int N, int M, int C, hipStream_t st) {
     const int mtiles = (M + IT - 1) / IT;
-    hipLaunchKernelGGL((direct_fwd_tiled_kernel<KIND, IT, CM>), dim3((unsigned)(P * mtiles)), dim3(ST_T), 0, st, q, k,
-                       v, out_w, out_u, D, N, M, C, mtiles);
+    if constexpr (KIND == 0) {                            // only the abs sum keeps A
+        if (a_out != nullptr) {
+            hipLaunchKernelGGL((direct_fwd_tiled_kernel<KIND, IT, CM, true>), dim3((unsigned)(P * mtiles)), dim3(ST_T),
+                               0, st, q, k, v, out_w, out_u, a_out, D, N, M, C, mtiles);
+            return;
+        }
+    }
+        hipLaunchKernelGGL((direct_fwd_tiled_kernel<KIND, IT, CM>), dim3((unsigned)(P * mtiles)), dim3(ST_T), 0, st,
+                           q, k, v, out_w, out_u, nullptr, D, N, M, C, mtiles);
 }
 
 template <int KIND>
-static void launch_fwd_tiled(const float* q, const float* k, const float* v, float* out_w, float* out_u, int P,
-                             int D, int N, int M, int C, hipStream_t st) {
-    if (pad4(C) <= 32) launch_fwd_tiled<KIND, 64, 32>(q, k, v, out_w, out_u, P, D, N, M, C, st);
-    else if (pad4(C) <= 64) launch_fwd_tiled<KIND, 32, 64>(q, k, v, out_w, out_u, P, D, N, M, C, st);
-    else launch_fwd_tiled<KIND, 32, 128>(q, k, v, out_w, out_u, P, D, N, M, C, st);
+static void launch_fwd_tiled(const float* q, const float* k, const float* v, float* out_w, float* out_u,
+                             float* a_out, int P, int D, int N, int M, int C, hipStream_t st) {
+    if (pad4(C) <= 32) launch_fwd_tiled<KIND, 64, 32>(q, k, v, out_w, out_u, a_out, P, D, N, M, C, st);
+    else if (pad4(C) <= 64) launch_fwd_tiled<KIND, 32, 64>(q, k, v, out_w, out_u, a_out, P, D, N, M, C, st);
+    else launch_fwd_tiled<KIND, 32, 128>(q, k, v, out_w, out_u, a_out, P, D, N, M, C, st);
+}
+
+// The dense forward runs the tiled kernel (which can keep A) unless the segments fit the one-workgroup kernel.
+bool direct_fwd_tiled(int D, int N, int M, int C) {
+    return !(pad4(M) <= DS_MAX && pad4(N) <= DS_MAX && direct_fwd_small_lds(D, N, M, C) <= DS_LDS_MAX);
+}
+
+// The abs forward of the tiled kernel that also writes A[p][m][n] = sum_d |q[p,d,m] - k[p,d,n]| (rows of pad4(N)
+// floats) to a_out, for dense_at_g; only where direct_fwd_tiled(D, N, M, C).
+int direct_fwd_keep_a(const float* q, const float* k, const float* v, float* out_w, float* out_u, float* a_out,
+                      int P, int D, int N, int M, int C, hipStream_t st) {
+    if (!direct_fwd_tiled(D, N, M, C) || a_out == nullptr) return (int)hipErrorInvalidValue;
+    StageTimer t("direct_fwd", st);
+    launch_fwd_tiled<0>(q, k, v, out_w, out_u, a_out, P, D, N, M, C, st);
+    return (int)hipGetLastError();
+}
+
+// out[p, n, :] = sum_m A[p, m, n] g[p, m, :] from a kept A ([p][m][pad4(N)], direct_fwd_keep_a): grad_v of the dense
+// abs sum without forming A again. The contraction of direct_fwd_tiled_kernel with A loaded instead of formed: one
+// workgroup of 256 threads per (p, tile of IT keys) walks the queries in tiles of ST_JT; A's tile ([m][n]) and g's rows
+// ([m][c], zero past M) go to LDS and the MFMA blocks, their order over m and so the sums are the forward kernel's
+// (its grad_v form, with the roles of q and k swapped, gives the same bits).
+template <int IT, int CM>
+__global__ __launch_bounds__(ST_T)
+void dense_at_g_kernel(const float* __restrict__ A, const float* __restrict__ g, float* __restrict__ out,
+                       const int N, const int M, const int C, const int ntiles)
+{
+    constexpr int VS = CM + 4;
+    constexpr int KV = CM / 4;                            // g values per thread (4 threads per row)
+    constexpr int AE = ST_JT * IT / ST_T;                 // A values per thread (4 threads per row)
+    constexpr int NBC = CM / 16, BW = (IT / 16) * NBC / 4;
+    static_assert(BW >= 1 && NBC % BW == 0 && AE % 4 == 0, "tile shape");
+    __shared__ float At[ST_JT * IT];                      // [m][n]
+    __shared__ float vs[ST_JT * VS];                      // [m][c]
+    const int p = blockIdx.x / ntiles, nb = (blockIdx.x - p * ntiles) * IT, tid = threadIdx.x;
+    const int Nl = min(IT, N - nb), NP = (N + 3) & ~3;
+    const int sr = tid / 4, sc = tid - sr * 4;
+    f4_t av[AE / 4];
+    float vv[KV];
+    auto load = [&](int m0) {
+        const int m = m0 + sr;
+#pragma unroll
+        for (int e = 0; e < AE / 4; ++e) {
+            const int n = nb + sc * AE + 4 * e;
+            av[e] = (m < M && n < NP) ? *reinterpret_cast<const f4_t*>(A + ((size_t)p * M + m) * NP + n)
+                                      : f4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        const rsrc_t rv = make_rsrc(g + ((size_t)p * M + m0) * C, (uint32_t)((M - m0) * C * 4));
+#pragma unroll
+        for (int e = 0; e < KV; ++e) vv[e] = buf_load(rv, (sr * C + sc + 4 * e) * 4, 0);
+    };
+    const int wv = wave_in_block(), ln = lane_id();
+    const int ni = (wv * BW) / NBC, cb0 = (wv * BW) % NBC;  // this wave's key block and first channel block
+    f4_t acc[BW];
+#pragma unroll
+    for (int t = 0; t < BW; ++t) acc[t] = f4_t{0.f, 0.f, 0.f, 0.f};
+    const int mt = (M + ST_JT - 1) / ST_JT;
+    load(0);
+    for (int t = 0; t < mt; ++t) {
+        __syncthreads();                                  // readers of the previous tile are done
+#pragma unroll
+        for (int e = 0; e < AE / 4; ++e) *reinterpret_cast<f4_t*>(At + sr * IT + sc * AE + 4 * e) = av[e];
+#pragma unroll
+        for (int e = 0; e < KV; ++e) vs[sr * VS + sc + 4 * e] = vv[e];
+        if (t + 1 < mt) load((t + 1) * ST_JT);
+        __syncthreads();
+        const float* Ap = At + (ln >> 4) * IT + ni * 16 + (ln & 15);
+        const float* Vp = vs + (ln >> 4) * VS + cb0 * 16 + (ln & 15);
+#pragma unroll 4
+        for (int kk = 0; kk < ST_JT / 4; ++kk) {
+            const float a = Ap[kk * 4 * IT];
+#pragma unroll
+            for (int b = 0; b < BW; ++b)
+                acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Vp[kk * 4 * VS + b * 16], acc[b], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int n = ni * 16 + 4 * (ln >> 4) + r;
+        if (n >= Nl) continue;
+        float* o = out + ((size_t)p * N + nb + n) * C;
+#pragma unroll
+        for (int b = 0; b < BW; ++b) {
+            const int c = (cb0 + b) * 16 + (ln & 15);
+            if (c < C) o[c] = acc[b][r];
+        }
+    }
+}
+
+int dense_at_g(const float* A, const float* g, float* out, int P, int N, int M, int C, hipStream_t st) {
+    StageTimer t("direct_fwd", st);
+    if (pad4(C) <= 32) {
+        const int nt = (N + 63) / 64;
+        hipLaunchKernelGGL((dense_at_g_kernel<64, 32>), dim3((unsigned)(P * nt)), dim3(ST_T), 0, st, A, g, out, N, M, C,
+                           nt);
+    } else if (pad4(C) <= 64) {
+        const int nt = (N + 31) / 32;
+        hipLaunchKernelGGL((dense_at_g_kernel<32, 64>), dim3((unsigned)(P * nt)), dim3(ST_T), 0, st, A, g, out, N, M, C,
+                           nt);
+    } else {
+        const int nt = (N + 31) / 32;
+        hipLaunchKernelGGL((dense_at_g_kernel<32, 128>), dim3((unsigned)(P * nt)), dim3(ST_T), 0, st, A, g, out, N, M,
+                           C, nt);
+    }
+    return (int)hipGetLastError();
 }
 
 int direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
@@ -343,8 +471,8 @@ int direct_fwd(int kind, const float* q, const float* k, const float* v, float* 
         return (int)hipGetLastError();
     }
     StageTimer t("direct_fwd", st);
-    if (kind == 0) launch_fwd_tiled<0>(q, k, v, out_w, out_u, P, D, N, M, C, st);
-    else launch_fwd_tiled<1>(q, k, v, out_w, out_u, P, D, N, M, C, st);
+    if (kind == 0) launch_fwd_tiled<0>(q, k, v, out_w, out_u, nullptr, P, D, N, M, C, st);
+    else launch_fwd_tiled<1>(q, k, v, out_w, out_u, nullptr, P, D, N, M, C, st);
     return (int)hipGetLastError();
 }
 

@@ -191,6 +191,13 @@ int range_count(int Ns, int C);          // key ranges per segment
 // Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null
 int direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
                int P, int D, int N, int M, int C, hipStream_t st);
+// The dense abs forward keeping its kernel matrix A[p][m][n] = sum_d |q[p,d,m] - k[p,d,n]| (P*M rows of pad4(N) floats)
+// in a_out, where the tiled kernel runs (direct_fwd_tiled); and out[p,n,:] = sum_m A[p,m,n] g[p,m,:] from such an A (the
+// dense grad_v, bit-identical to forming A again)
+bool direct_fwd_tiled(int D, int N, int M, int C);
+int direct_fwd_keep_a(const float* q, const float* k, const float* v, float* out_w, float* out_u, float* a_out,
+                      int P, int D, int N, int M, int C, hipStream_t st);
+int dense_at_g(const float* A, const float* g, float* out, int P, int N, int M, int C, hipStream_t st);
 // out[d, i] = scale * sum_j s(a[d,i] - b[d,j]) (<x[i], y[j]> + g_u[own ? i : j]), s(0) = tie; a (P, D, I), b (P, D, J),
 // x (P, I, C), y (P, J, C), g_u nullable
 int direct_sign(bool gu_own, const float* a, const float* b, const float* x, const float* y, const float* gu,

@@ -134,6 +134,35 @@ std::tuple<Tensor, OptTensor, std::vector<Tensor>> abs_forward_keep(const Tensor
     return {out, out_u, srt};
 }
 
+// The dense route's forward that keeps its kernel matrix A (P, M, (N + 3) & ~3) for the backward, and that backward
+// (qlka_abs_fwd_dense_keep / qlka_abs_bwd_dense_kept): only where qlka_abs_dense_keep_bytes is nonzero.
+std::tuple<Tensor, OptTensor, Tensor> abs_forward_dense_keep(const Tensor& q, const Tensor& k, const Tensor& v,
+                                                             bool full) {
+    const Dims d = check_qkv(q, k, v);
+    c10::DeviceGuard guard(q.device());
+    Tensor out = empty_f({d.P, d.M, d.C}, q);
+    OptTensor out_u;
+    if (full) out_u = empty_f({d.P, d.M}, q);
+    Tensor A = empty_f({d.P, d.M, (d.N + 3) & ~int64_t(3)}, q);
+    check_rc(qlka_abs_fwd_dense_keep(fptr(q), fptr(k), fptr(v), fptr(out), fptr(out_u), fptr(A), d.P, d.D, d.N, d.M,
+                                     d.C, stream_of(q)));
+    return {out, out_u, A};
+}
+
+std::tuple<Tensor, Tensor, Tensor> abs_backward_dense_kept(const Tensor& q, const Tensor& k, const Tensor& v,
+                                                           const Tensor& g_w, const OptTensor& g_u, const Tensor& A) {
+    const Dims d = check_qkv(q, k, v);
+    check_grad("g_w", g_w, q, {d.P, d.M, d.C});
+    if (g_u.has_value()) check_grad("g_u", *g_u, q, {d.P, d.M});
+    TORCH_CHECK(A.sizes() == at::IntArrayRef({d.P, d.M, (d.N + 3) & ~int64_t(3)}) && A.is_contiguous(),
+                "kept kernel matrix does not match q and k");
+    c10::DeviceGuard guard(q.device());
+    Tensor gq = empty_f({d.P, d.D, d.M}, q), gk = empty_f({d.P, d.D, d.N}, q), gv = empty_f({d.P, d.N, d.C}, q);
+    check_rc(qlka_abs_bwd_dense_kept(fptr(q), fptr(k), fptr(v), fptr(g_w), fptr(g_u), fptr(gq), fptr(gk), fptr(gv),
+                                     fptr(A), d.P, d.D, d.N, d.M, d.C, stream_of(q)));
+    return {gq, gk, gv};
+}
+
 std::tuple<Tensor, Tensor, Tensor> abs_backward(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& g_w,
                                                 const OptTensor& g_u) {
     const Dims d = check_qkv(q, k, v);
@@ -271,17 +300,26 @@ struct AbsSumFn : public torch::autograd::Function<AbsSumFn> {
         std::vector<Tensor> srt;
         Tensor out;
         OptTensor out_u;
+        bool dense_a = false;                 // srt holds the dense route's kernel matrix
         if (path == DIRECT) {
             q = q.contiguous();
             k = k.contiguous();
             v = v.contiguous();
             std::tie(out, out_u) = direct_forward(q, k, v, full);
+        } else if (keep && q.dim() == 3 && k.dim() == 3 && v.dim() == 3 &&     // else check_qkv raises below
+                   qlka_abs_dense_keep_bytes((int)q.size(0), (int)q.size(1), (int)k.size(2), (int)q.size(2),
+                                             (int)v.size(2)) > 0) {
+            Tensor A;
+            std::tie(out, out_u, A) = abs_forward_dense_keep(q, k, v, full);
+            srt = {A};
+            dense_a = true;
         } else if (keep) {
             std::tie(out, out_u, srt) = abs_forward_keep(q, k, v, path, full);
         } else {
             std::tie(out, out_u) = abs_forward(q, k, v, path, full);
         }
-        ctx->saved_data["sorted"] = !srt.empty();
+        ctx->saved_data["sorted"] = !srt.empty() && !dense_a;
+        ctx->saved_data["dense_a"] = dense_a;
         std::vector<Tensor> saved = {q, k, v};
         saved.insert(saved.end(), srt.begin(), srt.end());
         ctx->save_for_backward(saved);
@@ -304,6 +342,8 @@ struct AbsSumFn : public torch::autograd::Function<AbsSumFn> {
         Tensor gq, gk, gv;
         if (path == DIRECT)
             std::tie(gq, gk, gv) = direct_backward(q, k, v, g_w, g_u, 0.0);
+        else if (ctx->saved_data["dense_a"].toBool())
+            std::tie(gq, gk, gv) = abs_backward_dense_kept(q, k, v, g_w, g_u, saved[3]);
         else if (ctx->saved_data["sorted"].toBool())
             std::tie(gq, gk, gv) = abs_backward_sorted(q, k, v, g_w, g_u,
                                                        std::vector<Tensor>(saved.begin() + 3, saved.end()));

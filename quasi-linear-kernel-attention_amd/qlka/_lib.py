@@ -35,6 +35,9 @@ _SIGNATURES = {
     "qlka_abs_keep_state_bytes": (_c_size, [_c_int] * 5),
     "qlka_abs_fwd_keep": (_c_int, [_c_ptr] * 5 + [_c_int] * 6 + [_c_ptr] * 6 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_abs_bwd_sorted": (_c_int, [_c_ptr] * 8 + [_c_int] * 5 + [_c_ptr] * 5 + [_c_ptr, _c_size, _c_ptr]),
+    "qlka_abs_dense_keep_bytes": (_c_size, [_c_int] * 5),
+    "qlka_abs_fwd_dense_keep": (_c_int, [_c_ptr] * 6 + [_c_int] * 5 + [_c_ptr]),
+    "qlka_abs_bwd_dense_kept": (_c_int, [_c_ptr] * 9 + [_c_int] * 5 + [_c_ptr]),
     "qlka_sgn_fwd_ws_bytes": (_c_size, [_c_int] * 5),
     "qlka_sgn_fwd": (_c_int, [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr, _c_size, _c_ptr]),
     "qlka_direct_fwd": (_c_int, [_c_int] + [_c_ptr] * 5 + [_c_int] * 5 + [_c_ptr]),

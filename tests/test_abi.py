@@ -194,3 +194,19 @@ def test_keep_sorts_entries_validate(lib):
         assert lib.qlka_abs_bwd_walks(12, 16384, 17) == 1
     finally:
         lib.qlka_set_direct_max(prev)
+
+
+def test_dense_keep_entries(lib):
+    # the dense route keeps A (P*M rows of pad4(N) floats) where the forward and the backward both run dense, the
+    # forward runs its tiled kernel (segments over 128) and A stays within 256 MB
+    assert lib.qlka_abs_dense_keep_bytes(32, 64, 600, 600, 64) == 32 * 600 * 600 * 4
+    assert lib.qlka_abs_dense_keep_bytes(3, 5, 301, 200, 33) == 3 * 200 * 304 * 4
+    assert lib.qlka_abs_dense_keep_bytes(12, 64, 16384, 16384, 64) == 0      # walks
+    assert lib.qlka_abs_dense_keep_bytes(12, 64, 600, 600, 64) == 0          # the backward walks at L = 600, P = 12
+    assert lib.qlka_abs_dense_keep_bytes(512, 32, 65, 65, 32) == 0           # the one-workgroup kernel
+    assert lib.qlka_abs_dense_keep_bytes(4096, 8, 512, 512, 8) == 0          # A over 256 MB
+    # shapes where nothing is kept are rejected before any launch
+    rc = lib.qlka_abs_fwd_dense_keep(1, 1, 1, 1, None, 1, 12, 64, 16384, 16384, 64, None)
+    assert rc != 0 and b"not kept" in lib.qlka_last_error()
+    rc = lib.qlka_abs_bwd_dense_kept(1, 1, 1, 1, None, 1, 1, 1, None, 32, 64, 600, 600, 64, None)
+    assert rc != 0 and b"non-null" in lib.qlka_last_error()

@@ -327,6 +327,40 @@ def test_autograd_keeps_sorts_for_backward(dev, shape, full):
     _assert_rel(grads[True][2], wv, nv, "kept-sorts grad_v")
 
 
+@pytest.mark.parametrize("shape", [(3, 5, 301, 200, 33),     # dense route, A kept by the forward
+                                   (32, 16, 600, 520, 64),  # the dense backward at L = 600 (enough workgroups)
+                                   (2, 3, 150, 500, 128)])
+@pytest.mark.parametrize("full", [True, False])
+def test_autograd_keeps_dense_matrix(dev, shape, full):
+    # On the dense route a differentiable "cuda" forward keeps its kernel matrix A for the backward, whose grad_v is
+    # then A's contraction with g_w instead of forming A again: the gradients must equal those of the backward that
+    # forms it (the extension's plain backward), bit for bit, and the oracle's.
+    from qlka import _lib
+    from weighted_abs_sum import _ext, weighted_abs_sum, weighted_abs_sum_full
+    P, D, N, M, C = shape
+    assert _lib.load().qlka_abs_dense_keep_bytes(P, D, N, M, C) > 0
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) + 3, kind="ties")
+    rng = np.random.default_rng(13)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+    if full:
+        w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+        torch.autograd.backward([w, u], [_t(g_w, dev), _t(g_u, dev)])
+        ref = _ext.weighted_abs_sum_full_backward(_t(q, dev), _t(k, dev), _t(v, dev), _t(g_w, dev), _t(g_u, dev))
+    else:
+        w = weighted_abs_sum(tq, tk, tv, backend="cuda")
+        w.backward(_t(g_w, dev))
+        ref = _ext.weighted_abs_sum_backward(_t(q, dev), _t(k, dev), _t(v, dev), _t(g_w, dev))
+    got = [_np(t.grad) for t in (tq, tk, tv)]
+    for name, a, b in zip(("grad_q", "grad_k", "grad_v"), got, ref):
+        np.testing.assert_array_equal(a, _np(b), err_msg=f"{name}: kept A vs forming A again")
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u if full else None)
+    _assert_rel(got[0], wq, nq, "kept-A grad_q")
+    _assert_rel(got[1], wk, nk, "kept-A grad_k")
+    _assert_rel(got[2], wv, nv, "kept-A grad_v")
+
+
 @pytest.mark.parametrize("shape", [(2, 3, 1500, 1300, 16),      # one chunk
                                    (6, 64, 16384, 16384, 32),   # pipelined chunks of 2 p
                                    (2, 8, 40000, 30000, 65)])   # two-launch scans, two channel slots per lane
