@@ -8,6 +8,7 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -724,9 +725,72 @@ static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
     return WsSpec{P, D, N, M, C, std::max(N, M), N, false};   // the grad_v slab has one row per key
 }
 
+// The backward as one walk over the merged keys and queries (mbw.hip) where its sums can load rows 16 bytes at a time
+// and one channel slot per lane covers a row. Its workspace per chunk: the backward's own sorts (when the forward kept
+// none), the merged values and tags, the entry states of its scans and their aggregates, and the slab, which also
+// holds the sort scratch and the range summaries (both dead before the walk writes it).
+static bool mbw_applies(int C) { return C <= 64 && C % 4 == 0; }
+
+struct MbwWs {
+    float* ks; uint32_t* kp; float* qs; uint32_t* qp; void* sort_scratch;
+    float* mv; uint32_t* mt;
+    float *sa_q, *sb_q, *sa_k, *sa_e;              // summaries (in the slab region)
+    float *ta_q, *tb_q, *ta_k, *ta_e;              // entry states
+    float* aggs; float* slab; int G;
+};
+
+static size_t mbw_rows_bytes(size_t S, int G, int C) { return align256(S * (size_t)(G + 1) * (size_t)(C + 2) * 4); }
+
+static size_t mbw_part(int P, int D, int N, int M, int C, int i) {
+    const size_t S = (size_t)P * D;
+    const int L = N + M, G = (L + 63) / 64;
+    switch (i) {
+        case 0: case 1: return align256(S * N * 4);
+        case 2: case 3: return align256(S * M * 4);
+        case 4: case 5: return align256(S * L * 4);
+        case 6: return 4 * mbw_rows_bytes(S, G, C);
+        case 7: return align256(scan_agg_bytes((int)S, L, C));
+        case 8: {
+            const size_t slab = align256(S * slab_rows(N) * (size_t)slab_stride(C) * 4);
+            return std::max({slab, 4 * mbw_rows_bytes(S, G, C), align256(sort_scratch_need(abs_bwd_spec(P, D, N, M, C)))});
+        }
+    }
+    return 0;
+}
+
+static size_t mbw_ws_bytes(int P, int D, int N, int M, int C) {
+    size_t b = 0;
+    for (int i = 0; i < 9; ++i) b += mbw_part(P, D, N, M, C, i);
+    return b;
+}
+
+static MbwWs mbw_carve(void* ws, int P, int D, int N, int M, int C) {
+    char* part[9];
+    char* b = (char*)ws;
+    for (int i = 0; i < 9; ++i) { part[i] = b; b += mbw_part(P, D, N, M, C, i); }
+    const size_t S = (size_t)P * D;
+    MbwWs w;
+    w.G = (N + M + 63) / 64;
+    const size_t rb = mbw_rows_bytes(S, w.G, C);
+    w.ks = (float*)part[0]; w.kp = (uint32_t*)part[1]; w.qs = (float*)part[2]; w.qp = (uint32_t*)part[3];
+    w.mv = (float*)part[4]; w.mt = (uint32_t*)part[5];
+    w.ta_q = (float*)part[6]; w.tb_q = (float*)(part[6] + rb); w.ta_k = (float*)(part[6] + 2 * rb);
+    w.ta_e = (float*)(part[6] + 3 * rb);
+    w.aggs = mbw_part(P, D, N, M, C, 7) ? (float*)part[7] : nullptr;
+    w.slab = (float*)part[8];
+    w.sort_scratch = part[8];
+    w.sa_q = (float*)part[8]; w.sb_q = (float*)(part[8] + rb); w.sa_k = (float*)(part[8] + 2 * rb);
+    w.sa_e = (float*)(part[8] + 3 * rb);
+    return w;
+}
+
 size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0) return 0;
     if (dense_sign(P, N, M)) return 0;            // the dense route takes no workspace
+    if (mbw_applies(C)) {
+        auto bm = [&](int pc) { return mbw_ws_bytes(pc, D, N, M, C); };
+        return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, N), bm), bm);
+    }
     auto b1 = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
     return plan_bytes(plan_chunks(P, g_ws_budget.load(std::memory_order_relaxed), pipelined(P, D, N), b1), b1);
 }
@@ -734,6 +798,61 @@ size_t qlka_abs_bwd_ws_bytes(int P, int D, int N, int M, int C) {
 }  // extern "C"
 
 namespace {
+// The merged backward (mbw.hip), per chunk: the sorts (unless the forward kept them) and the merge of the sorted q and k
+// with its range summaries (prep); the scans (early, before the wait for the previous chunk's reduce); the walk (main);
+// the grad_v reduce (back). Copy j % 2's slab region, which holds the summaries, is free at prep of chunk j: main of
+// chunk j - 1 waited for the reduce of chunk j - 2.
+int abs_bwd_mbw(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
+                float* grad_k, float* grad_v, int P, int D, int N, int M, int C, const Presorted* pre, void* ws,
+                size_t ws_bytes_given, hipStream_t st) {
+    auto b1 = [&](int pc) { return mbw_ws_bytes(pc, D, N, M, C); };
+    const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, N), b1);
+    if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;
+    auto view = [&](int p0, int np, void* buf) {
+        MbwWs w = mbw_carve(buf, np, D, N, M, C);
+        if (pre) {
+            const Presorted ps = offset(*pre, (size_t)p0, D, N, M);
+            w.ks = ps.ks; w.kp = ps.kp; w.qs = ps.qs; w.qp = ps.qp;
+        }
+        return w;
+    };
+    auto prep = [&](int p0, int np, void* buf, hipStream_t s) {
+        MbwWs w = view(p0, np, buf);
+        const size_t p = (size_t)p0;
+        if (!pre) {
+            SortedWs sw{};
+            sw.ks = w.ks; sw.kp = w.kp; sw.qs = w.qs; sw.qp = w.qp; sw.sort_scratch = w.sort_scratch;
+            if (int e = sort_both(q + p * D * M, k + p * D * N, sw, np * D, N, M, s)) return e;
+        }
+        const int e = merge_sums_launch(w.qs, w.qp, w.ks, w.kp, v + p * N * C, g_w + p * M * C,
+                                        g_u ? g_u + p * M : nullptr, w.mv, w.mt, w.sa_q, w.sb_q, w.sa_k, w.sa_e,
+                                        np * D, D, N, M, C, w.G, s);
+        return hip_status(e, "merge of q and k and its range sums");
+    };
+    auto early = [&](int p0, int np, void* buf, hipStream_t s) {
+        MbwWs w = view(p0, np, buf);
+        const int S = np * D;
+        if (int e = abs_scan_rows(w.sa_q, w.sb_q, w.ta_q, w.tb_q, w.aggs, S, C, w.G, s))
+            return hip_status(e, "merged scan (queries)");
+        return hip_status(linked_scan_pair(w.sa_k, w.sa_e, w.ta_k, w.ta_e, w.aggs, S, C, w.G, s),
+                          "merged scans (keys, ties)");
+    };
+    auto main = [&](int p0, int np, void* buf, hipStream_t s) {
+        MbwWs w = view(p0, np, buf);
+        const size_t p = (size_t)p0;
+        return hip_status(mbw_walk_launch(w.mv, w.mt, v + p * N * C, g_w + p * M * C, g_u ? g_u + p * M : nullptr,
+                                          w.ta_q, w.tb_q, w.ta_k, w.ta_e, w.slab, grad_q + p * D * M,
+                                          grad_k + p * D * N, np * D, D, N, M, C, w.G, s), "merged walk");
+    };
+    auto back = [&](int p0, int np, void* buf, hipStream_t s) {
+        MbwWs w = view(p0, np, buf);
+        const int e = reduce_slabs(w.slab, nullptr, nullptr, nullptr, grad_v + (size_t)p0 * N * C, nullptr, np, D, N,
+                                   C, s);
+        return hip_status(e, "grad_v reduce");
+    };
+    return run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back, early);
+}
+
 int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_w, const float* g_u, float* grad_q,
                  float* grad_k, float* grad_v, int P, int D, int N, int M, int C, const Presorted* pre, void* ws,
                  size_t ws_bytes_given, void* stream) {
@@ -744,6 +863,8 @@ int abs_bwd_impl(const float* q, const float* k, const float* v, const float* g_
     hipStream_t st = (hipStream_t)stream;
     if (dense_sign(P, N, M))     // the walks' convention: a tie counts -1 in both gradients
         return dense_bwd(-1.f, q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, st);
+    if (mbw_applies(C))
+        return abs_bwd_mbw(q, k, v, g_w, g_u, grad_q, grad_k, grad_v, P, D, N, M, C, pre, ws, ws_bytes_given, st);
     auto b1 = [&](int pc) { return ws_bytes(abs_bwd_spec(pc, D, N, M, C)); };
     const Plan pl = plan_chunks(P, ws_bytes_given, pipelined(P, D, N), b1);
     if (int e = check_ws(ws, ws_bytes_given, plan_bytes(pl, b1))) return e;

@@ -188,6 +188,26 @@ int group_queries(const float* ks, const float* q, float* qs, uint32_t* qp, int*
 bool group_fits(int Ns, int Mq, int C);
 int range_count(int Ns, int C);          // key ranges per segment
 
+// The range scans of the walks over caller-given summary rows (C <= 64; aggs: scan_agg_bytes for G > 256 ranges)
+int abs_scan_rows(const float* sa, const float* sb, float* ta, float* tb, float* aggs, int S, int C, int G,
+                  hipStream_t st);
+// two independent linked sums X <- a_g + link_g X (link in slot C + 1) over range rows, totals in row G
+int linked_scan_pair(const float* sa, const float* sb, float* ta, float* tb, float* aggs, int S, int C, int G,
+                     hipStream_t st);
+size_t scan_agg_bytes(int S, int Ns, int C);
+
+// ---- mbw.hip: the abs backward as one walk over the merged keys and queries (C <= 64, C % 4 == 0)
+// merged values mv and tags mt (index, | 0x80000000 for a query; queries first among equal values) of the sorted
+// queries (qs, qp) and keys (ks, kp) of S segments (D per p), and the range summaries of the merged sequence (G =
+// ranges of 64 elements) for the scans: sa_q, sb_q (abs scan), sa_k, sa_e (linked sums)
+int merge_sums_launch(const float* qs, const uint32_t* qp, const float* ks, const uint32_t* kp, const float* v,
+                      const float* gw, const float* gu, float* mv, uint32_t* mt, float* sa_q, float* sb_q,
+                      float* sa_k, float* sa_e, int S, int D, int N, int M, int C, int G, hipStream_t st);
+// the walk: grad_q, grad_k, and the grad_v rows into the slab (one row per (p, d, key))
+int mbw_walk_launch(const float* mv, const uint32_t* mt, const float* v, const float* gw, const float* gu,
+                    const float* ta_q, const float* tb_q, const float* ta_k, const float* ta_e, float* slab,
+                    float* grad_q, float* grad_k, int S, int D, int N, int M, int C, int G, hipStream_t st);
+
 // Dense evaluation for short segments (direct.hip): kind 0 abs, 1 Laplace; out_u may be null
 int direct_fwd(int kind, const float* q, const float* k, const float* v, float* out_w, float* out_u,
                int P, int D, int N, int M, int C, hipStream_t st);

@@ -304,7 +304,9 @@ __device__ __forceinline__ float* agg_slot(float* rec, int i, int part) {
 // Laplace: entry L state of every range (relative to the last key before the range) and exit R state (relative to
 // the first key after it). Forward: L <- a_g + e^{-(klast_g - klast_{g-1})} L; backward: R <- b_g +
 // e^{-(kfirst_{g+1} - kfirst_g)} R. A piece composes to  out = local + (product of its decays) in.
-template <int NV, int RK, int PHASE>
+// FF: both arrays run the forward recurrence (two independent linked sums, X <- a_g + link_g X, link in the rows' last
+// slot), and row G of both outputs takes the segment's final state.
+template <int NV, int RK, int PHASE, bool FF = false>
 __global__ __launch_bounds__(SCAN_W * WAVE)
 void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, float* __restrict__ ta,
                     float* __restrict__ tb, float* __restrict__ aggs, const int S, const int C, const int G)
@@ -343,11 +345,13 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
         }
         return prod;
     };
-    // backward piece walk from state cur; writes exit states when OUT; returns the product of the piece's decays
+    // backward (FF: forward) piece walk from state cur; writes exit (entry) states when OUT; returns the product of
+    // the piece's decays
     auto bwd = [&](float (&cur)[NV + 1], const bool out) {
         float prod = 1.f;
 #pragma unroll
-        for (int i = SCAN_BLOCK / SCAN_W - 1; i >= 0; --i) {
+        for (int ii = 0; ii < SCAN_BLOCK / SCAN_W; ++ii) {
+            const int i = FF ? ii : SCAN_BLOCK / SCAN_W - 1 - ii;
             const int g = glo + i;
             if (g >= ghi) continue;
             float b_[NV + 1], dec;
@@ -387,7 +391,7 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
 #pragma unroll
             for (int j = 0; j <= NV; ++j) c[j] = 0.f;
             for (int k = 0; k < SCAN_W; ++k) {
-                const int ww = part == 0 ? k : SCAN_W - 1 - k;    // forward: left to right; backward: right to left
+                const int ww = (part == 0 || FF) ? k : SCAN_W - 1 - k;   // forward: left to right; backward: right to left
                 const float dd = span[part][ww];
 #pragma unroll
                 for (int j = 0; j <= NV; ++j) c[j] = agg[part][ww][j][l] + dd * c[j];
@@ -422,7 +426,8 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
 #pragma unroll
             for (int j = 0; j <= NV; ++j) cf[j] = bs[j * WAVE + l] + d * cf[j];
         }
-        for (int bb = nb - 1; bb > blk; --bb) {
+        for (int k = 0; k < (FF ? blk : nb - 1 - blk); ++k) {
+            const int bb = FF ? k : nb - 1 - k;            // forward: the workgroups before; backward: those after
             const float* bs = agg_slot<NV>(seg_aggs + (size_t)bb * scan_rec_floats<NV>(), SCAN_W, 1);
             const float d = bs[(NV + 1) * WAVE + l];
 #pragma unroll
@@ -434,13 +439,20 @@ void lap_range_scan(const float* __restrict__ sa, const float* __restrict__ sb, 
 #pragma unroll
         for (int j = 0; j <= NV; ++j) cf[j] = agg[0][ww][j][l] + d * cf[j];
     }
-    for (int ww = SCAN_W - 1; ww > w; --ww) {
+    for (int k = 0; k < (FF ? w : SCAN_W - 1 - w); ++k) {
+        const int ww = FF ? k : SCAN_W - 1 - k;
         const float d = span[1][ww];
 #pragma unroll
         for (int j = 0; j <= NV; ++j) cb[j] = agg[1][ww][j][l] + d * cb[j];
     }
     fwd(cf, true);
     bwd(cb, true);
+    if constexpr (FF) {
+        if (ghi == G && glo < G) {                        // the wave whose piece ends the segment writes the totals
+            store_scan_row<NV>(A + (size_t)G * CS, C, cf);
+            store_scan_row<NV>(B + (size_t)G * CS, C, cb);
+        }
+    }
 }
 
 // Emission through LDS. Each wave owns a private slice of its workgroup's LDS: the state rows of one chunk of
@@ -1444,6 +1456,47 @@ static int abs_emit_t(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_
 int range_count(int Ns, int C) {
     const int RK = range_keys(C);
     return (Ns + RK - 1) / RK;
+}
+
+// The range scans over caller-given summary rows (S segments of G ranges, rows of C + 2 floats, one channel slot per
+// lane: C <= 64): the abs scan's entry states (PW with its link-weighted B) and the Laplace scan's (forward L with its
+// link factors, backward R), as abs_prepare and laplace_prepare run them after their sums.
+int abs_scan_rows(const float* sa, const float* sb, float* ta, float* tb, float* aggs, int S, int C, int G,
+                  hipStream_t st) {
+    if (C > WAVE) return (int)hipErrorInvalidValue;
+    StageTimer t("abs_range_scan", st);
+    const int nb = scan_blocks(G);
+    if (nb <= 1) {
+        hipLaunchKernelGGL((abs_range_scan<1, 64, 0>), dim3(S), dim3(SCAN_W * WAVE), 0, st, sa, sb, ta, tb, nullptr, S,
+                           G * 64, C, G);
+    } else {
+        if (aggs == nullptr) return (int)hipErrorInvalidValue;
+        hipLaunchKernelGGL((abs_range_scan<1, 64, 1>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st, sa, sb, ta, tb, aggs,
+                           S, G * 64, C, G);
+        hipLaunchKernelGGL((abs_range_scan<1, 64, 2>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st, sa, sb, ta, tb, aggs,
+                           S, G * 64, C, G);
+    }
+    return (int)hipGetLastError();
+}
+
+// two independent linked sums over range rows (X <- a_g + link_g X), each row's link in its slot C + 1: the entry
+// states of ranges 0 .. G - 1 and the final state in row G
+int linked_scan_pair(const float* sa, const float* sb, float* ta, float* tb, float* aggs, int S, int C, int G,
+                     hipStream_t st) {
+    if (C > WAVE) return (int)hipErrorInvalidValue;
+    StageTimer t("linked_scan_pair", st);
+    const int nb = scan_blocks(G);
+    if (nb <= 1) {
+        hipLaunchKernelGGL((lap_range_scan<1, 64, 0, true>), dim3(S), dim3(SCAN_W * WAVE), 0, st, sa, sb, ta, tb,
+                           nullptr, S, C, G);
+    } else {
+        if (aggs == nullptr) return (int)hipErrorInvalidValue;
+        hipLaunchKernelGGL((lap_range_scan<1, 64, 1, true>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st, sa, sb, ta, tb,
+                           aggs, S, C, G);
+        hipLaunchKernelGGL((lap_range_scan<1, 64, 2, true>), dim3(S * nb), dim3(SCAN_W * WAVE), 0, st, sa, sb, ta, tb,
+                           aggs, S, C, G);
+    }
+    return (int)hipGetLastError();
 }
 
 int abs_prepare(const AbsWalkArgs& a, int mode, RangeArrays ra, hipStream_t st) {
