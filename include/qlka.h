@@ -115,7 +115,8 @@ int qlka_abs_bwd(const float* q, const float* k, const float* v, const float* g_
  * sets *kept = 1 when it filled the four buffers (0: left untouched, the backward would not use them); after
  * *kept != 0, qlka_abs_bwd_sorted with the same q, k, v computes what qlka_abs_bwd computes without sorting. Same
  * workspace sizes as qlka_abs_fwd / qlka_abs_bwd.
- * states (optional, may be NULL; qlka_abs_keep_state_bytes() bytes, 0 when the backward does not walk): the forward
+ * states (optional, may be NULL; qlka_abs_keep_state_bytes() bytes, 0 when the backward would read none: it takes the
+ * dense kernels, or, at C <= 64 with C % 4 == 0, walks once over the merged sorted keys and queries): the forward
  * also leaves there the range states and query bounds of its walk over the sorted keys, which the backward's grad_q
  * walk would compute again (the same range sums, scan and bounds); it sets *kept = 3 when it wrote them (its own walk
  * ran; a forward on the dense kernels keeps only the sorts). Passing them to qlka_abs_bwd_sorted after *kept = 3

@@ -676,8 +676,13 @@ int qlka_abs_fwd_keep(const float* q, const float* k, const float* v, float* out
     return abs_fwd_impl(q, k, v, out_w, out_u, P, D, N, M, C, path, &keep, kept, ws, ws_bytes_given, stream);
 }
 
+// the widths at which the backward walks once over the merged keys and queries (mbw.hip), which reads no range states
+// of the forward's walk
+static bool mbw_applies(int C) { return C <= 64 && C % 4 == 0; }
+
 size_t qlka_abs_keep_state_bytes(int P, int D, int N, int M, int C) {
     if (P <= 0 || D <= 0 || N <= 0 || M <= 0 || C <= 0 || C > 128 || N > 131072 || dense_sign(P, N, M)) return 0;
+    if (mbw_applies(C)) return 0;
     return kept_state_bytes(P, D, N, C);
 }
 
@@ -729,7 +734,6 @@ static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
 // and one channel slot per lane covers a row. Its workspace per chunk: the backward's own sorts (when the forward kept
 // none), the merged values and tags, the entry states of its scans and their aggregates, and the slab, which also
 // holds the sort scratch and the range summaries (both dead before the walk writes it).
-static bool mbw_applies(int C) { return C <= 64 && C % 4 == 0; }
 
 struct MbwWs {
     float* ks; uint32_t* kp; float* qs; uint32_t* qp; void* sort_scratch;

@@ -178,11 +178,13 @@ def test_keep_sorts_entries_validate(lib):
     assert lib.qlka_abs_bwd_walks(12, 16384, 16384) == 1
     assert lib.qlka_abs_bwd_walks(512, 65, 65) == 0
     # the optional range states: ta and tb ([P*D][G+1][C+2] floats) and qb ([P*D][G] ints), 256-byte aligned each;
-    # none where the backward takes the dense kernels
+    # none where the backward takes the dense kernels or the merged walk (C <= 64, C % 4 == 0), which reads none
     def al(x):
         return (x + 255) // 256 * 256
-    P, D, N, C, G = 12, 64, 16384, 64, 16384 // 64
+    P, D, N, C, G = 12, 64, 16384, 62, 16384 // 64
     assert lib.qlka_abs_keep_state_bytes(P, D, N, N, C) == 2 * al(P * D * (G + 1) * (C + 2) * 4) + al(P * D * G * 4)
+    assert lib.qlka_abs_keep_state_bytes(P, D, N, N, 64) == 0
+    assert lib.qlka_abs_keep_state_bytes(P, D, N, N, 4) == 0
     assert lib.qlka_abs_keep_state_bytes(512, 32, 65, 65, 32) == 0
     # a handful of keys on either side: the dense route (the walk's segment totals would cost accuracy), also with the
     # cutoff at 0

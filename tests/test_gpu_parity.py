@@ -361,13 +361,14 @@ def test_autograd_keeps_dense_matrix(dev, shape, full):
     _assert_rel(got[2], wv, nv, "kept-A grad_v")
 
 
-@pytest.mark.parametrize("shape", [(2, 3, 1500, 1300, 16),      # one chunk
-                                   (6, 64, 16384, 16384, 32),   # pipelined chunks of 2 p
+@pytest.mark.parametrize("shape", [(2, 3, 1500, 1300, 18),      # one chunk
+                                   (6, 64, 16384, 16384, 30),   # pipelined chunks of 2 p
                                    (2, 8, 40000, 30000, 65)])   # two-launch scans, two channel slots per lane
 def test_kept_range_states_match_recomputed(dev, shape):
-    # A walking forward that keeps its sorts also leaves its range states and query bounds (a fifth tensor): the
-    # backward over them (its grad_q walk skips its range passes) must equal the backward over the sorts alone, which
-    # recomputes them, bit for bit, with and without g_u; the gradients also against the oracle on a subsample.
+    # A walking forward that keeps its sorts also leaves its range states and query bounds (a fifth tensor) at the
+    # widths whose backward walks twice (C > 64 or C % 4 != 0): the backward over them (its grad_q walk skips its range
+    # passes) must equal the backward over the sorts alone, which recomputes them, bit for bit, with and without g_u;
+    # the gradients also against the oracle on a subsample.
     from oracle import inputs
     from weighted_abs_sum import _ext
     P, D, N, M, C = shape
@@ -392,6 +393,32 @@ def test_kept_range_states_match_recomputed(dev, shape):
     _assert_rel(sub(_np(gq), bq, 1), wq, nq, "kept-states grad_q")
     _assert_rel(sub(_np(gk), bk, 1), wk, nk, "kept-states grad_k")
     _assert_rel(sub(_np(gv), bk, 0), wv, nv, "kept-states grad_v")
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 1500, 1300, 16),      # one chunk
+                                   (6, 64, 16384, 16384, 32)])  # pipelined chunks of 2 p
+def test_merged_backward_over_kept_sorts(dev, shape):
+    # At C <= 64 with C % 4 == 0 the backward walks once over the merged sorted keys and queries and reads no range
+    # states: the forward keeps the four sorts only, and the backward over them equals, bit for bit, the backward that
+    # sorts again, with and without g_u.
+    from weighted_abs_sum import _ext
+    P, D, N, M, C = shape
+    print(f"merged backward over kept sorts {shape}", flush=True)
+    q, k, v = _data(P, D, N, M, C, seed=sum(shape) % 991, kind="ties")
+    rng = np.random.default_rng(23)
+    g_w = _t(rng.standard_normal((P, M, C)).astype(np.float32), dev)
+    g_u = _t(rng.standard_normal((P, M)).astype(np.float32), dev)
+    tq, tk, tv = _t(q, dev), _t(k, dev), _t(v, dev)
+    _, _, srt = _ext.weighted_abs_sum_forward_keep(tq, tk, tv, -1, True)
+    assert len(srt) == 4
+    kept = _ext.weighted_abs_sum_backward_sorted(tq, tk, tv, g_w, g_u, srt)
+    again = _ext.weighted_abs_sum_full_backward(tq, tk, tv, g_w, g_u)
+    for name, a, b in zip(("grad_q", "grad_k", "grad_v"), kept, again):
+        assert torch.equal(a, b), f"{name}: over the kept sorts vs sorting again"
+    kept = _ext.weighted_abs_sum_backward_sorted(tq, tk, tv, g_w, None, srt)
+    again = _ext.weighted_abs_sum_backward(tq, tk, tv, g_w)
+    for name, a, b in zip(("grad_q", "grad_k", "grad_v"), kept, again):
+        assert torch.equal(a, b), f"{name} (no g_u): over the kept sorts vs sorting again"
 
 
 def test_full_backward_only_u(dev):
