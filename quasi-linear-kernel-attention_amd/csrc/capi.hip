@@ -585,6 +585,8 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
                                  "bucket's shared memory to fit this device");
     hipStream_t st = (hipStream_t)stream;
     const bool keep_sorts = keep && !dense_sign(P, N, M);   // the backward will walk: hand it the sorts
+    // the range states only where qlka_abs_keep_state_bytes sizes a buffer for them (a backward that reads them)
+    const bool keep_states = keep_sorts && keep->states && qlka_abs_keep_state_bytes(P, D, N, M, C) != 0;
     if (dense_abs_fwd(N, M)) {
         if (keep_sorts) {
             auto db = [&](int pc) { return abs_dense_ws(P, pc, D, N, M, C); };
@@ -612,7 +614,7 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
         if (keep_sorts) {
             const Presorted ks = offset(*keep, (size_t)p0, D, N, M);
             w.ks = ks.ks; w.kp = ks.kp; w.qs = ks.qs; w.qp = ks.qp;
-            if (keep->states) kept_states(keep->states, P, D, N, C, (size_t)p0, w.ra);   // the scan writes them there
+            if (keep_states) kept_states(keep->states, P, D, N, C, (size_t)p0, w.ra);   // the scan writes them there
         }
         a = AbsWalkArgs{};
         a.ks = w.ks; a.kp = w.kp; a.Ns = N; a.w = v + (size_t)p0 * N * C; a.u = nullptr;
@@ -656,7 +658,7 @@ int abs_fwd_impl(const float* q, const float* k, const float* v, float* out_w, f
                                        out_u ? out_u + p * M : nullptr, np, D, M, C, s), "abs reduce");
     };
     if (int e = run_pipeline(P, pl, ws, b1(pl.pc), st, prep, main, back, early)) return e;
-    if (keep_sorts) *kept = keep->states ? 3 : 1;
+    if (keep_sorts) *kept = keep_states ? 3 : 1;
     return QLKA_OK;
 }
 }  // namespace

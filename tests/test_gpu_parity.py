@@ -421,6 +421,37 @@ def test_merged_backward_over_kept_sorts(dev, shape):
         assert torch.equal(a, b), f"{name} (no g_u): over the kept sorts vs sorting again"
 
 
+def test_fwd_keep_leaves_unsized_states_untouched(dev):
+    # Through the C ABI: where qlka_abs_keep_state_bytes is 0 (the merged backward, C <= 64, C % 4 == 0) the forward
+    # keeps the sorts only (*kept = 1) even when handed a states pointer, and writes nothing through it; at a width whose
+    # backward walks twice it fills a buffer of the stated size (*kept = 3).
+    import ctypes
+    from qlka import _lib
+    lib = _lib.load()
+    for C, want in ((64, 1), (62, 3)):
+        P, D, N, M = 2, 3, 3000, 2500
+        print(f"fwd_keep states C={C}", flush=True)
+        q, k, v = (_t(a, dev) for a in _data(P, D, N, M, C, seed=C, kind="ties"))
+        out_w = torch.empty((P, M, C), device=dev)
+        out_u = torch.empty((P, M), device=dev)
+        ks, qs = torch.empty((P, D, N), device=dev), torch.empty((P, D, M), device=dev)
+        kp = torch.empty((P, D, N), dtype=torch.int32, device=dev)
+        qp = torch.empty((P, D, M), dtype=torch.int32, device=dev)
+        nbytes = lib.qlka_abs_keep_state_bytes(P, D, N, M, C)
+        assert (nbytes == 0) == (want == 1)
+        states = torch.full((max(nbytes, 1 << 20) // 4,), 12345.0, device=dev)   # a sentinel where nothing is sized
+        ws = torch.empty((lib.qlka_abs_fwd_ws_bytes(P, D, N, M, C),), dtype=torch.uint8, device=dev)
+        kept = ctypes.c_int(-1)
+        _lib.check(lib.qlka_abs_fwd_keep(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(out_w), _lib.ptr(out_u),
+                                         P, D, N, M, C, -1, _lib.ptr(ks), _lib.ptr(kp), _lib.ptr(qs), _lib.ptr(qp),
+                                         _lib.ptr(states), ctypes.byref(kept), _lib.ptr(ws), ws.numel(),
+                                         _lib.stream_of(dev)))
+        torch.cuda.synchronize()
+        assert kept.value == want
+        if want == 1:
+            assert bool((states == 12345.0).all()), "the forward wrote through an unsized states pointer"
+
+
 def test_full_backward_only_u(dev):
     # out_w unused: g_w is None inside the autograd Function and becomes zeros (ops.py:99-101)
     from weighted_abs_sum import weighted_abs_sum_full
