@@ -370,10 +370,12 @@ def main():
                     help="only time libqlka's segmented sort against torch.sort(stable=True) (rocPRIM's segmented "
                          "radix sort) on a configs[4]-sized chunk and on headline-length segments, check that the two "
                          "permutations agree, and print one JSON line")
-    ap.add_argument("--op", choices=("laplace", "abs", "add_laplace", "add_riesz", "add_bump"), default=None,
+    ap.add_argument("--op", choices=("laplace", "abs", "abs_fwd_bwd", "add_laplace", "add_riesz", "add_bump"),
+                    default=None,
                     help="only run --warmup + --steps calls of this one headline op or fused attention layer (on the "
-                         "headline q, k, v) and print the call count (for per-call rocprofv3 runs: traffic per call = "
-                         "the sum over its dispatches / calls)")
+                         "headline q, k, v; abs_fwd_bwd: weighted_abs_sum_full forward and backward through autograd "
+                         "against fixed random output gradients) and print the call count (for per-call rocprofv3 "
+                         "runs: traffic per call = the sum over its dispatches / calls)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy 3 times (reference kernel of known traffic for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -422,6 +424,15 @@ def main():
             fn = lambda: weighted_laplace_sum(q, k, v)  # noqa: E731
         elif args.op == "abs":
             fn = lambda: weighted_abs_sum_full(q, k, v, backend="cuda")  # noqa: E731
+        elif args.op == "abs_fwd_bwd":
+            gen = torch.Generator(device=dev).manual_seed(1)
+            g_w = torch.randn(q.shape[0], q.shape[2], v.shape[2], generator=gen, device=dev)
+            g_u = torch.randn(q.shape[0], q.shape[2], generator=gen, device=dev)
+
+            def fn():
+                tq, tk, tv = (t.detach().requires_grad_(True) for t in (q, k, v))
+                w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+                torch.autograd.backward([w, u], [g_w, g_u])
         else:
             from qlka import layers
             fn = lambda: layers.layer_forward(args.op, q, k, v)  # noqa: E731
