@@ -240,6 +240,10 @@ int merge_sums_launch(const float* qs, const uint32_t* qp, const float* ks, cons
 // run of equal values began) and its grad_v row (a 4-byte store per lane, non-temporal) and adds its row to PW. The
 // dots' lane products go to wave-private LDS, 16 elements at a time, and are summed there (4 lanes per element, 16
 // channels each, then two lane shuffles) with the scalar g_u terms, computed per element beforehand.
+// The walk has no branches: every element's row address and slab row offset are computed lane-parallel beforehand and
+// read lane by lane, the query/key choice is a select, and a query's (or a padding element's) slab store goes to an
+// out-of-range offset, which drops it. Padding elements past a short last range have zero rows, the last value, no
+// new run and no store, so they leave every state as it was.
 __global__ __launch_bounds__(MB_WPB * WAVE)
 void mbw_walk(const float* __restrict__ mv, const uint32_t* __restrict__ mt, const float* __restrict__ v,
               const float* __restrict__ gw, const float* __restrict__ gu, const float* __restrict__ ta_q,
@@ -266,17 +270,17 @@ void mbw_walk(const float* __restrict__ mv, const uint32_t* __restrict__ mt, con
     const bool tie_into = g > 0 && mseg[base] == vbefore;
     const float vmax = mseg[L - 1];
     const float u = (isq && gu) ? gu[(size_t)p * M + idx] : 0.f;
-    const uint64_t qmask = __ballot(isq);
+    const uint64_t qmask = __ballot(isq), kmask = __ballot(isk);
 
-    const rsrc_t vr = make_rsrc(v + (size_t)p * N * C, (uint32_t)((size_t)N * C * 4));
-    const rsrc_t gr = make_rsrc(gw + (size_t)p * M * C, (uint32_t)((size_t)M * C * 4));
-    const int cl = min(l, C - 1) * 4;
+    // the element's own row: g_w for a query, v for a key (lanes past the range repeat its last element)
+    const float* row_l = (tag & QTAG) ? gw + ((size_t)p * M + idx) * C : v + ((size_t)p * N + idx) * C;
+    const uint32_t ra_lo = (uint32_t)(uint64_t)row_l, ra_hi = (uint32_t)((uint64_t)row_l >> 32);
+    const int cl = min(l, C - 1);
     float x[MB_RK];
 #pragma unroll
     for (int t = 0; t < MB_RK; ++t) {
-        const bool q = (qmask >> t) & 1;
-        const int off = (int)(bcast(idx, t) * (uint32_t)C * 4u);
-        x[t] = buf_load(q ? gr : vr, cl, t < nk ? off : MB_OOB);
+        const uint64_t rt = (uint64_t)bcast(ra_lo, t) | ((uint64_t)bcast(ra_hi, t) << 32);
+        x[t] = reinterpret_cast<const __attribute__((address_space(1))) float*>(rt)[cl];
     }
 
     // entry states (lane = channel; slot C: the scalar channel) and the segment totals (row G)
@@ -308,29 +312,28 @@ void mbw_walk(const float* __restrict__ mv, const uint32_t* __restrict__ mt, con
     const float sterm = isq ? u * (2.f * nkb - (float)N) : 2.f * pub - Ut;
 
     const int SGr = slab_group(D);
-    const rsrc_t sr_ = make_rsrc(slab + slab_seg_base(p, d, D, N, CR), slab_seg_bytes(d, D, N, CR));
+    // the segment's slab rows (uniform; read through readfirstlane so the descriptor stays in SGPRs)
+    const uint64_t sbu = uniform_u64((uint64_t)(slab + slab_seg_base(p, d, D, N, CR)));
+    const rsrc_t sr_ = make_rsrc(reinterpret_cast<const void*>(sbu), uniform_u32(slab_seg_bytes(d, D, N, CR)));
+    const int soff = isk ? slab_row_off((int)idx, SGr, CR) : 0;     // element t's slab row, read by lane t
+    const int vo = ch ? l * 4 : MB_OOB;
     float* gq = grad_q + (size_t)s * M;
     float* gk = grad_k + (size_t)s * N;
     float PGB = PG - (tie_into ? E : 0.f);
     float vprev = vbefore;
 #pragma unroll
     for (int t = 0; t < MB_RK; ++t) {
-        if (t < nk) {
-            const float vt = bcast(val, t);
-            if ((runmask >> t) & 1) PGB = PG;
-            B += (vt - vprev) * PG;
-            const bool q = (qmask >> t) & 1;
-            dot[t & 15][l] = x[t] * (q ? 2.f * PW - Wt : 2.f * PGB - Gt);
-            if (q) {
-                PG += x[t];
-            } else {
-                const float row = 2.f * B - Bt - (vt - vmax) * Gt;
-                const int n = (int)bcast(idx, t);
-                buf_store_stream(row, sr_, ch ? l * 4 : MB_OOB, slab_row_off(n, SGr, CR));
-                PW += x[t];
-            }
-            vprev = vt;
-        }
+        const float vt = bcast(val, t);
+        const bool q = (qmask >> t) & 1;
+        PGB = ((runmask >> t) & 1) ? PG : PGB;
+        B += (vt - vprev) * PG;
+        dot[t & 15][l] = x[t] * (q ? 2.f * PW - Wt : 2.f * PGB - Gt);
+        const float pg1 = PG + x[t], pw1 = PW + x[t];
+        PG = q ? pg1 : PG;
+        PW = q ? PW : pw1;
+        const float row = 2.f * B - Bt - (vt - vmax) * Gt;
+        buf_store_stream(row, sr_, ((kmask >> t) & 1) ? vo : MB_OOB, bcast(soff, t));
+        vprev = vt;
         if ((t & 15) == 15) {
             // the 16 elements t - 15 .. t: lane 4 e + k sums channels 16 k .. 16 k + 15 of element e
             const int c0 = t - 15, e = l >> 2, k4 = l & 3;

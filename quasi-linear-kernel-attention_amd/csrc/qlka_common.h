@@ -50,6 +50,14 @@ __device__ __forceinline__ uint32_t bcast(uint32_t x, int src) {
     return (uint32_t)__builtin_amdgcn_readlane((int)x, src);
 }
 
+// A value known to be wave-uniform, read from the first active lane so the compiler keeps it in SGPRs. The builtin
+// returns a signed int: each 32-bit half is converted back to unsigned before it is widened, else a low word with bit
+// 31 set would sign-extend over the high word of a 64-bit address.
+__device__ __forceinline__ uint32_t uniform_u32(uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); }
+__device__ __forceinline__ uint64_t uniform_u64(uint64_t x) {
+    return (uint64_t)uniform_u32((uint32_t)x) | ((uint64_t)uniform_u32((uint32_t)(x >> 32)) << 32);
+}
+
 // number of lanes below this one whose bit is set in the wave-uniform mask m (v_mbcnt)
 __device__ __forceinline__ int lanes_below(uint64_t m) {
     return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));

@@ -4,6 +4,8 @@ Bars: sort permutations and merge ranks bit-exact; every float output within REL
 normalised by the sum of |term|.
 """
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -421,11 +423,49 @@ def test_merged_backward_over_kept_sorts(dev, shape):
         assert torch.equal(a, b), f"{name} (no g_u): over the kept sorts vs sorting again"
 
 
+def test_backward_with_workspace_above_a_2gib_address_boundary(dev):
+    # The backward's kernels build buffer descriptors from 64-bit workspace addresses read through readfirstlane; a
+    # low address word with bit 31 set once sign-extended over the high word there. The workspace is placed so that
+    # the low 32 bits of every address in its first 2 GiB have bit 31 set, and the call through the C ABI must equal
+    # the call on a workspace from the allocator, bit for bit, for a merged-walk width and a two-walk width.
+    from qlka import _lib
+    lib = _lib.load()
+    for C in (64, 30):
+        P, D, N, M = 3, 4, 3000, 2600
+        print(f"backward, workspace above a 2 GiB boundary, C={C}", flush=True)
+        q, k, v = (_t(a, dev) for a in _data(P, D, N, M, C, seed=C + 5, kind="ties"))
+        rng = np.random.default_rng(C)
+        g_w = _t(rng.standard_normal((P, M, C)).astype(np.float32), dev)
+        g_u = _t(rng.standard_normal((P, M)).astype(np.float32), dev)
+        need = lib.qlka_abs_bwd_ws_bytes(P, D, N, M, C)
+        assert 0 < need < (1 << 30)
+
+        def run(ws_ptr):
+            gq, gk = torch.empty((P, D, M), device=dev), torch.empty((P, D, N), device=dev)
+            gv = torch.empty((P, N, C), device=dev)
+            _lib.check(lib.qlka_abs_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g_w), _lib.ptr(g_u),
+                                        _lib.ptr(gq), _lib.ptr(gk), _lib.ptr(gv), P, D, N, M, C, ws_ptr, need,
+                                        _lib.stream_of(dev)))
+            torch.cuda.synchronize()
+            return gq, gk, gv
+
+        plain = torch.empty((need,), dtype=torch.uint8, device=dev)
+        want = run(_lib.ptr(plain))
+        del plain
+        big = torch.empty(((4 << 30) + need,), dtype=torch.uint8, device=dev)
+        base = big.data_ptr()
+        off = (0x80000000 - (base & 0xFFFFFFFF)) % (1 << 32)     # base + off has low word 0x80000000
+        assert off + need <= big.numel() and ((base + off) & 0xFFFFFFFF) == 0x80000000
+        got = run(ctypes.c_void_p(base + off))
+        del big
+        for name, a, b in zip(("grad_q", "grad_k", "grad_v"), got, want):
+            assert torch.equal(a, b), f"{name} (C={C}): the workspace's address changed the result"
+
+
 def test_fwd_keep_leaves_unsized_states_untouched(dev):
     # Through the C ABI: where qlka_abs_keep_state_bytes is 0 (the merged backward, C <= 64, C % 4 == 0) the forward
     # keeps the sorts only (*kept = 1) even when handed a states pointer, and writes nothing through it; at a width whose
     # backward walks twice it fills a buffer of the stated size (*kept = 3).
-    import ctypes
     from qlka import _lib
     lib = _lib.load()
     for C, want in ((64, 1), (62, 3)):
