@@ -195,6 +195,41 @@ def test_forward_query_grouping_edges(dev, layout):
     _assert_rel(_np(u), ou, ou, f"abs out_u ({layout})")
 
 
+@pytest.mark.parametrize("layout", ["all_equal", "long_runs", "on_key_ranks"])
+def test_backward_tie_runs_across_tiles_and_scan_blocks(dev, layout):
+    # The backward's merged walk takes a key's query sums where its run of equal values began, carried across ranges,
+    # merge tiles (2048 merged elements) and scan workgroups (256 ranges) by the tie carry. N + M = 18000: 282 ranges,
+    # 9 tiles, two scan workgroups per segment. Layouts: every query and key one value (one run over the whole
+    # segment); runs of about 3000 equal values mixing queries and keys; queries equal to every 64th sorted key.
+    from oracle import inputs
+    from weighted_abs_sum import weighted_abs_sum_full
+    P, D, N, M, C = 2, 2, 9000, 9000, 16
+    print(f"backward tie runs ({layout})", flush=True)
+    q, k, v = _data(P, D, N, M, C, seed=41)
+    if layout == "all_equal":
+        q[:] = np.float32(0.5)
+        k[:] = np.float32(0.5)
+    elif layout == "long_runs":
+        q = np.floor(q * 2).astype(np.float32) / 2      # a handful of levels: runs of ~3000 values
+        k = np.floor(k * 2).astype(np.float32) / 2
+    else:
+        ks = np.sort(k, axis=2)
+        q = np.ascontiguousarray(ks[:, :, (np.arange(M) * 64) % N], dtype=np.float32)
+    rng = np.random.default_rng(43)
+    g_w = rng.standard_normal((P, M, C)).astype(np.float32)
+    g_u = rng.standard_normal((P, M)).astype(np.float32)
+    tq, tk, tv = (_t(a, dev).requires_grad_(True) for a in (q, k, v))
+    w, u = weighted_abs_sum_full(tq, tk, tv, backend="cuda")
+    torch.autograd.backward([w, u], [_t(g_w, dev), _t(g_u, dev)])
+    bq = inputs.query_subsample(P, M, per_p=6, seed=5)
+    bk = inputs.query_subsample(P, N, per_p=6, seed=6)
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward_sub(q, k, v, g_w, g_u, bq, bk)
+    sub = lambda a, idx, axis: np.stack([np.take(a[p], idx[p], axis=axis) for p in range(P)])  # noqa: E731
+    _assert_rel(sub(_np(tq.grad), bq, 1), wq, nq, f"grad_q ({layout})")
+    _assert_rel(sub(_np(tk.grad), bk, 1), wk, nk, f"grad_k ({layout})")
+    _assert_rel(sub(_np(tv.grad), bk, 0), wv, nv, f"grad_v ({layout})")
+
+
 def test_abs_translation_far_from_zero(dev):
     # keys and queries centred at 1000: the distance-relative walk must not cancel catastrophically
     from weighted_abs_sum import weighted_abs_sum_full
