@@ -735,7 +735,8 @@ static WsSpec abs_bwd_spec(int P, int D, int N, int M, int C) {
 // The backward as one walk over the merged keys and queries (mbw.hip) where its sums can load rows 16 bytes at a time
 // and one channel slot per lane covers a row. Its workspace per chunk: the backward's own sorts (when the forward kept
 // none), the merged values and tags, the entry states of its scans and their aggregates, and the slab, which also
-// holds the sort scratch and the range summaries (both dead before the walk writes it).
+// holds the backward's own sorts, the sort scratch and the range summaries (all dead before the walk writes it), so
+// that two copies of one configs[4] p (N = M = 131072) fit the default 5 GiB budget and the backward pipelines.
 
 struct MbwWs {
     float* ks; uint32_t* kp; float* qs; uint32_t* qp; void* sort_scratch;
@@ -751,14 +752,15 @@ static size_t mbw_part(int P, int D, int N, int M, int C, int i) {
     const size_t S = (size_t)P * D;
     const int L = N + M, G = (L + 63) / 64;
     switch (i) {
-        case 0: case 1: return align256(S * N * 4);
-        case 2: case 3: return align256(S * M * 4);
+        case 0: case 1: case 2: case 3: return 0;     // the backward's own sorts live in the slab region
         case 4: case 5: return align256(S * L * 4);
         case 6: return 4 * mbw_rows_bytes(S, G, C);
         case 7: return align256(scan_agg_bytes((int)S, L, C));
         case 8: {
             const size_t slab = align256(S * slab_rows(N) * (size_t)slab_stride(C) * 4);
-            return std::max({slab, 4 * mbw_rows_bytes(S, G, C), align256(sort_scratch_need(abs_bwd_spec(P, D, N, M, C)))});
+            const size_t sorted = 2 * align256(S * N * 4) + 2 * align256(S * M * 4);
+            return std::max(slab, sorted + std::max(4 * mbw_rows_bytes(S, G, C),
+                                                    align256(sort_scratch_need(abs_bwd_spec(P, D, N, M, C)))));
         }
     }
     return 0;
@@ -778,15 +780,20 @@ static MbwWs mbw_carve(void* ws, int P, int D, int N, int M, int C) {
     MbwWs w;
     w.G = (N + M + 63) / 64;
     const size_t rb = mbw_rows_bytes(S, w.G, C);
-    w.ks = (float*)part[0]; w.kp = (uint32_t*)part[1]; w.qs = (float*)part[2]; w.qp = (uint32_t*)part[3];
+    // the slab region: the backward's own sorts (read only by the merge), then the sort scratch, then (over the dead
+    // scratch) the range summaries; all of it dead before the walk writes the slab
+    const size_t kb = align256(S * (size_t)N * 4), qb = align256(S * (size_t)M * 4);
+    char* const sr = part[8];
+    w.ks = (float*)sr; w.kp = (uint32_t*)(sr + kb); w.qs = (float*)(sr + 2 * kb); w.qp = (uint32_t*)(sr + 2 * kb + qb);
+    char* const after = sr + 2 * kb + 2 * qb;
     w.mv = (float*)part[4]; w.mt = (uint32_t*)part[5];
     w.ta_q = (float*)part[6]; w.tb_q = (float*)(part[6] + rb); w.ta_k = (float*)(part[6] + 2 * rb);
     w.ta_e = (float*)(part[6] + 3 * rb);
     w.aggs = mbw_part(P, D, N, M, C, 7) ? (float*)part[7] : nullptr;
     w.slab = (float*)part[8];
-    w.sort_scratch = part[8];
-    w.sa_q = (float*)part[8]; w.sb_q = (float*)(part[8] + rb); w.sa_k = (float*)(part[8] + 2 * rb);
-    w.sa_e = (float*)(part[8] + 3 * rb);
+    w.sort_scratch = after;
+    w.sa_q = (float*)after; w.sb_q = (float*)(after + rb); w.sa_k = (float*)(after + 2 * rb);
+    w.sa_e = (float*)(after + 3 * rb);
     return w;
 }
 
