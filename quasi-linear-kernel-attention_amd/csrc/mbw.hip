@@ -31,7 +31,9 @@ namespace qlka {
 constexpr int MB_WPB = 4;                      // waves (ranges) per workgroup of the walk
 constexpr int MB_RK = 64;                      // elements per range
 constexpr uint32_t QTAG = 0x80000000u;         // tag bit of a query
-constexpr int MB_OOB = 0x7fff0000;             // a buffer offset past every row descriptor: loads read 0
+// a buffer offset past every descriptor of this file (rows of one p, a segment's slab rows: at most 67 MB at the widths
+// taken here): loads there read 0, stores are dropped
+constexpr int MB_OOB = 0x7fff0000;
 
 // ---------------------------------------------------------------------------------------------------- merge_sums
 constexpr int MKQ_T = 256, MKQ_ITEMS = 8, MKQ_TILE = MKQ_T * MKQ_ITEMS;
