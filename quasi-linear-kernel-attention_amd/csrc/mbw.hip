@@ -237,7 +237,7 @@ int merge_sums_launch(const float* qs, const uint32_t* qp, const float* ks, cons
 
 // ---------------------------------------------------------------------------------------------------- mbw_walk
 // One wave per 64-element range. The elements' rows (g_w for a query, v for a key) are gathered into registers
-// (lane = channel) and walked in order: at element t the B state moves its reference to the element's value, a query
+// (lane = channel), 32 at a time (62 VGPRs, 8 waves per SIMD; all 64 at once took 94-96 and 5), and walked in order: at element t the B state moves its reference to the element's value, a query
 // emits its dot with 2 PW - Wtot and adds its row to PG, a key emits its dot with 2 PG' - Gtot (PG' = PG where the key's
 // run of equal values began) and its grad_v row (a 4-byte store per lane, non-temporal) and adds its row to PW. The
 // dots' lane products go to wave-private LDS, 16 elements at a time, and are summed there (4 lanes per element, 16
@@ -278,12 +278,18 @@ void mbw_walk(const float* __restrict__ mv, const uint32_t* __restrict__ mt, con
     const float* row_l = (tag & QTAG) ? gw + ((size_t)p * M + idx) * C : v + ((size_t)p * N + idx) * C;
     const uint32_t ra_lo = (uint32_t)(uint64_t)row_l, ra_hi = (uint32_t)((uint64_t)row_l >> 32);
     const int cl = min(l, C - 1);
-    float x[MB_RK];
+    // the rows are gathered and walked in two halves of 32 elements, so that a wave holds 32 rows at a time
+    constexpr int HALF = MB_RK / 2;
+    auto gather = [&](float (&xs)[HALF], const int h) {
 #pragma unroll
-    for (int t = 0; t < MB_RK; ++t) {
-        const uint64_t rt = (uint64_t)bcast(ra_lo, t) | ((uint64_t)bcast(ra_hi, t) << 32);
-        x[t] = reinterpret_cast<const __attribute__((address_space(1))) float*>(rt)[cl];
-    }
+        for (int i = 0; i < HALF; ++i) {
+            const int t = h * HALF + i;
+            const uint64_t rt = (uint64_t)bcast(ra_lo, t) | ((uint64_t)bcast(ra_hi, t) << 32);
+            xs[i] = reinterpret_cast<const __attribute__((address_space(1))) float*>(rt)[cl];
+        }
+    };
+    float x0[HALF];
+    gather(x0, 0);
 
     // entry states (lane = channel; slot C: the scalar channel) and the segment totals (row G)
     const int CS = C + 2;
@@ -294,8 +300,6 @@ void mbw_walk(const float* __restrict__ mv, const uint32_t* __restrict__ mt, con
     const float PU = ta_q[r0 + C], cnt_in = ta_k[r0 + C], EU = ta_e[r0 + C];
     const float Gt = ch ? ta_q[rt + l] : 0.f, Bt = ch ? tb_q[rt + l] : 0.f, Wt = ch ? ta_k[rt + l] : 0.f;
     const float Ut = ta_q[rt + C];
-#pragma unroll
-    for (int t = 0; t < MB_RK; ++t) x[t] = (t < nk && ch) ? x[t] : 0.f;
 
     // per element (lane t): the start of a run of equal values, the keys below it, the g_u sum of the queries below
     // it, where its run began (-1: before the range), and its scalar term
@@ -323,38 +327,48 @@ void mbw_walk(const float* __restrict__ mv, const uint32_t* __restrict__ mt, con
     float* gk = grad_k + (size_t)s * N;
     float PGB = PG - (tie_into ? E : 0.f);
     float vprev = vbefore;
+    auto walk_half = [&](float (&xs)[HALF], const int h) {
 #pragma unroll
-    for (int t = 0; t < MB_RK; ++t) {
-        const float vt = bcast(val, t);
-        const bool q = (qmask >> t) & 1;
-        PGB = ((runmask >> t) & 1) ? PG : PGB;
-        B += (vt - vprev) * PG;
-        dot[t & 15][l] = x[t] * (q ? 2.f * PW - Wt : 2.f * PGB - Gt);
-        const float pg1 = PG + x[t], pw1 = PW + x[t];
-        PG = q ? pg1 : PG;
-        PW = q ? PW : pw1;
-        const float row = 2.f * B - Bt - (vt - vmax) * Gt;
-        buf_store_stream(row, sr_, ((kmask >> t) & 1) ? vo : MB_OOB, bcast(soff, t));
-        vprev = vt;
-        if ((t & 15) == 15) {
-            // the 16 elements t - 15 .. t: lane 4 e + k sums channels 16 k .. 16 k + 15 of element e
-            const int c0 = t - 15, e = l >> 2, k4 = l & 3;
-            const f4_t* rowp = reinterpret_cast<const f4_t*>(&dot[e][16 * k4]);
-            const f4_t a0 = rowp[0], a1 = rowp[1], a2 = rowp[2], a3 = rowp[3];
-            float sum = (a0[0] + a0[1] + a0[2] + a0[3]) + (a1[0] + a1[1] + a1[2] + a1[3]) +
-                        (a2[0] + a2[1] + a2[2] + a2[3]) + (a3[0] + a3[1] + a3[2] + a3[3]);
-            sum += __shfl_xor(sum, 1, WAVE);
-            sum += __shfl_xor(sum, 2, WAVE);
-            const int te = c0 + e;
-            const float st_e = __shfl(sterm, te, WAVE);
-            const uint32_t tg_e = __shfl(tag, te, WAVE);
-            if (k4 == 0 && te < nk) {
-                const uint32_t ie = tg_e & ~QTAG;
-                if (tg_e & QTAG) gq[ie] = sum + st_e;
-                else gk[ie] = sum + st_e;
+        for (int i = 0; i < HALF; ++i) xs[i] = (h * HALF + i < nk && ch) ? xs[i] : 0.f;
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) {
+            const int t = h * HALF + i;
+            const float xt = xs[i];
+            const float vt = bcast(val, t);
+            const bool q = (qmask >> t) & 1;
+            PGB = ((runmask >> t) & 1) ? PG : PGB;
+            B += (vt - vprev) * PG;
+            dot[t & 15][l] = xt * (q ? 2.f * PW - Wt : 2.f * PGB - Gt);
+            const float pg1 = PG + xt, pw1 = PW + xt;
+            PG = q ? pg1 : PG;
+            PW = q ? PW : pw1;
+            const float row = 2.f * B - Bt - (vt - vmax) * Gt;
+            buf_store_stream(row, sr_, ((kmask >> t) & 1) ? vo : MB_OOB, bcast(soff, t));
+            vprev = vt;
+            if ((t & 15) == 15) {
+                // the 16 elements t - 15 .. t: lane 4 e + k sums channels 16 k .. 16 k + 15 of element e
+                const int c0 = t - 15, e = l >> 2, k4 = l & 3;
+                const f4_t* rowp = reinterpret_cast<const f4_t*>(&dot[e][16 * k4]);
+                const f4_t a0 = rowp[0], a1 = rowp[1], a2 = rowp[2], a3 = rowp[3];
+                float sum = (a0[0] + a0[1] + a0[2] + a0[3]) + (a1[0] + a1[1] + a1[2] + a1[3]) +
+                            (a2[0] + a2[1] + a2[2] + a2[3]) + (a3[0] + a3[1] + a3[2] + a3[3]);
+                sum += __shfl_xor(sum, 1, WAVE);
+                sum += __shfl_xor(sum, 2, WAVE);
+                const int te = c0 + e;
+                const float st_e = __shfl(sterm, te, WAVE);
+                const uint32_t tg_e = __shfl(tag, te, WAVE);
+                if (k4 == 0 && te < nk) {
+                    const uint32_t ie = tg_e & ~QTAG;
+                    if (tg_e & QTAG) gq[ie] = sum + st_e;
+                    else gk[ie] = sum + st_e;
+                }
             }
         }
-    }
+    };
+    walk_half(x0, 0);
+    float x1[HALF];
+    gather(x1, 1);
+    walk_half(x1, 1);
 }
 
 int mbw_walk_launch(const float* mv, const uint32_t* mt, const float* v, const float* gw, const float* gu,
