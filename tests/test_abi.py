@@ -93,6 +93,21 @@ def test_workspace_budget_sizes_the_queries(lib):
         lib.qlka_set_workspace_budget(prev)
 
 
+def test_config4_backward_pipelines_under_the_default_budget(lib):
+    """At configs[4] (N = M = 131072, C = 64) one p's merged-backward workspace fits twice in the 5 GiB default budget
+    (its own sorts share the slab region), so the backward runs two copies of one-p chunks, each chunk's grad_v reduce
+    beside the next chunk's work; the forwards too."""
+    prev = lib.qlka_set_workspace_budget(5 << 30)
+    try:
+        dims = (12, 64, 131072, 131072, 64)
+        one = lib.qlka_abs_bwd_ws_bytes(1, *dims[1:])              # one p: not pipelined, one copy
+        assert lib.qlka_abs_bwd_ws_bytes(*dims) == 2 * one <= 5 << 30
+        for f in (lib.qlka_abs_fwd_ws_bytes, lib.qlka_laplace_fwd_ws_bytes):
+            assert f(*dims) == 2 * f(1, *dims[1:]) <= 5 << 30
+    finally:
+        lib.qlka_set_workspace_budget(prev)
+
+
 @pytest.mark.parametrize("dims,msg", [
     ((1, 1, 8, 8, 129), "C (v.size(2)) must be in [1, 128]"),
     ((1, 1, 8, 8, 0), "C (v.size(2)) must be in [1, 128]"),
