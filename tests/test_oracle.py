@@ -340,3 +340,90 @@ def test_grad_q_fp32_prefix_matches_fp64_backward(g_u):
     err = np.abs(got - want) / dn
     assert err.max() < 1e-5
     assert err.max() > 0                                  # an fp32 evaluation, not the fp64 one again
+
+
+def _merged_walk_backward(q, k, v, g_w, g_u, RK):
+    """The abs backward as the GPU's merged walk computes it (csrc/mbw.hip), restated in fp64 for small inputs: per
+    (p, d), the sorted queries and keys merged (queries first among equal values), ranges of RK elements, per-range
+    summaries, the three scans (abs scan with value-gap links for (PG, B), plain sums for (PW, key count), the tie
+    carry E as a linked sum with 0/1 links) and a walk of every range from its entry state."""
+    P, D, M = q.shape
+    N, C = k.shape[2], v.shape[2]
+    q, k, v, g_w = (np.asarray(a, np.float64) for a in (q, k, v, g_w))
+    g_u = np.zeros((P, M)) if g_u is None else np.asarray(g_u, np.float64)
+    gq, gk, gv = np.zeros((P, D, M)), np.zeros((P, D, N)), np.zeros((P, N, C))
+    for p in range(P):
+        for d in range(D):
+            vals = np.concatenate([q[p, d], k[p, d]])
+            isq = np.concatenate([np.ones(M, bool), np.zeros(N, bool)])
+            idx = np.concatenate([np.arange(M), np.arange(N)])
+            order = np.lexsort((idx, ~isq, vals))               # by value, queries first, then by index (stable)
+            vals, isq, idx = vals[order], isq[order], idx[order]
+            x = np.where(isq[:, None], g_w[p][np.where(isq, idx, 0)], v[p][np.where(isq, 0, idx)])
+            u = np.where(isq, g_u[p][np.where(isq, idx, 0)], 0.0)
+            L = N + M
+            G = (L + RK - 1) // RK
+            rng_ = [(g * RK, min(L, (g + 1) * RK)) for g in range(G)]
+            # entry states of every range (row G: the totals)
+            PG, B, PW, E = np.zeros((G + 1, C)), np.zeros((G + 1, C)), np.zeros((G + 1, C)), np.zeros((G + 1, C))
+            PU, CNT, EU = np.zeros(G + 1), np.zeros(G + 1), np.zeros(G + 1)
+            for g, (a, b) in enumerate(rng_):
+                vl, vf = vals[b - 1], vals[a]
+                gap = vl - vals[a - 1] if g > 0 else 0.0
+                qs = isq[a:b]
+                SG = x[a:b][qs].sum(0)
+                SB = ((vl - vals[a:b][qs])[:, None] * x[a:b][qs]).sum(0)
+                inlast = qs & (vals[a:b] == vl)
+                link = 1.0 if (g > 0 and vf == vals[a - 1] and vf == vl) else 0.0
+                B[g + 1] = SB + B[g] + gap * PG[g]
+                PG[g + 1] = PG[g] + SG
+                PU[g + 1] = PU[g] + u[a:b][qs].sum()
+                PW[g + 1] = PW[g] + x[a:b][~qs].sum(0)
+                CNT[g + 1] = CNT[g] + (~qs).sum()
+                E[g + 1] = x[a:b][inlast].sum(0) + link * E[g]
+                EU[g + 1] = u[a:b][inlast].sum() + link * EU[g]
+            Gt, Bt, Wt, Ut, vmax = PG[G], B[G], PW[G], PU[G], vals[L - 1]
+            for g, (a, b) in enumerate(rng_):
+                vbefore = vals[a - 1] if g > 0 else vals[a]
+                tie_into = g > 0 and vals[a] == vbefore
+                pg, bb, pw, pu, nk = PG[g].copy(), B[g].copy(), PW[g].copy(), PU[g], CNT[g]
+                pgb = pg - (E[g] if tie_into else 0.0)
+                pub = pu - (EU[g] if tie_into else 0.0)
+                vprev = vbefore
+                for t in range(a, b):
+                    vt = vals[t]
+                    if (t == a and not tie_into) or (t > a and vt != vals[t - 1]):
+                        pgb, pub = pg.copy(), pu
+                    bb = bb + (vt - vprev) * pg
+                    if isq[t]:
+                        gq[p, d, idx[t]] = x[t] @ (2 * pw - Wt) + u[t] * (2 * nk - N)
+                        pg = pg + x[t]
+                        pu = pu + u[t]
+                    else:
+                        gk[p, d, idx[t]] = x[t] @ (2 * pgb - Gt) + 2 * pub - Ut
+                        gv[p, idx[t]] += 2 * bb - Bt - (vt - vmax) * Gt
+                        pw = pw + x[t]
+                        nk += 1
+                    vprev = vt
+    return gq, gk, gv
+
+
+@pytest.mark.parametrize("ties", [False, True])
+@pytest.mark.parametrize("full", [False, True])
+def test_merged_walk_decomposition_matches_backward(ties, full):
+    # The merged walk's ranges, summaries, three scans and tie carry (csrc/mbw.hip) give the brute-force backward with
+    # s(0) = -1 in fp64, also when runs of equal values span many ranges (integer-valued inputs, 4-element ranges).
+    rng = np.random.default_rng(7 + 2 * ties + full)
+    P, D, N, M, C = 2, 2, 37, 29, 3
+    if ties:
+        q = rng.integers(-3, 4, (P, D, M)).astype(np.float64)
+        k = rng.integers(-3, 4, (P, D, N)).astype(np.float64)
+    else:
+        q, k = rng.standard_normal((P, D, M)), rng.standard_normal((P, D, N))
+    v, g_w = rng.standard_normal((P, N, C)), rng.standard_normal((P, M, C))
+    g_u = rng.standard_normal((P, M)) if full else None
+    got = _merged_walk_backward(q, k, v, g_w, g_u, RK=4)
+    (wq, wk, wv), (nq, nk, nv) = brute.abs_backward(q, k, v, g_w, g_u)
+    for name, a, b, n in zip(("grad_q", "grad_k", "grad_v"), got, (wq, wk, wv), (nq, nk, nv)):
+        err = brute.rel_err(a, b, n)
+        assert float(err.max()) < 1e-12, f"{name}: {float(err.max()):.3e}"
